@@ -1,0 +1,116 @@
+// extern "C" entry points: validate the descriptor on the host, then launch.
+// No allocation, no host<->device synchronisation.
+#include <stdint.h>
+
+#include "dft_device.h"
+
+namespace dft {
+int launch_tree_verify(const dft_verify_args* a, hipStream_t stream);
+int launch_block_inverse(float* x, int n_mats, int n, int64_t mat_stride, hipStream_t stream);
+int launch_tree_conv(const dft_conv_args* a, hipStream_t stream);
+int launch_tree_commit(const dft_commit_args* a, hipStream_t stream);
+int launch_tree_struct(const dft_tree_args* a, hipStream_t stream);
+}  // namespace dft
+
+namespace {
+
+bool float_tag(int32_t t) { return t == DFT_F32 || t == DFT_BF16 || t == DFT_F16; }
+bool index_tag(int32_t t) { return t == DFT_I32 || t == DFT_I64; }
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+}  // namespace
+
+extern "C" {
+
+int dft_abi_version(void) { return DFT_ABI_VERSION; }
+
+const char* dft_error_string(int status) {
+  switch (status) {
+    case DFT_OK: return "ok";
+    case DFT_ERR_INVALID: return "invalid argument (pointer, size, stride, dtype or alignment)";
+    case DFT_ERR_UNSUPPORTED: return "unsupported configuration";
+    case DFT_ERR_LAUNCH: return "HIP kernel launch failed";
+    default: return "unknown status";
+  }
+}
+
+int dft_tree_verify(const dft_verify_args* a, void* stream) {
+  if (!a) return DFT_ERR_INVALID;
+  if (a->batch < 0 || a->n_nodes < 0 || a->hk <= 0 || a->hv <= 0 || a->hv % a->hk != 0) return DFT_ERR_INVALID;
+  if (a->dk != 128 || a->dv != 128) return DFT_ERR_UNSUPPORTED;
+  if (a->n_nodes > 64) return DFT_ERR_UNSUPPORTED;
+  if (a->batch == 0 || a->n_nodes == 0) return DFT_OK;
+  if (!a->y || !a->a || !a->b || !a->state || !a->o) return DFT_ERR_INVALID;
+  if (!a->neg_exp_A && !a->A_log) return DFT_ERR_INVALID;
+  if (!a->dt_bias) return DFT_ERR_INVALID;
+  if ((a->anc_f32 == nullptr) == (a->anc_bits == nullptr)) return DFT_ERR_INVALID;
+  if (!float_tag(a->a_dtype) || !float_tag(a->b_dtype) || !float_tag(a->dt_bias_dtype) ||
+      (a->A_log && !float_tag(a->A_log_dtype)))
+    return DFT_ERR_INVALID;
+  if (a->o_dtype != DFT_F32 && a->o_dtype != DFT_BF16 && a->o_dtype != DFT_F16) return DFT_ERR_INVALID;
+  if (a->state_indices && !index_tag(a->state_indices_dtype)) return DFT_ERR_INVALID;
+  // q/k rows are read as 16-byte vectors
+  if (!aligned16(a->y) || a->y_row_stride % 8 != 0) return DFT_ERR_INVALID;
+  if ((int64_t)a->batch * a->hv > INT32_MAX) return DFT_ERR_UNSUPPORTED;
+  return dft::launch_tree_verify(a, static_cast<hipStream_t>(stream));
+}
+
+int dft_block_inverse(float* x, int32_t n_mats, int32_t n, int64_t mat_stride, void* stream) {
+  if (n_mats < 0 || n < 0 || n > 64) return DFT_ERR_INVALID;
+  if (n_mats == 0 || n == 0) return DFT_OK;
+  if (!x || mat_stride < (int64_t)n * n) return DFT_ERR_INVALID;
+  return dft::launch_block_inverse(x, n_mats, n, mat_stride, static_cast<hipStream_t>(stream));
+}
+
+int dft_tree_conv(const dft_conv_args* a, void* stream) {
+  if (!a) return DFT_ERR_INVALID;
+  if (a->batch < 0 || a->n_nodes < 0 || a->channels < 0) return DFT_ERR_INVALID;
+  if (a->width < 1 || a->width > 8) return DFT_ERR_UNSUPPORTED;
+  if (a->batch == 0 || a->n_nodes == 0 || a->channels == 0) return DFT_OK;
+  if (a->n_nodes > 65535 || a->batch > 65535) return DFT_ERR_UNSUPPORTED;
+  if (!a->x || !a->conv_state || !a->weight || !a->cidx || !a->y) return DFT_ERR_INVALID;
+  if (!float_tag(a->x_dtype) || !float_tag(a->cs_dtype) || !float_tag(a->w_dtype) || !float_tag(a->y_dtype))
+    return DFT_ERR_INVALID;
+  if (a->bias && !float_tag(a->bias_dtype)) return DFT_ERR_INVALID;
+  if (a->iw && !float_tag(a->iw_dtype)) return DFT_ERR_INVALID;
+  if (!index_tag(a->cidx_dtype)) return DFT_ERR_INVALID;
+  if (a->cs_indices && !index_tag(a->cs_indices_dtype)) return DFT_ERR_INVALID;
+  if (a->iw_indices && !index_tag(a->iw_indices_dtype)) return DFT_ERR_INVALID;
+  return dft::launch_tree_conv(a, static_cast<hipStream_t>(stream));
+}
+
+int dft_tree_commit(const dft_commit_args* a, void* stream) {
+  if (!a) return DFT_ERR_INVALID;
+  if (a->n_layers < 0 || a->batch < 0 || a->hv <= 0 || a->n_nodes < 0) return DFT_ERR_INVALID;
+  if (a->dk != 128 || a->dv != 128) return DFT_ERR_UNSUPPORTED;
+  if (a->n_nodes > 64 || a->path_cols < 0 || a->path_cols > 64) return DFT_ERR_UNSUPPORTED;
+  if (a->n_ends != 1 && a->n_ends != 2) return DFT_ERR_INVALID;
+  if (a->k_head_div <= 0 || a->hv % a->k_head_div != 0) return DFT_ERR_INVALID;
+  if (a->n_layers == 0 || a->batch == 0) return DFT_OK;
+  if (!a->path || !a->keys || !a->values || !a->gains || !a->src || !a->dst) return DFT_ERR_INVALID;
+  if (!index_tag(a->path_dtype)) return DFT_ERR_INVALID;
+  if (a->path_len && !index_tag(a->path_len_dtype)) return DFT_ERR_INVALID;
+  if (a->ends && !index_tag(a->ends_dtype)) return DFT_ERR_INVALID;
+  if (a->src_slots && !index_tag(a->src_slots_dtype)) return DFT_ERR_INVALID;
+  if (a->dst_slots && !index_tag(a->dst_slots_dtype)) return DFT_ERR_INVALID;
+  if ((a->flags & DFT_COMMIT_CHECK_ANC) && !a->anc_bits && !a->anc_f32) return DFT_ERR_INVALID;
+  // several ends writing one in-place state would race
+  if (a->dst == a->src && a->n_ends != 1) return DFT_ERR_INVALID;
+  const int64_t blocks = (int64_t)a->n_layers * a->batch * a->hv * a->n_ends;
+  if (blocks > INT32_MAX) return DFT_ERR_UNSUPPORTED;
+  return dft::launch_tree_commit(a, static_cast<hipStream_t>(stream));
+}
+
+int dft_tree_struct(const dft_tree_args* a, void* stream) {
+  if (!a) return DFT_ERR_INVALID;
+  if (a->batch < 0 || a->n_nodes < 0 || a->n_nodes > 64) return DFT_ERR_INVALID;
+  if (a->kc < 0 || a->kc > 16) return DFT_ERR_UNSUPPORTED;
+  if (a->batch == 0) return DFT_OK;
+  if (!a->parent || !index_tag(a->parent_dtype)) return DFT_ERR_INVALID;
+  if (a->depth && !index_tag(a->depth_dtype)) return DFT_ERR_INVALID;
+  if (a->cidx && (!index_tag(a->cidx_dtype) || a->kc < 1)) return DFT_ERR_INVALID;
+  if ((a->nxt || a->sib) && !index_tag(a->link_dtype)) return DFT_ERR_INVALID;
+  return dft::launch_tree_struct(a, static_cast<hipStream_t>(stream));
+}
+
+}  // extern "C"

@@ -1,0 +1,156 @@
+"""Drop-in for dforktree/fc1_fused.py on MI355X: the SGLang GDN adapter.
+
+Keeps the reference's module surface -- ``NN``, ``BS``, ``Context``, ``CTX``,
+``NATIVE_REFERENCE``, ``snapshots`` and ``install()`` (fc1_fused.py:4-97) --
+and routes the three hooked SGLang entry points to the gfx950 library:
+
+* ``TritonGDNKernel.target_verify``  -> ``tree_kernels.tree_gdn_split`` on the
+  conv output stashed in ``CTX.current_mixed`` (fc1_fused.py:59-75);
+* ``commit_mamba_states_after_verify`` -> the snapshot commit into
+  ``intermediate_ssm`` at the last / tracked accepted node, then SGLang's own
+  commit copies it to the live state (fc1_fused.py:77-87);
+* ``GDNAttnBackend._target_verify_supports_strided_qkv`` -> True for tree
+  verifies of NN tokens (fc1_fused.py:91-95).
+
+Shape guards fall back to the original SGLang functions exactly where the
+reference does (``cache_steps != NN``, ``draft_token_num != NN``).  Unlike
+the reference's snapshot kernel, an end of -1 (no tracked step) reads no
+state at all.
+"""
+from __future__ import annotations
+
+import os
+
+NN = int(os.environ.get('FC1_TREE_N', '64'))
+BS = int(os.environ.get('FC1_DRAFT_BLOCK', '24'))
+
+import torch  # noqa: E402
+
+if __package__:
+    from . import tree_kernels as TK
+else:  # bare import from this directory (fc1_plugin's sys.path insert)
+    import tree_kernels as TK
+try:
+    from dforktree_amd import ops as _ops
+except ImportError:
+    import pathlib
+    import sys
+    sys.path.insert(0, str(pathlib.Path(__file__).resolve().parents[1]))
+    from dforktree_amd import ops as _ops
+
+N_LAYERS = 24   # GDN layers of the target model (fc1_fused.py:15)
+N_HEADS = 32    # GDN v-heads (fc1_fused.py:15)
+D_HEAD = 128
+
+
+class Context:
+    """Per-process verify context (fc1_fused.py:12-20): the tree's ancestor
+    matrix and, per GDN layer, the normalised keys, WY values and cumulative
+    decays that the commit consumes."""
+
+    def __init__(self, device='cuda'):
+        self.anc = torch.eye(NN, device=device, dtype=torch.float32)
+        self.keys = torch.empty(N_LAYERS, N_HEADS, NN, D_HEAD, device=device)
+        self.values = torch.empty_like(self.keys)
+        self.gains = torch.empty(N_LAYERS, N_HEADS, NN, device=device)
+        self.layers = {}
+        self.inter_indices = None
+
+    def layer(self, A_log):
+        """Layer index by first sight of A_log's storage, plus the cached
+        -exp(A_log) (fc1_fused.py:65-68)."""
+        key = A_log.data_ptr()
+        if key not in self.layers:
+            self.layers[key] = (len(self.layers), -A_log.float().exp())
+        return self.layers[key]
+
+
+CTX = None
+NATIVE_REFERENCE = False
+COLLECT_LAYER = False
+LAYER_STATS = []
+
+
+def snapshot_commit(temporal, keys, values, gains, anc, accept_index, ends, slots, inter_indices,
+                    intermediate_ssm):
+    """fc1_fused.py:26-49 for every (layer, head, end):
+    intermediate_ssm[l, dst, u, h] = e^{G_u} S + sum_t on_t e^{G_u-G_t} k_t vn_t^T,
+    on_t = path node t is an ancestor-or-self of u; u in ``ends`` (-1 = skip).
+    temporal [L, slots, H, V, K]; keys/values [>=L, H, NN, 128];
+    accept_index [batch, P] (-1 padded); ends [batch*E] or [batch, E]."""
+    L = temporal.shape[0]
+    Bq = accept_index.shape[0] if accept_index.dim() == 2 else 1
+    n = anc.shape[-1]
+    _ops.tree_commit(temporal, keys[:L], values[:L], gains[:L], accept_index.reshape(Bq, -1), n_nodes=n,
+                     ends=ends.reshape(Bq, -1), anc=anc, src_slots=slots, dst=intermediate_ssm,
+                     dst_slots=inter_indices)
+
+
+class _Snapshots:
+    """Keeps the reference's launch form ``snapshots[grid](S, K, V, G, A, Path,
+    Ends, Slot, InterSlot, Out, NN, BS, *strides)``; grid and strides come
+    from the tensors themselves."""
+
+    def __getitem__(self, grid):
+        def launch(S, K, V, G, A, Path, Ends, Slot, InterSlot, Out, nn_, bs_, *strides, num_warps=4):
+            path = Path.reshape(Path.shape[0] if Path.dim() == 2 else 1, -1)[:, :int(bs_)]
+            snapshot_commit(S, K, V, G, A, path, Ends, Slot, InterSlot, Out)
+        return launch
+
+
+snapshots = _Snapshots()
+
+
+def _context():
+    global CTX
+    if CTX is None:
+        CTX = Context()
+    return CTX
+
+
+def install():
+    """Patch SGLang's GDN verify, mamba commit and routing (fc1_fused.py:51-97)."""
+    from sglang.srt.layers.attention.linear.kernels.gdn_triton import TritonGDNKernel
+    from sglang.srt.speculative import eagle_worker_common as common
+    from sglang.srt.speculative.spec_utils import _verify_commit_step_indices
+    from sglang.srt.layers.attention.linear.gdn_backend import GDNAttnBackend
+    original_verify = TritonGDNKernel.target_verify
+    original_commit = common.commit_mamba_states_after_verify
+    original_routing = GDNAttnBackend._target_verify_supports_strided_qkv
+
+    def fused(self, A_log, dt_bias, q, k, v, a, b, **kw):
+        if kw['cache_steps'] != NN:
+            return original_verify(self, A_log, dt_bias, q, k, v, a, b, **kw)
+        ctx = _context()
+        li, neg = ctx.layer(A_log)
+        assert li < N_LAYERS and q.shape[0] == 1 and q.shape[1] == NN
+        ctx.inter_indices = kw['intermediate_state_indices']
+        pool = kw['ssm_states']
+        out = TK.tree_gdn_split(ctx.current_mixed, a.reshape(NN, -1), b.reshape(NN, -1), A_log, dt_bias,
+                                pool[0].transpose(-1, -2), ctx.anc, q.shape[2], v.shape[2], q.shape[3], v.shape[3],
+                                aux=(ctx.keys[li], ctx.values[li], ctx.gains[li]), neg_exp_A=neg,
+                                state_indices=kw['cache_indices'], state_slot_stride=pool.stride(0))
+        return out.unsqueeze(0)
+
+    def fused_commit(target_worker, batch, accept_lens, accept_index, draft_token_num, prepared_step_indices=None):
+        if CTX is not None and draft_token_num == NN and accept_index.numel():
+            last, track = _verify_commit_step_indices(batch=batch, accept_index=accept_index,
+                                                      accept_lens=accept_lens, draft_token_num=draft_token_num)
+            if track is None:
+                track = torch.full_like(last, -1)
+            ends = torch.stack((last.reshape(-1), track.reshape(-1)), 1)
+            pool = target_worker.model_runner.req_to_token_pool
+            state = pool.get_speculative_mamba2_params_all_layers()
+            slots = pool.get_mamba_indices(batch.req_pool_indices)
+            snapshot_commit(state.temporal, CTX.keys, CTX.values, CTX.gains, CTX.anc, accept_index, ends, slots,
+                            CTX.inter_indices, state.intermediate_ssm)
+        return original_commit(target_worker, batch, accept_lens, accept_index, draft_token_num, prepared_step_indices)
+
+    def direct_routing(self, **kwargs):
+        if not NATIVE_REFERENCE and kwargs['draft_token_num'] == NN:
+            return True
+        return original_routing(self, **kwargs)
+
+    GDNAttnBackend._target_verify_supports_strided_qkv = direct_routing
+    TritonGDNKernel.target_verify = fused
+    common.commit_mamba_states_after_verify = fused_commit

@@ -1,0 +1,442 @@
+"""Torch-facing operators over the HIP library (batched and packed-varlen).
+
+Tensors are caller-owned device tensors passed as pointer + element strides;
+launches go on the current HIP stream of the tensors' device and nothing here
+synchronises with the host, so every operator can be captured in a HIP graph.
+Per-request slot and path indices stay on the device.
+
+These are the building blocks of the reference-named modules
+(``tree_kernels``, ``fc1_fused``, ``fc1_conv``, ``tree_ops``,
+``fc1_block_inverse``) and of the batched API the reference lacks (it is
+batch-1 only: fc1_fused.py:69, fc1_branch64.py:13).
+"""
+from __future__ import annotations
+
+import ctypes as C
+from typing import Optional
+
+import torch
+
+from . import _lib
+from ._lib import (DFT_BF16, DFT_F16, DFT_F32, DFT_I32, DFT_I64, CommitArgs, ConvArgs, TreeArgs,
+                   VerifyArgs, check, load)
+
+_FLOAT_TAG = {torch.float32: DFT_F32, torch.bfloat16: DFT_BF16, torch.float16: DFT_F16}
+_INDEX_TAG = {torch.int32: DFT_I32, torch.int64: DFT_I64}
+D_HEAD = 128
+MAX_NODES = 64
+
+
+def _ftag(t: torch.Tensor, name: str) -> int:
+    try:
+        return _FLOAT_TAG[t.dtype]
+    except KeyError:
+        raise TypeError(f"{name}: unsupported dtype {t.dtype}") from None
+
+
+def _itag(t: torch.Tensor, name: str) -> int:
+    try:
+        return _INDEX_TAG[t.dtype]
+    except KeyError:
+        raise TypeError(f"{name}: index tensor must be int32 or int64, got {t.dtype}") from None
+
+
+def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def _device_of(*ts) -> torch.device:
+    dev = None
+    for t in ts:
+        if t is None:
+            continue
+        if not t.is_cuda:
+            raise ValueError("dforktree_amd operators take GPU tensors (HIP device memory)")
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise ValueError(f"tensors on different devices: {dev} and {t.device}")
+    return dev
+
+
+def _stream(dev: torch.device) -> int:
+    return torch.cuda.current_stream(dev).cuda_stream
+
+
+def _idx_vec(t: Optional[torch.Tensor], name: str):
+    if t is None:
+        return None, DFT_I32
+    if t.dim() != 1:
+        t = t.reshape(-1)
+    if t.stride(0) != 1:
+        t = t.contiguous()
+    return t, _itag(t, name)
+
+
+# ---------------------------------------------------------------------------
+# tree verify
+# ---------------------------------------------------------------------------
+def tree_verify(y: torch.Tensor, a: torch.Tensor, b: torch.Tensor, A_log: Optional[torch.Tensor],
+                dt_bias: torch.Tensor, state: torch.Tensor, *, hk: int, hv: int,
+                anc: Optional[torch.Tensor] = None, anc_bits: Optional[torch.Tensor] = None,
+                batch: Optional[int] = None, n_nodes: Optional[int] = None,
+                cu_seqlens: Optional[torch.Tensor] = None, scale: Optional[float] = None,
+                neg_exp_A: Optional[torch.Tensor] = None, state_indices: Optional[torch.Tensor] = None,
+                state_slot_stride: Optional[int] = None, o: Optional[torch.Tensor] = None,
+                o_dtype: Optional[torch.dtype] = None, aux_k: Optional[torch.Tensor] = None,
+                aux_v: Optional[torch.Tensor] = None, aux_g: Optional[torch.Tensor] = None,
+                aux_k_per_khead: bool = False) -> torch.Tensor:
+    """Fused tree verify of every (request, v-head).
+
+    y [rows, 2*hk*128 + hv*128] bf16 with channel stride 1; a, b [rows, hv];
+    state: S0 viewed as [slots, hv, dk, dv] (index k, v; any strides -- pass
+    ``pool.transpose(-1, -2)`` for a V-major pool) or [hv, dk, dv] for one slot;
+    the tree as ``anc`` [batch, N, N] / [N, N] 0/1 or ``anc_bits`` [rows]
+    int64 bit masks.  Rows of request b start at cu_seqlens[b] (packed) or
+    b*n_nodes.  Returns o [rows, hv, dv]; aux_k [hv|hk, rows, dk],
+    aux_v [hv, rows, dv], aux_g [hv, rows] are filled when given.
+    """
+    dev = _device_of(y, a, b, A_log, dt_bias, state, anc, anc_bits, cu_seqlens, neg_exp_A,
+                     state_indices, o, aux_k, aux_v, aux_g)
+    if y.dim() != 2 or y.stride(1) != 1:
+        raise ValueError("y must be [rows, channels] with channel stride 1")
+    if y.dtype != torch.bfloat16:
+        raise TypeError("y must be bfloat16")
+    rows = y.shape[0]
+    if y.shape[1] < 2 * hk * D_HEAD + hv * D_HEAD:
+        raise ValueError(f"y has {y.shape[1]} channels, need {2 * hk * D_HEAD + hv * D_HEAD}")
+    if y.data_ptr() % 16 or y.stride(0) % 8:
+        y = y.contiguous()
+    if cu_seqlens is not None:
+        if batch is None:
+            batch = cu_seqlens.numel() - 1
+        if n_nodes is None:
+            raise ValueError("packed input needs n_nodes (the largest request) on the host")
+        if cu_seqlens.dtype != torch.int32:
+            raise TypeError("cu_seqlens must be int32")
+        cu_seqlens = cu_seqlens.contiguous()
+    else:
+        if n_nodes is None and batch is None:
+            batch, n_nodes = 1, rows
+        elif n_nodes is None:
+            n_nodes = rows // batch
+        elif batch is None:
+            batch = rows // max(n_nodes, 1)
+        if batch * n_nodes > rows:
+            raise ValueError(f"batch*n_nodes = {batch * n_nodes} exceeds the {rows} rows of y")
+    if n_nodes > MAX_NODES:
+        raise ValueError(f"at most {MAX_NODES} nodes per request, got {n_nodes}")
+    for t, nm in ((a, "a"), (b, "b")):
+        if t.dim() != 2 or t.shape[1] < hv or t.stride(1) != 1:
+            raise ValueError(f"{nm} must be [rows, hv] with stride 1 along heads")
+    if state.dim() == 3:
+        s_slot = 0 if state_slot_stride is None else state_slot_stride
+        s_h, s_k, s_v = state.stride()
+        shp = state.shape
+    elif state.dim() == 4:
+        s_slot, s_h, s_k, s_v = state.stride()
+        if state_slot_stride is not None:
+            s_slot = state_slot_stride
+        shp = state.shape[1:]
+    else:
+        raise ValueError("state must be [hv, dk, dv] or [slots, hv, dk, dv]")
+    if tuple(shp) != (hv, D_HEAD, D_HEAD):
+        raise ValueError(f"state head block must be ({hv}, 128, 128), got {tuple(shp)}")
+    if state.dtype != torch.float32:
+        raise TypeError("state must be float32")
+    if (anc is None) == (anc_bits is None):
+        raise ValueError("give exactly one of anc / anc_bits")
+    anc_row = anc_req = 0
+    if anc is not None:
+        if anc.dtype != torch.float32:
+            anc = anc.float()
+        if anc.stride(-1) != 1:
+            anc = anc.contiguous()
+        anc_row = anc.stride(-2)
+        anc_req = anc.stride(0) if anc.dim() == 3 else 0
+    if anc_bits is not None:
+        if anc_bits.dtype != torch.int64:
+            raise TypeError("anc_bits must be int64 (uint64 bit masks)")
+        anc_bits = anc_bits.contiguous()
+    if o is None:
+        o = torch.empty(rows, hv, D_HEAD, device=dev, dtype=o_dtype or y.dtype)
+    if o.stride(-1) != 1:
+        raise ValueError("o must have stride 1 along dv")
+    si, si_tag = _idx_vec(state_indices, "state_indices")
+    scale = D_HEAD ** -0.5 if scale is None else float(scale)
+
+    args = VerifyArgs()
+    args.batch, args.n_nodes, args.hk, args.hv = batch, n_nodes, hk, hv
+    args.dk = args.dv = D_HEAD
+    args.scale = scale
+    args.flags = _lib.DFT_VERIFY_AUX_K_PER_KHEAD if aux_k_per_khead else 0
+    args.y, args.y_row_stride, args.cu_seqlens = y.data_ptr(), y.stride(0), _ptr(cu_seqlens)
+    args.a, args.a_row_stride, args.a_dtype = a.data_ptr(), a.stride(0), _ftag(a, "a")
+    args.b, args.b_row_stride, args.b_dtype = b.data_ptr(), b.stride(0), _ftag(b, "b")
+    if A_log is not None:
+        args.A_log, args.A_log_dtype = A_log.data_ptr(), _ftag(A_log, "A_log")
+    args.dt_bias, args.dt_bias_dtype = dt_bias.data_ptr(), _ftag(dt_bias, "dt_bias")
+    if neg_exp_A is not None:
+        if neg_exp_A.dtype != torch.float32:
+            raise TypeError("neg_exp_A must be float32")
+        args.neg_exp_A = neg_exp_A.data_ptr()
+    args.anc_f32, args.anc_row_stride, args.anc_req_stride = _ptr(anc), anc_row, anc_req
+    args.anc_bits = _ptr(anc_bits)
+    args.state = state.data_ptr()
+    args.state_slot_stride, args.state_h_stride = s_slot, s_h
+    args.state_k_stride, args.state_v_stride = s_k, s_v
+    args.state_indices, args.state_indices_dtype = _ptr(si), si_tag
+    args.o, args.o_row_stride, args.o_h_stride, args.o_dtype = o.data_ptr(), o.stride(0), o.stride(1), _ftag(o, "o")
+    if aux_k is not None:
+        _check_aux(aux_k, "aux_k", torch.float32)
+        args.aux_k, args.aux_k_h_stride, args.aux_k_row_stride = aux_k.data_ptr(), aux_k.stride(0), aux_k.stride(1)
+    if aux_v is not None:
+        _check_aux(aux_v, "aux_v", torch.float32)
+        args.aux_v, args.aux_v_h_stride, args.aux_v_row_stride = aux_v.data_ptr(), aux_v.stride(0), aux_v.stride(1)
+    if aux_g is not None:
+        _check_aux(aux_g, "aux_g", torch.float32, dims=2)
+        args.aux_g, args.aux_g_h_stride, args.aux_g_row_stride = aux_g.data_ptr(), aux_g.stride(0), aux_g.stride(1)
+    check("dft_tree_verify", load().dft_tree_verify(C.byref(args), _stream(dev)))
+    return o
+
+
+def _check_aux(t, name, dtype, dims=3):
+    if t.dtype != dtype:
+        raise TypeError(f"{name} must be {dtype}")
+    if t.dim() != dims or (dims == 3 and t.stride(-1) != 1):
+        raise ValueError(f"{name} has the wrong shape or strides: {tuple(t.shape)} {t.stride()}")
+
+
+# ---------------------------------------------------------------------------
+# tree conv
+# ---------------------------------------------------------------------------
+def tree_conv(x: torch.Tensor, conv_state: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor],
+              cidx: torch.Tensor, *, silu: bool = True, cs_indices: Optional[torch.Tensor] = None,
+              y: Optional[torch.Tensor] = None, iw: Optional[torch.Tensor] = None,
+              iw_indices: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Tree-parent causal conv1d over a batch of trees.
+
+    x [batch, N, C] pre-conv tokens (any strides); conv_state [slots, C, >=W-1]
+    or [C, >=W-1]; weight [C, W]; bias [C] or None; cidx [batch, N, W] or
+    [N, W] (shared).  Writes y [batch, N, C] (x.dtype by default) and, when
+    given, the window iw [islots, N, C, W-1].
+    """
+    dev = _device_of(x, conv_state, weight, bias, cidx, cs_indices, y, iw, iw_indices)
+    if x.dim() == 2:
+        x = x.unsqueeze(0)
+    B, N, Cn = x.shape
+    W = weight.shape[-1]
+    if weight.dim() != 2 or weight.shape[0] != Cn:
+        raise ValueError(f"weight must be [C, W] = [{Cn}, W]")
+    cs = conv_state if conv_state.dim() == 3 else conv_state.unsqueeze(0)
+    if cs.shape[1] != Cn or cs.shape[2] < W - 1:
+        raise ValueError("conv_state must be [slots, C, >=W-1]")
+    if conv_state.dim() == 2 and cs_indices is not None:
+        raise ValueError("a 2-D conv_state has a single slot")
+    ci = cidx if cidx.dim() == 3 else cidx.unsqueeze(0)
+    if ci.shape[1] != N or ci.shape[2] != W or ci.stride(2) != 1:
+        ci = ci.contiguous()
+        if ci.shape[1] != N or ci.shape[2] != W:
+            raise ValueError(f"cidx must be [batch, {N}, {W}] or [{N}, {W}]")
+    ci_req = ci.stride(0) if ci.shape[0] == B else 0
+    if ci.shape[0] not in (1, B):
+        raise ValueError("cidx batch must be 1 or match x")
+    if y is None:
+        y = torch.empty(B, N, Cn, device=dev, dtype=x.dtype)
+    y3 = y if y.dim() == 3 else y.view(B, N, Cn)
+    if y3.stride(2) != 1:
+        raise ValueError("y must have channel stride 1")
+    a = ConvArgs()
+    a.batch, a.n_nodes, a.channels, a.width, a.silu = B, N, Cn, W, int(bool(silu))
+    a.x, a.x_req_stride, a.x_node_stride, a.x_chan_stride = x.data_ptr(), x.stride(0), x.stride(1), x.stride(2)
+    a.x_dtype = _ftag(x, "x")
+    a.conv_state, a.cs_slot_stride, a.cs_chan_stride, a.cs_col_stride = cs.data_ptr(), *cs.stride()
+    a.cs_dtype = _ftag(cs, "conv_state")
+    csi, a.cs_indices_dtype = _idx_vec(cs_indices, "cs_indices")
+    a.cs_indices = _ptr(csi)
+    a.weight, a.w_chan_stride, a.w_tap_stride, a.w_dtype = weight.data_ptr(), *weight.stride(), _ftag(weight, "weight")
+    if bias is not None:
+        a.bias, a.bias_dtype = bias.data_ptr(), _ftag(bias, "bias")
+    a.cidx, a.cidx_req_stride, a.cidx_node_stride, a.cidx_dtype = ci.data_ptr(), ci_req, ci.stride(1), _itag(ci, "cidx")
+    a.y, a.y_req_stride, a.y_node_stride, a.y_dtype = y3.data_ptr(), y3.stride(0), y3.stride(1), _ftag(y3, "y")
+    if iw is not None:
+        if iw.dim() != 4 or iw.shape[1] < N or iw.shape[2] != Cn or iw.shape[3] < W - 1:
+            raise ValueError("iw must be [islots, N, C, W-1]")
+        a.iw, a.iw_slot_stride, a.iw_node_stride, a.iw_chan_stride, a.iw_col_stride = iw.data_ptr(), *iw.stride()
+        a.iw_dtype = _ftag(iw, "iw")
+    iwi, a.iw_indices_dtype = _idx_vec(iw_indices, "iw_indices")
+    a.iw_indices = _ptr(iwi)
+    check("dft_tree_conv", load().dft_tree_conv(C.byref(a), _stream(dev)))
+    return y
+
+
+# ---------------------------------------------------------------------------
+# commit
+# ---------------------------------------------------------------------------
+def tree_commit(src: torch.Tensor, keys: torch.Tensor, values: torch.Tensor, gains: torch.Tensor,
+                path: torch.Tensor, *, n_nodes: int, path_len: Optional[torch.Tensor] = None,
+                len_is_last: bool = False, ends: Optional[torch.Tensor] = None,
+                anc: Optional[torch.Tensor] = None, anc_bits: Optional[torch.Tensor] = None,
+                cu_seqlens: Optional[torch.Tensor] = None, src_slots: Optional[torch.Tensor] = None,
+                dst: Optional[torch.Tensor] = None, dst_slots: Optional[torch.Tensor] = None,
+                kv_layout: bool = False, k_head_div: int = 1) -> torch.Tensor:
+    """Closed-form commit of the accepted path for every (layer, request, head).
+
+    src: states [L, slots, H, rows=V, cols=K] (pool layout; ``kv_layout=True``
+    for [.., K, V]); keys [L, H', T, 128], values [L, H, T, 128], gains
+    [L, H, T] as saved by ``tree_verify`` (T = total node rows); path
+    [batch, P] accepted local node ids (-1 padded).  In place when ``dst`` is
+    None; otherwise dst is [L, dslots, N, H, rows, cols] and receives S_u at
+    node u for every end in ``ends`` [batch, E] (-1 = skip).  ``anc`` /
+    ``anc_bits`` restrict the sum to ancestors of u (fc1_fused.py:41).
+    """
+    dev = _device_of(src, keys, values, gains, path, path_len, ends, anc, anc_bits, cu_seqlens,
+                     src_slots, dst, dst_slots)
+    if src.dim() != 5 or tuple(src.shape[-2:]) != (D_HEAD, D_HEAD):
+        raise ValueError("src must be [L, slots, H, 128, 128]")
+    L, _, H = src.shape[:3]
+    for t, nm in ((src, "src"), (keys, "keys"), (values, "values"), (gains, "gains")):
+        if t.dtype != torch.float32:
+            raise TypeError(f"{nm} must be float32")
+    if keys.dim() != 4 or values.dim() != 4 or gains.dim() != 3:
+        raise ValueError("keys/values must be [L, H, rows, 128], gains [L, H, rows]")
+    if keys.stride(-1) != 1 or values.stride(-1) != 1:
+        raise ValueError("keys/values need stride 1 along the head dim")
+    if path.dim() == 1:
+        path = path.unsqueeze(0)
+    if path.stride(1) != 1:
+        path = path.contiguous()
+    B, P = path.shape
+    if P > MAX_NODES or n_nodes > MAX_NODES:
+        raise ValueError(f"paths and trees are limited to {MAX_NODES} nodes")
+    a = CommitArgs()
+    a.n_layers, a.batch, a.hv, a.dk, a.dv = L, B, H, D_HEAD, D_HEAD
+    a.n_nodes, a.path_cols = n_nodes, P
+    a.k_head_div = k_head_div
+    flags = _lib.DFT_COMMIT_KV if kv_layout else 0
+    if len_is_last:
+        flags |= _lib.DFT_COMMIT_LEN_IS_LAST
+    a.path, a.path_req_stride, a.path_dtype = path.data_ptr(), path.stride(0), _itag(path, "path")
+    pl, a.path_len_dtype = _idx_vec(path_len, "path_len")
+    a.path_len = _ptr(pl)
+    if ends is not None:
+        if ends.dim() == 1:
+            ends = ends.unsqueeze(1) if B > 1 or ends.numel() == 1 else ends.unsqueeze(0)
+        ends = ends.contiguous()
+        a.n_ends = ends.shape[1]
+        a.ends, a.ends_req_stride, a.ends_dtype = ends.data_ptr(), ends.stride(0), _itag(ends, "ends")
+    else:
+        a.n_ends = 1
+    if anc is not None or anc_bits is not None:
+        flags |= _lib.DFT_COMMIT_CHECK_ANC
+        if anc_bits is not None:
+            if anc_bits.dtype != torch.int64:
+                raise TypeError("anc_bits must be int64")
+            anc_bits = anc_bits.contiguous()
+            a.anc_bits = anc_bits.data_ptr()
+        else:
+            anc = anc.float().contiguous()
+            a.anc_f32, a.anc_row_stride = anc.data_ptr(), anc.stride(-2)
+            a.anc_req_stride = anc.stride(0) if anc.dim() == 3 else 0
+    a.flags = flags
+    if cu_seqlens is not None:
+        if cu_seqlens.dtype != torch.int32:
+            raise TypeError("cu_seqlens must be int32")
+        cu_seqlens = cu_seqlens.contiguous()
+        a.cu_seqlens = cu_seqlens.data_ptr()
+    a.keys, a.k_layer_stride, a.k_h_stride, a.k_row_stride = keys.data_ptr(), *keys.stride()[:3]
+    a.values, a.v_layer_stride, a.v_h_stride, a.v_row_stride = values.data_ptr(), *values.stride()[:3]
+    a.gains, a.g_layer_stride, a.g_h_stride, a.g_row_stride = gains.data_ptr(), *gains.stride()
+    a.src = src.data_ptr()
+    (a.src_layer_stride, a.src_slot_stride, a.src_h_stride, a.src_row_stride, a.src_col_stride) = src.stride()
+    ss, a.src_slots_dtype = _idx_vec(src_slots, "src_slots")
+    a.src_slots = _ptr(ss)
+    if dst is None:
+        a.dst = a.src
+        (a.dst_layer_stride, a.dst_slot_stride, a.dst_h_stride, a.dst_row_stride, a.dst_col_stride) = src.stride()
+        a.dst_node_stride = 0
+        if a.n_ends != 1:
+            raise ValueError("an in-place commit takes one end per request")
+    else:
+        if dst.dim() != 6 or tuple(dst.shape[-2:]) != (D_HEAD, D_HEAD) or dst.dtype != torch.float32:
+            raise ValueError("dst must be float32 [L, slots, N, H, 128, 128]")
+        a.dst = dst.data_ptr()
+        (a.dst_layer_stride, a.dst_slot_stride, a.dst_node_stride, a.dst_h_stride, a.dst_row_stride,
+         a.dst_col_stride) = dst.stride()
+    ds, a.dst_slots_dtype = _idx_vec(dst_slots, "dst_slots")
+    a.dst_slots = _ptr(ds)
+    check("dft_tree_commit", load().dft_tree_commit(C.byref(a), _stream(dev)))
+    return src if dst is None else dst
+
+
+# ---------------------------------------------------------------------------
+# tree structure and the standalone inverse
+# ---------------------------------------------------------------------------
+def tree_struct(parent: torch.Tensor, kc: int = 4, *, batch: Optional[int] = None,
+                n_nodes: Optional[int] = None, cu_seqlens: Optional[torch.Tensor] = None,
+                want=("anc_bits", "anc", "depth", "cidx", "nxt", "sib", "status"),
+                index_dtype: torch.dtype = torch.int64) -> dict:
+    """Ancestor bits / dense Anc / depth / cidx / nxt / sib of a batch of trees
+    given by parent indices [rows] (or [batch, N])."""
+    dev = _device_of(parent, cu_seqlens)
+    if parent.dim() == 2:
+        batch, n_nodes = parent.shape
+        parent = parent.reshape(-1)
+    parent = parent.contiguous()
+    rows = parent.numel()
+    if cu_seqlens is not None:
+        batch = cu_seqlens.numel() - 1 if batch is None else batch
+        if n_nodes is None:
+            raise ValueError("packed input needs n_nodes (the largest request)")
+        cu_seqlens = cu_seqlens.contiguous()
+    else:
+        if batch is None and n_nodes is None:
+            batch, n_nodes = 1, rows
+        elif n_nodes is None:
+            n_nodes = rows // batch
+        elif batch is None:
+            batch = rows // max(n_nodes, 1)
+    if n_nodes > MAX_NODES:
+        raise ValueError(f"at most {MAX_NODES} nodes per tree")
+    out = {}
+    a = TreeArgs()
+    a.batch, a.n_nodes, a.kc = batch, n_nodes, kc
+    a.parent, a.parent_dtype = parent.data_ptr(), _itag(parent, "parent")
+    a.cu_seqlens = _ptr(cu_seqlens)
+    if "anc_bits" in want:
+        out["anc_bits"] = torch.zeros(rows, device=dev, dtype=torch.int64)
+        a.anc_bits = out["anc_bits"].data_ptr()
+    if "anc" in want:
+        out["anc"] = torch.zeros(batch, n_nodes, n_nodes, device=dev, dtype=torch.float32)
+        a.anc_f32, a.anc_row_stride, a.anc_req_stride = out["anc"].data_ptr(), n_nodes, n_nodes * n_nodes
+    if "depth" in want:
+        out["depth"] = torch.empty(rows, device=dev, dtype=index_dtype)
+        a.depth, a.depth_dtype = out["depth"].data_ptr(), _itag(out["depth"], "depth")
+    if "cidx" in want:
+        out["cidx"] = torch.empty(rows, kc, device=dev, dtype=index_dtype)
+        a.cidx, a.cidx_dtype = out["cidx"].data_ptr(), _itag(out["cidx"], "cidx")
+    a.link_dtype = _INDEX_TAG[index_dtype]
+    if "nxt" in want:
+        out["nxt"] = torch.empty(rows, device=dev, dtype=index_dtype)
+        a.nxt = out["nxt"].data_ptr()
+    if "sib" in want:
+        out["sib"] = torch.empty(rows, device=dev, dtype=index_dtype)
+        a.sib = out["sib"].data_ptr()
+    if "status" in want:
+        out["status"] = torch.empty(batch, device=dev, dtype=torch.int32)
+        a.status = out["status"].data_ptr()
+    check("dft_tree_struct", load().dft_tree_struct(C.byref(a), _stream(dev)))
+    return out
+
+
+def block_inverse_(x: torch.Tensor) -> torch.Tensor:
+    """In place: x[..., n, n] (strictly-lower A, fp32) <- (I + A)^-1, n <= 64."""
+    dev = _device_of(x)
+    if x.dtype != torch.float32 or x.dim() < 2 or x.shape[-1] != x.shape[-2]:
+        raise ValueError("x must be float32 [..., n, n]")
+    if not x.is_contiguous():
+        raise ValueError("x must be contiguous (it is updated in place)")
+    n = x.shape[-1]
+    mats = x.numel() // max(n * n, 1)
+    check("dft_block_inverse", load().dft_block_inverse(x.data_ptr(), mats, n, n * n, _stream(dev)))
+    return x

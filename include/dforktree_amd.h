@@ -1,0 +1,264 @@
+/*
+ * dforktree_amd -- C ABI of the MI355X (gfx950) GDN tree-verify path.
+ *
+ * Every entry point:
+ *   - takes plain device pointers, element strides and sizes in a POD
+ *     descriptor plus a hipStream_t (passed as void*; NULL = legacy stream);
+ *   - allocates nothing and never synchronises with the host, so it can be
+ *     recorded into a hipGraph;
+ *   - reads per-request slot / path indices on the device;
+ *   - returns DFT_OK or a DFT_ERR_* code (dft_error_string explains it).
+ *     A non-zero status means nothing was launched.
+ *
+ * Dtype tags (the *_dtype fields): DFT_F32, DFT_BF16, DFT_F16 for floating
+ * inputs, DFT_I32 / DFT_I64 for index arrays.
+ *
+ * Reference interfaces replaced (Perseus037/DForkTree, dforktree/):
+ *   dft_tree_verify    tree_gdn_split   tree_kernels.py:193-208 (with
+ *                      _tree_prepare :135-164, invert{16,32,64}
+ *                      fc1_block_inverse.py:36-83, _tree_finish :166-191) and
+ *                      tree_gdn_fused   tree_kernels.py:95-108
+ *   dft_tree_conv      fc1_conv.conv / install.call   fc1_conv.py:7-46 and
+ *                      tree_conv_fused  tree_kernels.py:17-33, :86-93
+ *   dft_tree_commit    closed_commit    tree_kernels.py:111-132 (in place) and
+ *                      fc1_fused.snapshots / fused_commit fc1_fused.py:26-49,
+ *                      :77-87 (snapshot into the intermediate cache)
+ *   dft_tree_struct    tree_ops.tree_struct tree_ops.py:68-89 and the builder's
+ *                      nxt/sib links fc1_builder.py:38-47
+ *   dft_block_inverse  invert16/32/64   fc1_block_inverse.py:36-83
+ */
+#ifndef DFORKTREE_AMD_H
+#define DFORKTREE_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define DFT_ABI_VERSION 1
+
+#if defined(__GNUC__)
+#define DFT_API __attribute__((visibility("default")))
+#else
+#define DFT_API
+#endif
+
+enum dft_status {
+  DFT_OK = 0,
+  DFT_ERR_INVALID = 1,     /* a pointer, size, stride or alignment is invalid */
+  DFT_ERR_UNSUPPORTED = 2, /* valid but not implemented here (e.g. Dk != 128) */
+  DFT_ERR_LAUNCH = 3       /* the HIP runtime rejected the launch */
+};
+
+enum dft_dtype { DFT_F32 = 0, DFT_BF16 = 1, DFT_F16 = 2, DFT_I32 = 3, DFT_I64 = 4 };
+
+/* ---------------------------------------------------------------------------
+ * Tree verify: one fused launch of prepare + (I+A)^-1 + finish for every
+ * (request, v-head).  Node i of request b lives at row row0(b)+i of y/a/b/o,
+ * row0(b) = cu_seqlens[b] if cu_seqlens else b*n_nodes.
+ * ------------------------------------------------------------------------- */
+enum dft_verify_flags {
+  DFT_VERIFY_AUX_K_PER_KHEAD = 1 /* aux_k holds one row set per k-head */
+};
+
+typedef struct dft_verify_args {
+  int32_t batch;   /* requests */
+  int32_t n_nodes; /* nodes per request; with cu_seqlens the maximum, <= 64 */
+  int32_t hk, hv;  /* q/k heads and v heads, hv % hk == 0 */
+  int32_t dk, dv;  /* head dims, both 128 */
+  float scale;     /* q scale (reference default dk^-0.5) */
+  int32_t flags;   /* dft_verify_flags */
+
+  /* y [rows, 2*hk*dk + hv*dv] bf16 = [q | k | v], channel stride 1 */
+  const void* y;
+  int64_t y_row_stride;
+  const int32_t* cu_seqlens; /* [batch+1] or NULL */
+
+  /* gate inputs a, b [rows, hv] (channel stride 1) and per-head A_log, dt_bias */
+  const void* a;
+  int64_t a_row_stride;
+  int32_t a_dtype;
+  const void* b;
+  int64_t b_row_stride;
+  int32_t b_dtype;
+  const void* A_log;
+  int32_t A_log_dtype;
+  const void* dt_bias;
+  int32_t dt_bias_dtype;
+  const float* neg_exp_A; /* [hv] cached -exp(A_log), or NULL */
+
+  /* tree: exactly one of anc_f32 (0/1 matrix per request) or anc_bits
+   * (uint64 per row, bit j = node j is an ancestor-or-self). Nodes must be
+   * in topological order (parent < child); bits above the diagonal are
+   * ignored. */
+  const float* anc_f32;
+  int64_t anc_row_stride, anc_req_stride;
+  const uint64_t* anc_bits;
+
+  /* initial state S0(k, v) = state[slot*slot_stride + h*h_stride + k*k_stride
+   * + v*v_stride], fp32.  slot = max(state_indices[b], 0), or b if NULL. */
+  const float* state;
+  int64_t state_slot_stride, state_h_stride, state_k_stride, state_v_stride;
+  const void* state_indices;
+  int32_t state_indices_dtype;
+
+  /* outputs o[row][h][v] (bf16 or f32), channel stride 1 */
+  void* o;
+  int64_t o_row_stride, o_h_stride;
+  int32_t o_dtype;
+
+  /* optional saves for the commit (fp32; NULL to skip):
+   * aux_k[h'][row][dk] normalised keys (h' = h, or h/(hv/hk) with
+   * DFT_VERIFY_AUX_K_PER_KHEAD), aux_v[h][row][dv] the WY values vn,
+   * aux_g[h][row] the path-cumulative log decay G. */
+  float* aux_k;
+  int64_t aux_k_h_stride, aux_k_row_stride;
+  float* aux_v;
+  int64_t aux_v_h_stride, aux_v_row_stride;
+  float* aux_g;
+  int64_t aux_g_h_stride, aux_g_row_stride;
+} dft_verify_args;
+
+DFT_API int dft_tree_verify(const dft_verify_args* args, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Tree-parent causal conv1d: y[n,c] = act(sum_j w[c,j] xt[cidx[n,j]][c] + bias[c])
+ * with xt = [conv_state columns 0..width-2 || x tokens]; optionally writes
+ * the per-node window iw[dst][n][c][j-1] = xt[cidx[n,j]][c] for j >= 1.
+ * ------------------------------------------------------------------------- */
+typedef struct dft_conv_args {
+  int32_t batch, n_nodes, channels, width; /* width = taps (<= 8) */
+  int32_t silu;                            /* 1: SiLU, 0: identity */
+
+  const void* x; /* token n of request b, channel c */
+  int64_t x_req_stride, x_node_stride, x_chan_stride;
+  int32_t x_dtype;
+
+  const void* conv_state; /* [slot][c][col] */
+  int64_t cs_slot_stride, cs_chan_stride, cs_col_stride;
+  int32_t cs_dtype;
+  const void* cs_indices; /* slot per request, or NULL: slot = b */
+  int32_t cs_indices_dtype;
+
+  const void* weight; /* [c][tap] */
+  int64_t w_chan_stride, w_tap_stride;
+  int32_t w_dtype;
+  const void* bias; /* [c] or NULL */
+  int32_t bias_dtype;
+
+  const void* cidx; /* [b][n][tap] column into xt */
+  int64_t cidx_req_stride, cidx_node_stride;
+  int32_t cidx_dtype;
+
+  void* y; /* [b][n][c] */
+  int64_t y_req_stride, y_node_stride;
+  int32_t y_dtype;
+
+  void* iw; /* optional [dst][n][c][col] */
+  int64_t iw_slot_stride, iw_node_stride, iw_chan_stride, iw_col_stride;
+  int32_t iw_dtype;
+  const void* iw_indices; /* dst per request, or NULL: dst = b */
+  int32_t iw_indices_dtype;
+} dft_conv_args;
+
+DFT_API int dft_tree_conv(const dft_conv_args* args, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Closed-form accepted-path commit, for every (layer, request, head, end):
+ *   S_u = e^{G_u} S0 + sum_{t in path, t anc-or-self of u} e^{G_u-G_t} k_t vn_t^T
+ * written in place (dst == src, dst_node_stride 0) or into a snapshot slot.
+ * The state is addressed as rows x cols with rows = v and cols = k for the
+ * V-major pool layout (src_row_stride = v stride); pass DFT_COMMIT_KV to
+ * address rows = k, cols = v instead.
+ * ------------------------------------------------------------------------- */
+enum dft_commit_flags {
+  DFT_COMMIT_KV = 1,        /* state rows are k, columns are v */
+  DFT_COMMIT_CHECK_ANC = 2, /* count only path nodes that are ancestors of u */
+  DFT_COMMIT_LEN_IS_LAST = 4 /* path_len holds the index of the last entry */
+};
+
+typedef struct dft_commit_args {
+  int32_t n_layers, batch, hv;
+  int32_t dk, dv;      /* both 128 */
+  int32_t n_nodes;     /* nodes per request (index bound), <= 64 */
+  int32_t path_cols;   /* entries per request in path, <= 64 */
+  int32_t n_ends;      /* 1 or 2 */
+  int32_t flags;       /* dft_commit_flags */
+  int32_t k_head_div;  /* aux_k head = h / k_head_div */
+
+  const void* path; /* [b][path_cols] node ids, negative = unused */
+  int64_t path_req_stride;
+  int32_t path_dtype;
+  const void* path_len; /* [b] number of valid entries, or NULL (all >= 0 entries) */
+  int32_t path_len_dtype;
+  const void* ends; /* [b][n_ends] node u to commit, negative = skip; NULL: u = last path entry */
+  int64_t ends_req_stride;
+  int32_t ends_dtype;
+
+  const uint64_t* anc_bits; /* for DFT_COMMIT_CHECK_ANC: [rows] */
+  const float* anc_f32;     /*   or 0/1 matrices per request */
+  int64_t anc_row_stride, anc_req_stride;
+  const int32_t* cu_seqlens; /* row0(b) as in dft_verify_args */
+
+  const float* keys; /* [l][h'][row][dk] */
+  int64_t k_layer_stride, k_h_stride, k_row_stride;
+  const float* values; /* [l][h][row][dv] */
+  int64_t v_layer_stride, v_h_stride, v_row_stride;
+  const float* gains; /* [l][h][row] */
+  int64_t g_layer_stride, g_h_stride, g_row_stride;
+
+  const float* src; /* [l][slot][h][row][col] */
+  int64_t src_layer_stride, src_slot_stride, src_h_stride, src_row_stride, src_col_stride;
+  const void* src_slots; /* slot per request (clamped >= 0), or NULL: b */
+  int32_t src_slots_dtype;
+
+  float* dst; /* [l][slot][u][h][row][col] */
+  int64_t dst_layer_stride, dst_slot_stride, dst_node_stride, dst_h_stride, dst_row_stride,
+      dst_col_stride;
+  const void* dst_slots; /* dst slot per request, or NULL: same as src slot */
+  int32_t dst_slots_dtype;
+} dft_commit_args;
+
+DFT_API int dft_tree_commit(const dft_commit_args* args, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Tree structure from parent indices (node 0 is the root; for i >= 1 the
+ * parent is max(parent[i], 0) as tree_ops.py:73 clamps it).  Exact closure
+ * for any depth.  Every output is optional.
+ * ------------------------------------------------------------------------- */
+typedef struct dft_tree_args {
+  int32_t batch, n_nodes, kc; /* kc: conv taps for cidx (<= 16) */
+  const void* parent;         /* [rows] local parent index */
+  int32_t parent_dtype;
+  const int32_t* cu_seqlens; /* row0(b) as in dft_verify_args */
+  uint64_t* anc_bits;        /* [rows] */
+  float* anc_f32;            /* [b][i][j] dense 0/1 */
+  int64_t anc_row_stride, anc_req_stride;
+  void* depth; /* [rows] */
+  int32_t depth_dtype;
+  void* cidx; /* [rows][kc] */
+  int32_t cidx_dtype;
+  void* nxt; /* [rows] first child or -1 */
+  void* sib; /* [rows] next sibling or -1 */
+  int32_t link_dtype;
+  int32_t* status; /* optional [batch]: 0 ok, 1 parent not < child, 2 cycle */
+} dft_tree_args;
+
+DFT_API int dft_tree_struct(const dft_tree_args* args, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * In-place (I + A)^-1 of n_mats strictly-lower-triangular fp32 n x n matrices
+ * (n <= 64, row-major, consecutive matrices mat_stride elements apart).
+ * The upper triangle of the result is zeroed.
+ * ------------------------------------------------------------------------- */
+DFT_API int dft_block_inverse(float* x, int32_t n_mats, int32_t n, int64_t mat_stride, void* stream);
+
+DFT_API const char* dft_error_string(int status);
+DFT_API int dft_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DFORKTREE_AMD_H */

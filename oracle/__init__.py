@@ -1,0 +1,25 @@
+"""CPU oracle for the GDN tree-verify path.
+
+TEST INFRASTRUCTURE ONLY. This package is the checker, never the product:
+only ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of
+``bench.py`` may import it.  The product path (``dforktree_amd``) runs the HIP
+kernels and raises when the HIP library is missing; it never calls in here.
+
+Contents (``oracle.gdn_tree``):
+
+* ``tree_struct``            exact ancestor closure / depth / conv gather columns
+                             (tree_ops.py:68-89), ``tree_links`` (fc1_builder.py:41-47)
+* ``prepare`` / ``block_invert`` / ``finish`` / ``tree_gdn_split``
+                             fp32 restatement of the split verify
+                             (tree_kernels.py:135-208, fc1_block_inverse.py:10-83)
+* ``tree_gdn_neumann``       the single-kernel variant with its Neumann-16
+                             inverse (tree_kernels.py:35-81)
+* ``recurrent_f64``          independent fp64 per-node recurrence (the pin)
+* ``tree_conv``              tree-parent causal conv1d (fc1_conv.py:7-27,
+                             tree_kernels.py:17-33)
+* ``closed_commit`` / ``snapshot_commit`` closed-form accepted-path commit
+                             (tree_kernels.py:111-127, fc1_fused.py:26-49)
+
+Pinning status of every function is listed in the module docstring of
+``oracle.gdn_tree``.
+"""

@@ -1,0 +1,103 @@
+"""The C ABI boundary, checked on the CPU: the library loads, exports every
+entry point the header declares, the ctypes descriptors match the C structs
+byte for byte (offsets computed by gcc from the header), and argument
+validation rejects bad descriptors before any launch."""
+import ctypes
+import json
+import re
+import subprocess
+
+import pytest
+
+from conftest import ROOT
+
+HEADER = ROOT / "include" / "dforktree_amd.h"
+
+
+def declared_functions():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^DFT_API\s+(?:int|const char\*)\s+(dft_\w+)\s*\(", text, re.M)))
+
+
+def test_library_exports_every_declared_symbol():
+    from dforktree_amd import _lib
+    names = declared_functions()
+    assert set(names) == set(_lib.EXPORTS)
+    lib = _lib.load()
+    for n in names:
+        assert getattr(lib, n) is not None
+    out = subprocess.run(["nm", "-D", "--defined-only", str(_lib.LIB_PATH)], capture_output=True, text=True).stdout
+    exported = {l.split()[-1] for l in out.splitlines() if " T " in l}
+    assert exported == set(names), "only the C ABI is exported"
+    assert lib.dft_abi_version() == 1
+
+
+@pytest.fixture(scope="module")
+def c_layouts(tmp_path_factory):
+    from dforktree_amd import _lib
+    structs = {"dft_verify_args": _lib.VerifyArgs, "dft_conv_args": _lib.ConvArgs,
+               "dft_commit_args": _lib.CommitArgs, "dft_tree_args": _lib.TreeArgs}
+    lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"', "int main(void) {",
+             'printf("{");']
+    first = True
+    for cname, py in structs.items():
+        for f, _ in py._fields_:
+            sep = "" if first else ","
+            first = False
+            lines.append(f'printf("{sep}\\"{cname}.{f}\\": %zu", offsetof({cname}, {f}));')
+        lines.append(f'printf(",\\"{cname}.__size__\\": %zu", sizeof({cname}));')
+    lines += ['printf("}");', "return 0; }"]
+    d = tmp_path_factory.mktemp("abi")
+    src, exe = d / "layout.c", d / "layout"
+    src.write_text("\n".join(lines))
+    subprocess.run(["gcc", "-std=c99", "-o", str(exe), str(src)], check=True)
+    return json.loads(subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout), structs
+
+
+def test_ctypes_structs_match_c_layout(c_layouts):
+    layout, structs = c_layouts
+    for cname, py in structs.items():
+        assert ctypes.sizeof(py) == layout[f"{cname}.__size__"], cname
+        for f, _ in py._fields_:
+            assert getattr(py, f).offset == layout[f"{cname}.{f}"], f"{cname}.{f}"
+
+
+def test_validation_rejects_bad_descriptors_without_launching():
+    """Every check below fails on the host before any HIP call."""
+    from dforktree_amd import _lib
+    lib = _lib.load()
+    v = _lib.VerifyArgs()
+    v.batch, v.n_nodes, v.hk, v.hv, v.dk, v.dv = 1, 32, 2, 4, 64, 128
+    assert lib.dft_tree_verify(ctypes.byref(v), None) == _lib.DFT_ERR_UNSUPPORTED  # dk != 128
+    v.dk = 128
+    v.hv = 3
+    assert lib.dft_tree_verify(ctypes.byref(v), None) == _lib.DFT_ERR_INVALID      # hv % hk
+    v.hv, v.n_nodes = 4, 65
+    assert lib.dft_tree_verify(ctypes.byref(v), None) == _lib.DFT_ERR_UNSUPPORTED  # > 64 nodes
+    v.n_nodes = 32
+    assert lib.dft_tree_verify(ctypes.byref(v), None) == _lib.DFT_ERR_INVALID      # null pointers
+    v.batch = 0
+    assert lib.dft_tree_verify(ctypes.byref(v), None) == _lib.DFT_OK                # empty batch: no-op
+    c = _lib.CommitArgs()
+    c.n_layers, c.batch, c.hv, c.dk, c.dv, c.n_nodes, c.path_cols, c.n_ends, c.k_head_div = 1, 1, 4, 128, 128, 32, 16, 3, 1
+    assert lib.dft_tree_commit(ctypes.byref(c), None) == _lib.DFT_ERR_INVALID       # n_ends
+    c.n_ends = 2
+    c.path = c.keys = c.values = c.gains = c.src = c.dst = 16
+    assert lib.dft_tree_commit(ctypes.byref(c), None) == _lib.DFT_ERR_INVALID       # 2 ends in place
+    t = _lib.TreeArgs()
+    t.batch, t.n_nodes, t.kc = 1, 65, 4
+    assert lib.dft_tree_struct(ctypes.byref(t), None) == _lib.DFT_ERR_INVALID
+    k = _lib.ConvArgs()
+    k.batch, k.n_nodes, k.channels, k.width = 1, 4, 8, 9
+    assert lib.dft_tree_conv(ctypes.byref(k), None) == _lib.DFT_ERR_UNSUPPORTED
+    assert lib.dft_block_inverse(None, 1, 65, 65 * 65, None) == _lib.DFT_ERR_INVALID
+    assert lib.dft_error_string(2) == b"unsupported configuration"
+
+
+def test_python_layer_refuses_cpu_tensors():
+    """No CPU fallback: the operators take device tensors only."""
+    import torch
+    from dforktree_amd import ops
+    x = torch.zeros(4, 4)
+    with pytest.raises(ValueError, match="GPU tensors"):
+        ops.block_inverse_(x)

@@ -1,0 +1,167 @@
+"""GPU parity of the closed-form accepted-path commit.
+
+Committed states: rel-L2 <= 2e-3 against the fp64 sequential replay of the
+accepted tokens (the commit after a GPU verify), and 1e-5 against the fp32
+closed form on the same saved inputs; path/ancestor index handling is exact
+(a state the path does not reach is bit-identical to its input).
+"""
+import numpy as np
+import pytest
+import torch
+
+from conftest import REL_L2, announce, rel_l2
+from _ref import np32, request_slices
+from oracle import gdn_tree as O
+
+pytestmark = pytest.mark.gpu
+
+
+def _aux(seed, L, H, rows):
+    g = torch.Generator().manual_seed(seed)
+    k = torch.randn(L, H, rows, 128, generator=g)
+    k = k / k.norm(dim=-1, keepdim=True)
+    v = torch.randn(L, H, rows, 128, generator=g) * 0.3
+    gains = -torch.rand(L, H, rows, generator=g) * 2.0
+    return k, v, gains
+
+
+def _paths(pars, max_len, seed):
+    from dforktree_amd import synth
+    g = torch.Generator().manual_seed(seed)
+    paths = [synth.accepted_path(p, max_len, g) for p in pars]
+    P = max_len
+    idx = torch.full((len(paths), P), -1, dtype=torch.int32)
+    for i, p in enumerate(paths):
+        idx[i, :len(p)] = p
+    return paths, idx, torch.tensor([len(p) for p in paths], dtype=torch.int32)
+
+
+def test_commit_inplace_closed_form(cuda):
+    from dforktree_amd import ops, synth
+    announce("commit in place closed form")
+    L, B, H, N = 3, 6, 4, 32
+    g = torch.Generator().manual_seed(0)
+    pars = [synth.tree_parents(N, "random", g) for _ in range(B)]
+    keys, vals, gains = _aux(1, L, H, B * N)
+    S = torch.randn(L, B, H, 128, 128) * 0.02  # [L, slot, H, V, K]
+    paths, idx, lens = _paths(pars, 16, 2)
+    Sg = S.to(cuda)
+    ops.tree_commit(Sg, keys.to(cuda), vals.to(cuda), gains.to(cuda), idx.to(cuda), n_nodes=N,
+                    path_len=lens.to(cuda))
+    torch.cuda.synchronize()
+    got = np32(Sg)
+    for l in range(L):
+        for b in range(B):
+            sl = slice(b * N, (b + 1) * N)
+            want = O.closed_commit(np32(S[l, b]).transpose(0, 2, 1), np32(keys[l, :, sl]), np32(vals[l, :, sl]),
+                                   np32(gains[l, :, sl]), paths[b].tolist())
+            assert rel_l2(got[l, b].transpose(0, 2, 1), want) <= 1e-5, (l, b)
+
+
+def test_verify_then_commit_matches_replay(cuda):
+    """Config-4 shape in miniature: verify every layer on the GPU (saving k, vn,
+    G), commit the accepted root-to-node walk in place, compare with an fp64
+    decoder that consumes only the accepted tokens."""
+    from dforktree_amd import ops, synth
+    announce("verify+commit vs replay")
+    L, B, N, hk, hv = 2, 5, 32, 2, 4
+    batches = [synth.make_batch(4, l, [N] * B, hk=hk, hv=hv, kinds=["random", "chain", "bushy", "random", "chain"])
+               for l in range(L)]
+    pars = [batches[0].parent[s] for s in request_slices(batches[0])]
+    for bt in batches[1:]:  # same trees in every layer
+        bt.parent = batches[0].parent.clone()
+    rows = B * N
+    keys = torch.zeros(L, hv, rows, 128, device=cuda)
+    vals = torch.zeros(L, hv, rows, 128, device=cuda)
+    gains = torch.zeros(L, hv, rows, device=cuda)
+    state = torch.stack([bt.state for bt in batches]).to(cuda)  # [L, B, hv, V, K]
+    ts = ops.tree_struct(batches[0].parent.to(cuda), 4, batch=B, n_nodes=N, want=("anc_bits",))
+    for l, bt in enumerate(batches):
+        gb = bt.to(cuda)
+        ops.tree_verify(gb.y, gb.a, gb.b, gb.A_log, gb.dt_bias, state[l].transpose(-1, -2), hk=hk, hv=hv,
+                        anc_bits=ts["anc_bits"], batch=B, n_nodes=N, aux_k=keys[l], aux_v=vals[l], aux_g=gains[l])
+    paths, idx, lens = _paths(pars, 16, 3)
+    ops.tree_commit(state, keys, vals, gains, idx.to(cuda), n_nodes=N, path_len=lens.to(cuda))
+    torch.cuda.synchronize()
+    got = np32(state)
+    for l, bt in enumerate(batches):
+        for b, sl in enumerate(request_slices(bt)):
+            S0 = np32(bt.state[b]).transpose(0, 2, 1)
+            want = O.replay_path_f64(np32(bt.y[sl]), np32(bt.a[sl]), np32(bt.b[sl]), np32(bt.A_log),
+                                     np32(bt.dt_bias), S0, paths[b].tolist(), hk, hv, 128, 128)
+            assert rel_l2(got[l, b].transpose(0, 2, 1), want) <= REL_L2, (l, b)
+
+
+def test_snapshot_two_ends_with_ancestry(cuda):
+    """fc1_fused snapshot form: two ends per request (last accepted and a
+    tracked earlier step, or -1), ancestry-checked path, a separate
+    destination cache indexed by node; untouched destinations stay intact."""
+    from dforktree_amd import fc1_fused, synth
+    announce("snapshot two ends")
+    L, B, H, N = 2, 3, 4, 32
+    g = torch.Generator().manual_seed(5)
+    pars = [synth.tree_parents(N, "random", g) for _ in range(B)]
+    keys, vals, gains = _aux(6, L, H, B * N)
+    temporal = torch.randn(L, 4, H, 128, 128) * 0.02
+    slots = torch.tensor([2, 0, 3], dtype=torch.int32)
+    dsts = torch.tensor([1, 0, 2], dtype=torch.int32)
+    paths, idx, lens = _paths(pars, 16, 7)
+    # add an off-path node id to each path row to exercise the ancestry mask
+    anc = torch.stack([torch.from_numpy(O.tree_struct(p.numpy())[0]) for p in pars])
+    ends = torch.full((B, 2), -1, dtype=torch.int32)
+    for b, p in enumerate(paths):
+        ends[b, 0] = p[-1]
+        if len(p) > 2:
+            ends[b, 1] = p[len(p) // 2]
+        if len(p) < 16:
+            off = [u for u in range(N) if anc[b, p[-1], u] < 0.5]
+            if off:
+                idx[b, len(p)] = off[0]
+    sentinel = 123.0
+    out = torch.full((L, 3, N, H, 128, 128), sentinel)
+    outg = out.to(cuda)
+    for b in range(B):
+        # snapshot_commit is the batch-1 hook form; call it per request with its own slice
+        sl = slice(b * N, (b + 1) * N)
+        fc1_fused.snapshot_commit(temporal.to(cuda), keys[:, :, sl].contiguous().to(cuda),
+                                  vals[:, :, sl].contiguous().to(cuda), gains[:, :, sl].contiguous().to(cuda),
+                                  anc[b].to(cuda), idx[b:b + 1].to(cuda), ends[b].to(cuda), slots[b:b + 1].to(cuda),
+                                  dsts[b:b + 1].to(cuda), outg)
+    torch.cuda.synchronize()
+    got = outg.cpu()
+    touched = torch.zeros(L, 3, N, dtype=torch.bool)
+    for b in range(B):
+        sl = slice(b * N, (b + 1) * N)
+        for e in range(2):
+            u = int(ends[b, e])
+            if u < 0:
+                continue
+            touched[:, int(dsts[b]), u] = True
+            for l in range(L):
+                want = O.closed_commit(np32(temporal[l, int(slots[b])]).transpose(0, 2, 1), np32(keys[l, :, sl]),
+                                       np32(vals[l, :, sl]), np32(gains[l, :, sl]), idx[b].tolist(), u=u,
+                                       anc=anc[b].numpy())
+                assert rel_l2(np32(got[l, int(dsts[b]), u]).transpose(0, 2, 1), want) <= 1e-5
+    assert torch.all(got[~touched] == sentinel)
+
+
+def test_closed_commit_dropin(cuda):
+    """tree_kernels.closed_commit: states [L, H, DK, DV] (k-major), path src
+    with the last index n on the device, in place."""
+    from dforktree_amd import synth, tree_kernels as TK
+    announce("closed_commit drop-in")
+    L, H, N = 3, 4, 32
+    g = torch.Generator().manual_seed(8)
+    par = synth.tree_parents(N, "random", g)
+    path = synth.accepted_path(par, 16, g)
+    keys, vals, gains = _aux(9, L, H, N)
+    S = torch.randn(L, H, 128, 128) * 0.02
+    Sg = S.to(cuda)
+    src = torch.zeros(16, dtype=torch.int64)
+    src[:len(path)] = path
+    n = torch.tensor([len(path) - 1], dtype=torch.int32)
+    TK.closed_commit(Sg, keys.to(cuda), vals.to(cuda), gains.to(cuda), src.to(cuda), n.to(cuda))
+    torch.cuda.synchronize()
+    for l in range(L):
+        want = O.closed_commit(np32(S[l]), np32(keys[l]), np32(vals[l]), np32(gains[l]), path.tolist())
+        assert rel_l2(np32(Sg[l]), want) <= 1e-5

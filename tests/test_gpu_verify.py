@@ -1,0 +1,181 @@
+"""GPU parity of the fused tree verify against the CPU oracle.
+
+Tolerances (stated for this path): node outputs and WY values within
+rel-L2 <= 2e-3 of the fp32 recurrence, bf16 outputs within max-abs <= 1e-2;
+the saved ancestry-derived gains G and the normalised keys within 1e-5.
+"""
+import numpy as np
+import pytest
+import torch
+
+from conftest import MAX_ABS_BF16, REL_L2, announce, max_abs, rel_l2
+from _ref import np32, oracle_recurrent, oracle_verify, request_slices
+from oracle import gdn_tree as O
+
+pytestmark = pytest.mark.gpu
+
+
+def run_gpu(batch, dev, use_bits=False, o_dtype=torch.bfloat16, packed=None, state_indices=None, state=None):
+    from dforktree_amd import ops
+    g = batch.to(dev)
+    rows = g.y.shape[0]
+    uniform = len(set(batch.sizes)) == 1
+    packed = (not uniform) if packed is None else packed
+    aux_k = torch.zeros(batch.hv, rows, 128, device=dev)
+    aux_v = torch.zeros(batch.hv, rows, 128, device=dev)
+    aux_g = torch.zeros(batch.hv, rows, device=dev)
+    st = (g.state if state is None else state).transpose(-1, -2)
+    kw = dict(hk=batch.hk, hv=batch.hv, o_dtype=o_dtype, aux_k=aux_k, aux_v=aux_v, aux_g=aux_g,
+              state_indices=state_indices)
+    if packed:
+        kw.update(cu_seqlens=g.cu_seqlens, n_nodes=batch.n_max, batch=batch.batch)
+    else:
+        kw.update(batch=batch.batch, n_nodes=batch.sizes[0])
+    if use_bits or packed:
+        ts = ops.tree_struct(g.parent, 4, cu_seqlens=g.cu_seqlens, n_nodes=batch.n_max, batch=batch.batch,
+                             want=("anc_bits",))
+        kw["anc_bits"] = ts["anc_bits"]
+    else:
+        anc = torch.stack([torch.from_numpy(O.tree_struct(p)[0]) for p in
+                           [batch.parent[s].numpy() for s in request_slices(batch)]]).to(dev)
+        kw["anc"] = anc
+    o = ops.tree_verify(g.y, g.a, g.b, g.A_log, g.dt_bias, st, **kw)
+    torch.cuda.synchronize()
+    return o, aux_k, aux_v, aux_g
+
+
+def check_against_oracle(batch, o, aux_k, aux_v, aux_g, o_bf16=True):
+    ref = oracle_verify(batch)
+    o, aux_k, aux_v, aux_g = (np32(t) for t in (o, aux_k, aux_v, aux_g))
+    for r, sl in enumerate(request_slices(batch)):
+        want_o = O.bf16_round(ref[r]["o"]) if o_bf16 else ref[r]["o"]
+        assert rel_l2(o[sl], want_o) <= REL_L2, f"request {r}: o rel-L2 {rel_l2(o[sl], want_o):.3e}"
+        if o_bf16:
+            assert max_abs(o[sl], want_o) <= MAX_ABS_BF16
+        assert rel_l2(aux_v[:, sl], ref[r]["vn"]) <= REL_L2, f"request {r}: vn"
+        assert rel_l2(aux_k[:, sl], ref[r]["k"]) <= 1e-5, f"request {r}: k"
+        assert rel_l2(aux_g[:, sl], ref[r]["G"]) <= 1e-5, f"request {r}: G"
+
+
+@pytest.mark.parametrize("n,kind", [(32, "random"), (32, "chain"), (32, "bushy"), (16, "random"), (1, "random"),
+                                    (20, "random"), (64, "random"), (64, "chain"), (48, "bushy"), (33, "random")])
+def test_verify_single_request(cuda, n, kind):
+    announce(f"verify single n={n} kind={kind}")
+    batch = __import__("dforktree_amd.synth", fromlist=["x"]).make_batch(11, 0, [n], hk=2, hv=4, kinds=kind)
+    check_against_oracle(batch, *run_gpu(batch, cuda))
+
+
+def test_verify_config0_full_width(cuda):
+    """Batch 1, 32 nodes, 16 q/k heads, 32 v heads, fp32 S0 -- and directly
+    against the fp64 node-by-node recurrence as well."""
+    from dforktree_amd import synth
+    announce("verify config0 full width")
+    batch = synth.make_batch(0, 0, [32], hk=16, hv=32)
+    o, k, v, g = run_gpu(batch, cuda)
+    check_against_oracle(batch, o, k, v, g)
+    f = oracle_recurrent(batch, 0)
+    assert rel_l2(np32(o), f["o"]) <= REL_L2
+    assert rel_l2(np32(v), f["vn"]) <= REL_L2
+
+
+def test_verify_fp32_output_tighter(cuda):
+    """With fp32 outputs the hi/lo split keeps the result far inside the tolerance."""
+    from dforktree_amd import synth
+    announce("verify fp32 out")
+    batch = synth.make_batch(5, 0, [32], hk=2, hv=4)
+    o, k, v, g = run_gpu(batch, cuda, o_dtype=torch.float32)
+    ref = oracle_verify(batch)[0]
+    assert rel_l2(np32(o), ref["o"]) <= 5e-5
+    assert rel_l2(np32(v), ref["vn"]) <= 5e-5
+
+
+def test_verify_batched_uniform_bits(cuda):
+    from dforktree_amd import synth
+    announce("verify batched uniform anc_bits")
+    batch = synth.make_batch(1, 0, [32] * 6, hk=2, hv=4, kinds=["random", "chain", "bushy"] * 2)
+    check_against_oracle(batch, *run_gpu(batch, cuda, use_bits=True))
+
+
+def test_verify_packed_ragged(cuda):
+    """Packed varlen rows with cu_seqlens, sizes 1..64, the 64-wide path."""
+    from dforktree_amd import synth
+    announce("verify packed ragged")
+    sizes, kinds = [8, 64, 17, 1, 33, 64, 40, 9], ["chain", "random", "bushy", "random", "chain", "bushy",
+                                                 "random", "chain"]
+    batch = synth.make_batch(3, 0, sizes, hk=2, hv=4, kinds=kinds)
+    check_against_oracle(batch, *run_gpu(batch, cuda, packed=True))
+
+
+def test_verify_state_indices(cuda):
+    """Slots are read on the device: permuted slots, and -1 clamps to slot 0."""
+    from dforktree_amd import synth
+    announce("verify state_indices")
+    batch = synth.make_batch(4, 0, [32] * 3, hk=2, hv=4)
+    pool = torch.randn(5, 4, 128, 128) * 0.02
+    slots = torch.tensor([3, -1, 4], dtype=torch.int32)
+    batch.state = pool[slots.clamp(min=0).long()]
+    o, k, v, g = run_gpu(batch, cuda, state=pool.to(cuda), state_indices=slots.to(cuda))
+    check_against_oracle(batch, o, k, v, g)
+
+
+def test_tree_gdn_split_dropin(cuda):
+    """tree_kernels.tree_gdn_split with the plugin's argument forms: pool view,
+    slot on device, cached neg_exp_A, aux buffers [Hv, N, D]."""
+    from dforktree_amd import synth, tree_kernels as TK
+    announce("tree_gdn_split drop-in")
+    batch = synth.make_batch(6, 0, [32], hk=2, hv=4)
+    anc = torch.from_numpy(O.tree_struct(batch.parent.numpy())[0])
+    pool = (torch.randn(3, 4, 128, 128) * 0.02)
+    batch.state = pool[2:3]
+    g = batch.to(cuda)
+    poolg = pool.to(cuda)
+    keys = torch.zeros(4, 32, 128, device=cuda)
+    vals = torch.zeros_like(keys)
+    gains = torch.zeros(4, 32, device=cuda)
+    neg = -g.A_log.exp()
+    o = TK.tree_gdn_split(g.y, g.a, g.b, g.A_log, g.dt_bias, poolg[0].transpose(-1, -2), anc.to(cuda), 2, 4, 128, 128,
+                          aux=(keys, vals, gains), neg_exp_A=neg,
+                          state_indices=torch.tensor([2], device=cuda, dtype=torch.int32),
+                          state_slot_stride=poolg.stride(0))
+    torch.cuda.synchronize()
+    assert o.shape == (32, 4, 128) and o.dtype == torch.bfloat16
+    check_against_oracle(batch, o, keys, vals, gains)
+    with pytest.raises(KeyError):
+        TK.tree_gdn_split(g.y[:20], g.a[:20], g.b[:20], g.A_log, g.dt_bias, poolg[0].transpose(-1, -2),
+                          anc[:20, :20].to(cuda), 2, 4, 128, 128)
+
+
+def test_tree_gdn_fused_dropin(cuda):
+    """tree_gdn_fused returns fp32 and, for N > 32, delegates to the split path."""
+    from dforktree_amd import synth, tree_kernels as TK
+    announce("tree_gdn_fused drop-in")
+    for n in (24, 64):
+        batch = synth.make_batch(7, 0, [n], hk=2, hv=4)
+        anc = torch.from_numpy(O.tree_struct(batch.parent.numpy())[0]).to(cuda)
+        g = batch.to(cuda)
+        o = TK.tree_gdn_fused(g.y, g.a, g.b, g.A_log, g.dt_bias, g.state[0].transpose(-1, -2), anc, 2, 4, 128, 128)
+        torch.cuda.synchronize()
+        ref = oracle_verify(batch)[0]
+        if n <= 32:
+            assert o.dtype == torch.float32
+            assert rel_l2(np32(o), ref["o"]) <= 5e-5
+        else:
+            assert o.dtype == torch.bfloat16
+            assert rel_l2(np32(o), O.bf16_round(ref["o"])) <= REL_L2
+
+
+def test_block_inverse_dropin(cuda):
+    from dforktree_amd import fc1_block_inverse as FBI
+    import scipy.linalg
+    announce("block inverse")
+    rng = np.random.default_rng(0)
+    for n, inv in ((16, FBI.invert16), (32, FBI.invert32), (64, FBI.invert64)):
+        A = np.tril(rng.standard_normal((8, n, n)).astype(np.float32) * 0.2, -1)
+        X = torch.from_numpy(A + np.triu(np.ones((n, n), np.float32), 0)[None] * 7.0).to(cuda)  # junk above
+        inv[8,](X, n, num_warps=4, num_stages=1)
+        torch.cuda.synchronize()
+        Xh = X.cpu().numpy()
+        for m in range(8):
+            want = scipy.linalg.solve_triangular(np.eye(n) + A[m], np.eye(n), lower=True)
+            assert np.abs(Xh[m] - want).max() <= 1e-5
+            assert np.all(np.triu(Xh[m], 1) == 0)
