@@ -1,0 +1,260 @@
+"""Benchmark of the GDN tree-verify hot path on one MI355X.
+
+Workload (the state-bandwidth-bound stacked step): 24 GDN layers, batch 64,
+one random recursive 32-node tree per request, 16 q/k heads, 32 v heads,
+dk = dv = 128, a distinct fp32 2 MiB state per request per layer (3 GiB).
+One step = the tree verify of all 24 layers (one launch per layer, as the
+model runs them) followed by the closed-form in-place commit of every
+request's accepted root-to-node path (length 1-16) for all 24 layers (one
+launch).  Inputs are resident in HBM before timing starts.
+
+Printed: one JSON line.  ``value`` = verified nodes / s / layer
+= batch * nodes / (step time / 24).  ``roofline`` is for the kernel with the
+most time per step, from HIP-event timing of that kernel alone;
+``cpu_baseline`` times the CPU oracle (numpy, the fp32 restatement of the
+reference recurrence) on one layer of the same workload.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, vendor figure
+B, L, N, HK, HV, D = 64, 24, 32, 16, 32, 128
+MAX_PATH = 16
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--eager", action="store_true", help="time eager launches instead of a HIP graph")
+    return ap.parse_args()
+
+
+class Workload:
+    """Device buffers of the stacked step; every tensor preallocated."""
+
+    def __init__(self, dev, seed=2):
+        import torch
+        from dforktree_amd import ops, synth
+        C = 2 * HK * D + HV * D
+        rows = B * N
+        self.rows = rows
+        self.y = synth.device_randn_(torch.empty(L, rows, C, device=dev, dtype=torch.bfloat16), seed)
+        self.a = synth.device_randn_(torch.empty(L, rows, HV, device=dev, dtype=torch.bfloat16), seed + 1)
+        self.b = synth.device_randn_(torch.empty(L, rows, HV, device=dev, dtype=torch.bfloat16), seed + 2)
+        self.A_log = torch.full((HV,), -0.6931471805599453, device=dev)
+        self.dt_bias = torch.zeros(HV, device=dev)
+        self.neg = -self.A_log.exp()
+        # pool layout [layer, slot, head, V, K]
+        self.state = synth.device_randn_(torch.empty(L, B, HV, D, D, device=dev), seed + 3, std=0.02)
+        g = torch.Generator().manual_seed(seed)
+        parents = [synth.tree_parents(N, "random", g) for _ in range(B)]
+        paths = [synth.accepted_path(p, MAX_PATH, g) for p in parents]
+        self.path_lens = [len(p) for p in paths]
+        idx = torch.full((B, MAX_PATH), -1, dtype=torch.int32)
+        for i, p in enumerate(paths):
+            idx[i, :len(p)] = p
+        self.accept = idx.to(dev)
+        self.parent = torch.cat(parents).to(dev)
+        self.anc_bits = ops.tree_struct(self.parent, 4, batch=B, n_nodes=N, want=("anc_bits",))["anc_bits"]
+        self.o = torch.empty(L, rows, HV, D, device=dev, dtype=torch.bfloat16)
+        self.keys = torch.empty(L, HK, rows, D, device=dev)   # one key set per k-head
+        self.vals = torch.empty(L, HV, rows, D, device=dev)
+        self.gains = torch.empty(L, HV, rows, device=dev)
+
+    def verify(self, l):
+        from dforktree_amd import ops
+        ops.tree_verify(self.y[l], self.a[l], self.b[l], self.A_log, self.dt_bias, self.state[l].transpose(-1, -2),
+                        hk=HK, hv=HV, anc_bits=self.anc_bits, batch=B, n_nodes=N, neg_exp_A=self.neg, o=self.o[l],
+                        aux_k=self.keys[l], aux_v=self.vals[l], aux_g=self.gains[l], aux_k_per_khead=True)
+
+    def commit(self):
+        from dforktree_amd import ops
+        ops.tree_commit(self.state, self.keys, self.vals, self.gains, self.accept, n_nodes=N, k_head_div=HV // HK)
+
+    def step(self):
+        for l in range(L):
+            self.verify(l)
+        self.commit()
+
+    # ---- algorithmic bytes: every mandatory tensor touched once
+    def verify_bytes_per_launch(self):
+        C = 2 * HK * D + HV * D
+        per_req = (HV * D * D * 4          # S0 read
+                   + N * C * 2             # y = [q|k|v] bf16 read
+                   + 2 * N * HV * 2        # a, b bf16 read
+                   + N * 8                 # ancestor bit masks
+                   + N * HV * D * 2        # o bf16 write
+                   + HV * N * D * 4        # vn fp32 write
+                   + HV * N * 4            # G write
+                   + HK * N * D * 4)       # normalised k fp32 write (per k-head)
+        return B * per_req
+
+    def commit_bytes_per_launch(self):
+        tot = 0
+        for ell in self.path_lens:
+            tot += (2 * HV * D * D * 4           # state read + write
+                    + ell * (HK + HV) * D * 4    # path keys (per k-head) and values
+                    + (ell + 1) * HV * 4         # path and end gains
+                    + MAX_PATH * 4)              # path indices
+        return L * tot
+
+    def state_bytes_per_step(self):
+        return L * B * 3 * HV * D * D * 4   # verify read + commit read and write
+
+
+def time_graph(fn, reps, warmup, eager=False):
+    """ms per call of fn (a sequence of launches), HIP events on the current stream."""
+    import torch
+    if eager:
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / reps
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fn()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fn()
+    for _ in range(warmup):
+        g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / reps
+
+
+def cpu_baseline(seconds):
+    """The CPU oracle on one layer of the workload (64 requests x 32 nodes,
+    verify + commit of each accepted path), repeated for ~`seconds`."""
+    import numpy as np
+    import torch
+    from dforktree_amd import synth
+    from oracle import gdn_tree as O
+    try:
+        from threadpoolctl import threadpool_info
+        threads = max([i.get("num_threads", 1) for i in threadpool_info() if i.get("internal_api") == "openblas"]
+                      or [1])
+    except Exception:  # threadpoolctl missing: report the env setting
+        threads = int(os.environ.get("OMP_NUM_THREADS", "1"))
+    bt = synth.make_batch(2, 0, [N] * B, hk=HK, hv=HV)
+    y = bt.y.float().numpy().reshape(B, N, -1)
+    a = bt.a.numpy().reshape(B, N, -1)
+    b = bt.b.numpy().reshape(B, N, -1)
+    S0 = np.ascontiguousarray(bt.state.numpy().transpose(0, 1, 3, 2))
+    par = bt.parent.numpy().reshape(B, N)
+    g = torch.Generator().manual_seed(3)
+    paths = [synth.accepted_path(torch.from_numpy(p), MAX_PATH, g).tolist() for p in par]
+
+    def layer():
+        anc = np.stack([O.tree_struct(p)[0] for p in par])
+        r = O.tree_gdn_split(y, a, b, bt.A_log.numpy(), bt.dt_bias.numpy(), S0, anc, HK, HV, D, D)
+        for i in range(B):
+            O.closed_commit(S0[i], r["k"][i], r["vn"][i], r["G"][i], paths[i])
+
+    layer()  # warm-up
+    times = []
+    t_end = time.perf_counter() + seconds
+    while time.perf_counter() < t_end or len(times) < 3:
+        t0 = time.perf_counter()
+        layer()
+        times.append(time.perf_counter() - t0)
+    t = float(np.median(times))
+    return {"value": B * N / t, "unit": "nodes/s/layer", "cores": threads, "kind": "port",
+            "sample": f"{len(times)} x one layer of the workload ({B} requests x {N} nodes, verify + "
+                      f"commit of the accepted paths) through the numpy fp32 oracle, median {t * 1e3:.0f} ms"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported (every rank would run an "
+              f"independent copy of this single-GPU path; see the sharding notes in DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    dev = torch.device("cuda:0")
+    w = Workload(dev)
+    torch.cuda.synchronize()
+
+    reps_kernel = max(args.steps, 10)
+    t_verify_layers = time_graph(lambda: [w.verify(l) for l in range(L)], reps_kernel, args.warmup, args.eager)
+    t_verify = t_verify_layers / L
+    t_commit = time_graph(w.commit, reps_kernel, args.warmup, args.eager)
+    t_step = time_graph(w.step, args.steps, args.warmup, args.eager)
+
+    vb, cb = w.verify_bytes_per_launch(), w.commit_bytes_per_launch()
+    kernels = {
+        "tree_verify_kernel": dict(ms=t_verify, bytes=vb, per_step=L),
+        "tree_commit_kernel": dict(ms=t_commit, bytes=cb, per_step=1),
+    }
+    dom = max(kernels, key=lambda k: kernels[k]["ms"] * kernels[k]["per_step"])
+    kd = kernels[dom]
+    achieved = kd["bytes"] / (kd["ms"] * 1e-3) / 1e9
+    traffic = None
+    prof = ROOT / "profiles" / "hbm_traffic.json"
+    if prof.exists():
+        try:
+            traffic = json.loads(prof.read_text()).get(dom, {}).get("traffic_bytes_per_launch")
+        except (ValueError, OSError):
+            traffic = None
+    value = B * N / (t_step * 1e-3 / L)
+    state_gbs = w.state_bytes_per_step() / ((L * t_verify + t_commit) * 1e-3) / 1e9
+    out = {
+        "metric": "GDN tree-verify nodes/sec/layer (bs64, 32-node tree) + % HBM peak",
+        "value": round(value, 1),
+        "unit": "nodes/s/layer",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(t_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": "stacked GDN tree verify + accepted-path commit", "batch": B, "nodes": N,
+                   "layers": L, "qk_heads": HK, "v_heads": HV, "dk": D, "dv": D, "tree": "random recursive",
+                   "accepted_path": "random walk, length 1-16", "timing": "eager" if args.eager else "hip graph"},
+        "roofline": {"kernel": dom, "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "algorithmic_bytes_per_launch": kd["bytes"]},
+        "verify_us_per_layer": round(t_verify * 1e3, 2),
+        "verify_hbm_frac": round(vb / (t_verify * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "commit_ms": round(t_commit, 4),
+        "commit_hbm_frac": round(cb / (t_commit * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "state_traffic_hbm_frac": round(state_gbs / HBM_PEAK_GBS, 4),
+        "verify_only_nodes_per_s_per_layer": round(B * N / (t_verify * 1e-3), 1),
+    }
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()
