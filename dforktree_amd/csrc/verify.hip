@@ -84,6 +84,16 @@ __device__ __forceinline__ void update_block32(float (&y)[32], const float (&x)[
   }
 }
 
+// Forces x to be computed here: without a use at this point the compiler may
+// sink pure register arithmetic below a following barrier while the loads it
+// consumes stay above it, leaving every loaded operand live at once.
+__device__ __forceinline__ void materialize32(const float (&x)[32]) {
+#pragma unroll
+  for (int i = 0; i < 32; i += 8)
+    asm volatile("" ::"v"(x[i]), "v"(x[i + 1]), "v"(x[i + 2]), "v"(x[i + 3]), "v"(x[i + 4]), "v"(x[i + 5]),
+                 "v"(x[i + 6]), "v"(x[i + 7]));
+}
+
 // 8 bf16 of one LDS row as two 8-byte halves at columns c0 and c0 + 16
 __device__ __forceinline__ bf16x8 lds_bf16x8_split(const uint16_t* row, int c0) {
   const uint2 lo = *reinterpret_cast<const uint2*>(row + c0);
@@ -93,7 +103,7 @@ __device__ __forceinline__ bf16x8 lds_bf16x8_split(const uint16_t* row, int c0) 
 }
 
 template <int NP>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NP == 32 ? 3 : 1))) tree_verify_kernel(const VerifyParams P) {
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NP == 32 ? 4 : 1))) tree_verify_kernel(const VerifyParams P) {
   constexpr int MT = NP / 16;  // 16-node tiles
   constexpr int LDA = VerifySmem<NP>::LDA;
   const dft_verify_args& p = P.a;
@@ -352,9 +362,11 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NP == 
   rhs(x0, 0);
   if constexpr (NP == 64) rhs(x1, 32);
   solve_block32<LDA>(x0, sm.at, 0);
+  materialize32(x0);
   if constexpr (NP == 64) {
     update_block32<LDA>(x1, x0, sm.at, 0, 32);
     solve_block32<LDA>(x1, sm.at, 32);
+    materialize32(x1);
   }
   __syncthreads();  // every lane has read its Ck column
   auto save = [&](const float (&x)[32], int base) {
@@ -443,9 +455,11 @@ __global__ void __launch_bounds__(64) block_inverse_kernel(float* x, int n, int6
     c1[i] = (i + 32 == lane) ? 1.f : 0.f;
   }
   solve_block32<LD>(c0, at, 0);
+  materialize32(c0);
   if constexpr (NP == 64) {
     update_block32<LD>(c1, c0, at, 0, 32);
     solve_block32<LD>(c1, at, 32);
+    materialize32(c1);
   }
   __syncthreads();
   if (lane < n) {

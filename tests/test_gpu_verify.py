@@ -179,3 +179,18 @@ def test_block_inverse_dropin(cuda):
             want = scipy.linalg.solve_triangular(np.eye(n) + A[m], np.eye(n), lower=True)
             assert np.abs(Xh[m] - want).max() <= 1e-5
             assert np.all(np.triu(Xh[m], 1) == 0)
+
+
+@pytest.mark.parametrize("sizes_kind", ["uniform32", "ragged64"])
+def test_verify_persistent_loop_many_heads(cuda, sizes_kind):
+    """More (request, head) items than resident workgroups, so every
+    workgroup runs the multi-head pipeline (prefetch of the next head)."""
+    from dforktree_amd import synth
+    announce(f"verify persistent loop {sizes_kind}")
+    if sizes_kind == "uniform32":
+        sizes = [32] * 40          # 40 x 32 heads = 1280 items (> 4 per CU x 256 CUs)
+        kinds = ["random", "chain", "bushy", "random"] * 10
+    else:
+        sizes, kinds = synth.ragged_sizes(12, 8, 64, seed=3)  # 384 items (> 1 per CU x 256)
+    batch = synth.make_batch(9, 0, sizes, hk=16, hv=32, kinds=kinds)
+    check_against_oracle(batch, *run_gpu(batch, cuda, packed=(sizes_kind != "uniform32")))
