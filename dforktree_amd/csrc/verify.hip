@@ -2,27 +2,30 @@
 // (request, v-head) does prepare + (I+A)^-1 + finish of
 // tree_kernels.py:135-208 in a single pass over the recurrent state.
 //
-// Math (per head; q_n, k_n normalised, rq/rk the row scales, so that
-// q_n = rq * q_raw and k_n = rk * k_raw with q_raw/k_raw exact bf16):
+// Math (per head; q_n = rq q_raw, k_n = rk k_raw with q_raw/k_raw the exact
+// bf16 rows, so every MFMA left operand on the state is exact):
 //   G_i   = sum_{j anc-or-self i} g_j
 //   A_ij  = [j strict anc i] beta_i (k_n,i . k_n,j) e^{G_i - G_j}
+//   Pq_ij = [j anc-or-self i] (q_n,i . k_n,j) e^{G_i - G_j}
+//   X     = (I + A)^-1,   M = Pq X
 //   Cq    = q_raw S0,  Ck = k_raw S0                   (bf16 MFMA, S0 split hi+lo)
-//   (I+A) vn = diag(beta) (v - diag(e^G rk) Ck)        (= X(beta v) - X(beta e^G k) S0, :182-186)
-//   o     = diag(e^G rq) Cq + Pq vn,  Pq_ij = [j anc-or-self i] (q_n,i . k_n,j) e^{G_i-G_j}
+//   W     = diag(beta) (v - diag(e^G rk) Ck)
+//   vn    = X W  (= X(beta v) - X(beta e^G k) S0 of :182-186)
+//   o     = diag(e^G rq) Cq + M W  (= (e^G q) S0 + Pq vn of :190)
 //
-// Work split: wave w owns the 32 value columns [32w, 32w+32).
-//  * The 64 KiB state is streamed once, straight into MFMA B operands of
-//    v_mfma_f32_16x16x32_bf16: lane (n = l%16, g = l/16) loads 16 bytes at
-//    k = 16j + 4g of state row n, so the 4 lanes of a row cover a whole 64-byte
-//    sector per instruction.  The contraction order over k is chosen to match
-//    (a permutation of k applied to both operands).  Only S0 needs the hi/lo
-//    split: the left operands are the exact raw bf16 q/k rows.
-//  * The triangular solve runs with one lane per value column holding the
-//    whole column in registers (forward substitution, no cross-lane traffic,
-//    a dependency chain of N steps); the ancestor structure only enters
-//    through A.  X = (I+A)^-1 is never formed.
-//  * o accumulates in the 16x16 accumulator layout of phase 2 (fp32 MFMA for
-//    Pq vn), so Cq never leaves registers.
+// Phases:
+//  0. the 64 KiB state tile streams straight into MFMA B operands of
+//     v_mfma_f32_16x16x32_bf16 (lane (n = l%16, g = l/16) loads 16 bytes at
+//     k = 16j + 4g of state row n: the 4 lanes of a row cover a 64-byte
+//     sector per instruction); q/k/v rows, gates and ancestry go to LDS.
+//  1. while the state is in flight: norms, G, the Gram tiles (A, Pq), the
+//     blocked inverse X (16x16 diagonal blocks by forward substitution,
+//     off-diagonal blocks X_ij = -D_i sum_m A_im X_mj by fp32 MFMA) and M.
+//  2. Cq, Ck on the wave's 32 value columns.
+//  3. [X; M] W as one bf16x3 MFMA product (hi*hi + hi*lo + lo*hi) whose B
+//     operand is W in the accumulator layout of phase 2, read with the node
+//     permutation that layout implies: nothing is transposed or staged.
+// Every wave streams its own columns; LDS holds only per-head O(N^2) data.
 #include "dft_device.h"
 
 namespace dft {
@@ -39,18 +42,12 @@ struct VerifyParams {
 template <int NP>
 struct VerifySmem {
   static constexpr int LDA = NP + 4;  // fp32 row pitch, rows 16-byte aligned
-  union {
-    struct {
-      uint16_t q[NP * kQS];
-      uint16_t k[NP * kQS];
-    } qk;                    // raw q/k rows (phases 1-2)
-    float ct[4][32 * LDA];   // per wave: Ck, then vn, transposed to [column][node]
-  } u;
-  uint16_t v[NP * kQS];
-  float cqs[NP == 64 ? 4 * 32 * LDA : 1];  // 64-node trees: Cq parked across the solve
-  float at[NP * LDA];  // at[m][i] = A[i][m]
-  float pq[NP * LDA];  // pq[i][m]
-  float g[NP], G[NP], eG[NP], beta[NP], rq[NP], rk[NP];
+  uint16_t q[NP * kQS], k[NP * kQS], v[NP * kQS];
+  float am[NP * LDA];  // at[m][i] = A[i][m] until X is formed, then M[i][j]
+  float pq[NP * LDA];  // Pq[i][j]
+  float x[NP * LDA];   // X[i][j]
+  float gc[NP];        // g, then e^G rk once G is formed
+  float G[NP], beta[NP], rq[NP], rk[NP], cO[NP];
   uint64_t anc[NP];
 };
 
@@ -102,9 +99,68 @@ __device__ __forceinline__ bf16x8 lds_bf16x8_split(const uint16_t* row, int c0) 
   return __builtin_bit_cast(bf16x8, w);
 }
 
+// 8 fp32 of one LDS row at columns c0..c0+3 and c0+16..c0+19
+__device__ __forceinline__ void lds_f32x8_split(const float* row, int c0, float (&out)[8]) {
+  const f32x4 lo = *reinterpret_cast<const f32x4*>(row + c0);
+  const f32x4 hi = *reinterpret_cast<const f32x4*>(row + c0 + 16);
+  out[0] = lo[0]; out[1] = lo[1]; out[2] = lo[2]; out[3] = lo[3];
+  out[4] = hi[0]; out[5] = hi[1]; out[6] = hi[2]; out[7] = hi[3];
+}
+
+// Forward substitution on one 16x16 unit-lower block: x <- (I + A_bb)^-1 e_j.
+template <int LDA>
+__device__ __forceinline__ void solve_block16(float (&x)[16], const float* at, int base) {
+#pragma unroll
+  for (int m = 0; m < 15; ++m) {
+    const float xm = x[m];
+#pragma unroll
+    for (int i = m + 1; i < 16; ++i) x[i] -= at[(base + m) * LDA + base + i] * xm;
+  }
+}
+
+__device__ __forceinline__ void materialize16(const float (&x)[16]) {
+  asm volatile("" ::"v"(x[0]), "v"(x[1]), "v"(x[2]), "v"(x[3]), "v"(x[4]), "v"(x[5]), "v"(x[6]), "v"(x[7]));
+  asm volatile("" ::"v"(x[8]), "v"(x[9]), "v"(x[10]), "v"(x[11]), "v"(x[12]), "v"(x[13]), "v"(x[14]), "v"(x[15]));
+}
+
+// acc += A_blk(bi, bm) * B_blk(bm, bj) over one 16x16x16 block product with
+// fp32 MFMA; A from a row-major or (transposed) column-major LDS matrix, B
+// row-major.  Lane (n, g), k-step s covers k = 4s + g.
+template <int LDA, bool A_TRANSPOSED>
+__device__ __forceinline__ f32x4 block_mma(f32x4 acc, const float* a, int bi, int bm, const float* bmat, int bj,
+                                           int n16, int g4) {
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    const int kk = 16 * bm + 4 * s + g4;
+    const float av = A_TRANSPOSED ? a[kk * LDA + 16 * bi + n16] : a[(16 * bi + n16) * LDA + kk];
+    const float bv = bmat[kk * LDA + 16 * bj + n16];
+    acc = mfma_f32_16x16x4(av, bv, acc);
+  }
+  return acc;
+}
+
+// X_ij = -D_i T for T in the accumulator layout (lane (n, g) holds rows
+// 4g + r): k-step s takes row 4g + s of T from register s, so T never leaves
+// registers; D_i = X_ii is read from LDS with the same permutation.
+template <int LDA>
+__device__ __forceinline__ f32x4 neg_diag_times(const float* x, int bi, f32x4 T, int n16, int g4) {
+  f32x4 acc = {};
+#pragma unroll
+  for (int s = 0; s < 4; ++s) acc = mfma_f32_16x16x4(x[(16 * bi + n16) * LDA + 16 * bi + 4 * g4 + s], T[s], acc);
+  return -acc;
+}
+
+template <int LDA>
+__device__ __forceinline__ void store_block(float* m, int bi, int bj, f32x4 acc, int n16, int g4) {
+#pragma unroll
+  for (int r = 0; r < 4; ++r) m[(16 * bi + 4 * g4 + r) * LDA + 16 * bj + n16] = acc[r];
+}
+
 template <int NP>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NP == 32 ? 4 : 1))) tree_verify_kernel(const VerifyParams P) {
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NP == 32 ? 4 : 1)))
+tree_verify_kernel(const VerifyParams P) {
   constexpr int MT = NP / 16;  // 16-node tiles
+  constexpr int KS = NP / 32;  // 32-node k-steps of phase 3
   constexpr int LDA = VerifySmem<NP>::LDA;
   const dft_verify_args& p = P.a;
   __shared__ VerifySmem<NP> sm;
@@ -149,15 +205,14 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NP == 
   }
   const float* S0 = p.state + slot * p.state_slot_stride + (int64_t)h * p.state_h_stride;
 
-  // ---- 1. state loads first.  s0r[t][j] holds S0[k = 16j + 4g + e][v = 32w + 16t + n]
+  // ---- 0. state loads first: s0r[t][j] = S0[k = 16j + 4g + e][v = 32w + 16t + n]
   f32x4 s0r[2][8];
   if (P.s0_vec) {
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
       const float* rowp = S0 + (int64_t)(32 * wave + 16 * t + n16) * p.state_v_stride + 4 * g4;
 #pragma unroll
-      for (int j = 0; j < 8; ++j)
-        s0r[t][j] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(rowp + 16 * j));
+      for (int j = 0; j < 8; ++j) s0r[t][j] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(rowp + 16 * j));
     }
   } else {
 #pragma unroll
@@ -173,8 +228,6 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NP == 
   const int KD = p.hk * kD;
   const int64_t ys = p.y_row_stride;
   const uint16_t* ybase = reinterpret_cast<const uint16_t*>(p.y) + row0 * ys;
-
-  // ---- 2. raw q/k/v rows to LDS (16-byte loads, rows >= n zero-filled)
   {
     const uint16_t* yq = ybase + hk * kD;
     const uint16_t* yk = yq + KD;
@@ -187,25 +240,23 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NP == 
         vk = *reinterpret_cast<const uint4*>(yk + i * ys + ch);
         vv = *reinterpret_cast<const uint4*>(yv + i * ys + ch);
       }
-      *reinterpret_cast<uint4*>(&sm.u.qk.q[i * kQS + ch]) = vq;
-      *reinterpret_cast<uint4*>(&sm.u.qk.k[i * kQS + ch]) = vk;
+      *reinterpret_cast<uint4*>(&sm.q[i * kQS + ch]) = vq;
+      *reinterpret_cast<uint4*>(&sm.k[i * kQS + ch]) = vk;
       *reinterpret_cast<uint4*>(&sm.v[i * kQS + ch]) = vv;
     }
   }
-  // ---- 3. gates and ancestry
   if (tid < NP) {
     const int i = tid;
     float gi = 0.f, bi = 0.f;
     if (i < n) {
-      const float a = ld_f(p.a, (row0 + i) * p.a_row_stride + h, p.a_dtype) +
-                      ld_f(p.dt_bias, h, p.dt_bias_dtype);
+      const float a = ld_f(p.a, (row0 + i) * p.a_row_stride + h, p.a_dtype) + ld_f(p.dt_bias, h, p.dt_bias_dtype);
       const float sp = a > 20.f ? a : logf(1.f + expf(fminf(a, 20.f)));
       const float dec = p.neg_exp_A ? p.neg_exp_A[h] : -expf(ld_f(p.A_log, h, p.A_log_dtype));
       gi = dec * sp;
       const float bb = ld_f(p.b, (row0 + i) * p.b_row_stride + h, p.b_dtype);
       bi = 1.f / (1.f + expf(-bb));
     }
-    sm.g[i] = gi;
+    sm.gc[i] = gi;
     sm.beta[i] = bi;
     if (p.anc_bits) sm.anc[i] = i < n ? (p.anc_bits[row0 + i] & mask_upto(i) & mask_below(n)) : 0ull;
   }
@@ -219,9 +270,9 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NP == 
   }
   __syncthreads();
 
-  // ---- 4. row norms and path-cumulative decay
+  // ---- 1a. row norms and path-cumulative decay
   if (tid < 2 * NP) {
-    const uint16_t* rowp = (tid < NP ? sm.u.qk.q : sm.u.qk.k) + (tid % NP) * kQS;
+    const uint16_t* rowp = (tid < NP ? sm.q : sm.k) + (tid % NP) * kQS;
     float ss = 0.f;
 #pragma unroll
     for (int c = 0; c < kD; c += 8) {
@@ -242,20 +293,18 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NP == 
     float G = 0.f;
 #pragma unroll
     for (int j = 0; j < NP; ++j)
-      if ((bits >> j) & 1ull) G += sm.g[j];
+      if ((bits >> j) & 1ull) G += sm.gc[j];
     sm.G[i] = G;
-    sm.eG[i] = __expf(G);
   }
   __syncthreads();
 
-  // ---- 5. saves for the commit (normalised keys, G) and the Gram tiles:
-  // lower 16x16 tiles of k k^T (-> A, stored transposed) and q k^T (-> Pq)
+  // ---- 1b. saves for the commit, output row scales, Gram tiles
   const bool per_khead = (p.flags & DFT_VERIFY_AUX_K_PER_KHEAD) != 0;
   if (p.aux_k && (!per_khead || rr == 0)) {
     float* dk = p.aux_k + (int64_t)(per_khead ? hk : h) * p.aux_k_h_stride + row0 * p.aux_k_row_stride;
     for (int c = tid; c < n * 32; c += 256) {
       const int i = c >> 5, d = (c & 31) * 4;
-      const uint2 u = *reinterpret_cast<const uint2*>(&sm.u.qk.k[i * kQS + d]);
+      const uint2 u = *reinterpret_cast<const uint2*>(&sm.k[i * kQS + d]);
       const float r = sm.rk[i];
       const f32x4 val = {__uint_as_float(u.x << 16) * r, __uint_as_float(u.x & 0xffff0000u) * r,
                          __uint_as_float(u.y << 16) * r, __uint_as_float(u.y & 0xffff0000u) * r};
@@ -268,7 +317,12 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NP == 
       }
     }
   }
-  if (p.aux_g && tid < n) p.aux_g[(int64_t)h * p.aux_g_h_stride + (row0 + tid) * p.aux_g_row_stride] = sm.G[tid];
+  if (tid < NP) {
+    const float eG = __expf(sm.G[tid]);
+    sm.gc[tid] = eG * sm.rk[tid];  // g is no longer needed
+    sm.cO[tid] = eG * sm.rq[tid];
+    if (p.aux_g && tid < n) p.aux_g[(int64_t)h * p.aux_g_h_stride + (row0 + tid) * p.aux_g_row_stride] = sm.G[tid];
+  }
   {
     int item = 0;
 #pragma unroll
@@ -278,12 +332,12 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NP == 
 #pragma unroll
         for (int jt = 0; jt <= it; ++jt, ++item) {
           if ((item & 3) != wave) continue;
-          const uint16_t* left = which == 0 ? sm.u.qk.k : sm.u.qk.q;
+          const uint16_t* left = which == 0 ? sm.k : sm.q;
           f32x4 acc = {};
 #pragma unroll
           for (int s = 0; s < 4; ++s) {
             const bf16x8 av = *reinterpret_cast<const bf16x8*>(left + (16 * it + n16) * kQS + 32 * s + 8 * g4);
-            const bf16x8 bv = *reinterpret_cast<const bf16x8*>(sm.u.qk.k + (16 * jt + n16) * kQS + 32 * s + 8 * g4);
+            const bf16x8 bv = *reinterpret_cast<const bf16x8*>(sm.k + (16 * jt + n16) * kQS + 32 * s + 8 * g4);
             acc = mfma_bf16_16x16x32(av, bv, acc);
           }
           const int j = 16 * jt + n16;
@@ -292,17 +346,70 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NP == 
           for (int r = 0; r < 4; ++r) {
             const int i = 16 * it + 4 * g4 + r;
             const bool on = (sm.anc[i] >> j) & 1ull;
-            if (which == 0) {
-              sm.at[j * LDA + i] =
-                  (on && j < i) ? sm.beta[i] * sm.rk[i] * rkj * acc[r] * __expf(sm.G[i] - Gj) : 0.f;
-            } else {
+            if (which == 0)
+              sm.am[j * LDA + i] = (on && j < i) ? sm.beta[i] * sm.rk[i] * rkj * acc[r] * __expf(sm.G[i] - Gj) : 0.f;
+            else
               sm.pq[i * LDA + j] = on ? sm.rq[i] * rkj * acc[r] * __expf(sm.G[i] - Gj) : 0.f;
-            }
           }
         }
   }
+  __syncthreads();
 
-  // ---- 6. Cq = q_raw S0, Ck = k_raw S0 for the wave's 32 columns.  k-step s,
+  // ---- 1c. diagonal blocks of X by forward substitution (wave 0, lane
+  // group b = block, lane j = column); the other waves zero X above the diagonal.
+  if (wave == 0) {
+    const int bb = g4, j = n16;
+    if (bb < MT) {
+      float xc[16];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) xc[i] = (i == j) ? 1.f : 0.f;
+      solve_block16<LDA>(xc, sm.am, 16 * bb);
+      materialize16(xc);
+#pragma unroll
+      for (int i = 0; i < 16; ++i) sm.x[(16 * bb + i) * LDA + 16 * bb + j] = xc[i];
+    }
+  } else {
+    for (int e = tid - 64; e < NP * NP; e += 192) {
+      const int i = e / NP, jj = e % NP;
+      if ((i >> 4) < (jj >> 4)) sm.x[i * LDA + jj] = 0.f;
+    }
+  }
+  __syncthreads();
+
+  // ---- 1d. off-diagonal blocks X_ij = -D_i sum_{m=j}^{i-1} A_im X_mj, by
+  // distance d = i - j (each level needs the previous ones)
+#pragma unroll
+  for (int d = 1; d < MT; ++d) {
+    const int bj = wave, bi = wave + d;
+    if (bi < MT) {
+      f32x4 T = {};
+#pragma unroll
+      for (int bm = 0; bm < MT; ++bm)
+        if (bm >= bj && bm < bi) T = block_mma<LDA, true>(T, sm.am, bi, bm, sm.x, bj, n16, g4);
+      store_block<LDA>(sm.x, bi, bj, neg_diag_times<LDA>(sm.x, bi, T, n16, g4), n16, g4);
+    }
+    __syncthreads();
+  }
+
+  // ---- 1e. M = Pq X (block lower triangular; overwrites A)
+  {
+    int blk = 0;
+#pragma unroll
+    for (int bi = 0; bi < MT; ++bi)
+#pragma unroll
+      for (int bj = 0; bj < MT; ++bj, ++blk) {
+        if ((blk & 3) != wave) continue;
+        f32x4 acc = {};
+        if (bj <= bi) {
+#pragma unroll
+          for (int bm = 0; bm < MT; ++bm)
+            if (bm >= bj && bm <= bi) acc = block_mma<LDA, false>(acc, sm.pq, bi, bm, sm.x, bj, n16, g4);
+        }
+        store_block<LDA>(sm.am, bi, bj, acc, n16, g4);
+      }
+  }
+
+  // ---- 2. Cq = q_raw S0, Ck = k_raw S0 for the wave's 32 columns.  k-step s,
   // lane group g, element e -> k = 32s + 4g + e (e < 4), 32s + 16 + 4g + e-4.
   f32x4 cq[MT][2], ck[MT][2];
 #pragma unroll
@@ -314,108 +421,84 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NP == 
     }
 #pragma unroll
   for (int s = 0; s < 4; ++s) {
+    bf16x8 bhi[2], blo[2];
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
-      const float x[8] = {s0r[t][2 * s][0],     s0r[t][2 * s][1],     s0r[t][2 * s][2],     s0r[t][2 * s][3],
-                          s0r[t][2 * s + 1][0], s0r[t][2 * s + 1][1], s0r[t][2 * s + 1][2], s0r[t][2 * s + 1][3]};
-      bf16x8 bhi, blo;
-      split_bf16x8(x, bhi, blo);
+      const float xs[8] = {s0r[t][2 * s][0],     s0r[t][2 * s][1],     s0r[t][2 * s][2],     s0r[t][2 * s][3],
+                           s0r[t][2 * s + 1][0], s0r[t][2 * s + 1][1], s0r[t][2 * s + 1][2], s0r[t][2 * s + 1][3]};
+      split_bf16x8(xs, bhi[t], blo[t]);
+    }
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
-        const int off = (16 * mt + n16) * kQS + 32 * s + 4 * g4;
-        const bf16x8 aq = lds_bf16x8_split(sm.u.qk.q, off);
-        const bf16x8 ak = lds_bf16x8_split(sm.u.qk.k, off);
-        cq[mt][t] = mfma_bf16_16x16x32(aq, bhi, cq[mt][t]);
-        ck[mt][t] = mfma_bf16_16x16x32(ak, bhi, ck[mt][t]);
-        cq[mt][t] = mfma_bf16_16x16x32(aq, blo, cq[mt][t]);
-        ck[mt][t] = mfma_bf16_16x16x32(ak, blo, ck[mt][t]);
+    for (int mt = 0; mt < MT; ++mt) {
+      const int off = (16 * mt + n16) * kQS + 32 * s + 4 * g4;
+      const bf16x8 aq = lds_bf16x8_split(sm.q, off);
+      const bf16x8 ak = lds_bf16x8_split(sm.k, off);
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        cq[mt][t] = mfma_bf16_16x16x32(aq, bhi[t], cq[mt][t]);
+        ck[mt][t] = mfma_bf16_16x16x32(ak, bhi[t], ck[mt][t]);
+        cq[mt][t] = mfma_bf16_16x16x32(aq, blo[t], cq[mt][t]);
+        ck[mt][t] = mfma_bf16_16x16x32(ak, blo[t], ck[mt][t]);
       }
     }
   }
-  __syncthreads();  // q/k reads done: the union now holds the transposed tiles
+  __syncthreads();  // X and M complete
 
-  // ---- 7. Ck to [column][node] in the wave's own slice
-  float* ct = sm.u.ct[wave];
+  // ---- 3. W = beta (v - e^G rk Ck) in the accumulator layout, split into
+  // bf16 hi/lo B operands: k-step ks, lane group g, element e -> node
+  // 32ks + 4g + e (e < 4), 32ks + 16 + 4g + e-4, i.e. registers of tiles 2ks, 2ks+1.
+  bf16x8 wh[KS][2], wl[KS][2];
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt)
+  for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
-      *reinterpret_cast<f32x4*>(&ct[(16 * t + n16) * LDA + 16 * mt + 4 * g4]) = ck[mt][t];
-      if constexpr (NP == 64)
-        *reinterpret_cast<f32x4*>(&sm.cqs[wave * 32 * LDA + (16 * t + n16) * LDA + 16 * mt + 4 * g4]) = cq[mt][t];
-    }
-  __syncthreads();
-
-  // ---- 8. (I + A) vn = diag(beta)(v - e^G rk Ck), lane = value column; both
-  // halves of the wave solve the same column (no cross-lane traffic).
-  const int c = lane & 31, hf = lane >> 5;
-  const int vcol = 32 * wave + c;
-  float x0[32], x1[32];  // nodes 0..31 and (NP = 64) 32..63
-  auto rhs = [&](float (&x)[32], int base) {
+      const int col = 32 * wave + 16 * t + n16;
+      float w8[8];
 #pragma unroll
-    for (int ii = 0; ii < 32; ++ii) {
-      const int i = base + ii;
-      const float vv = bf16_bits_to_f32(sm.v[i * kQS + vcol]);
-      x[ii] = sm.beta[i] * (vv - sm.eG[i] * sm.rk[i] * ct[c * LDA + i]);
-    }
-  };
-  rhs(x0, 0);
-  if constexpr (NP == 64) rhs(x1, 32);
-  solve_block32<LDA>(x0, sm.at, 0);
-  materialize32(x0);
-  if constexpr (NP == 64) {
-    update_block32<LDA>(x1, x0, sm.at, 0, 32);
-    solve_block32<LDA>(x1, sm.at, 32);
-    materialize32(x1);
-  }
-  __syncthreads();  // every lane has read its Ck column
-  auto save = [&](const float (&x)[32], int base) {
-    if (hf == 0) {
-#pragma unroll
-      for (int i = 0; i < 32; i += 4)
-        *reinterpret_cast<f32x4*>(&ct[c * LDA + base + i]) = f32x4{x[i], x[i + 1], x[i + 2], x[i + 3]};
-    }
-    if (p.aux_v) {
-      float* dv = p.aux_v + (int64_t)h * p.aux_v_h_stride + row0 * p.aux_v_row_stride + vcol;
-#pragma unroll
-      for (int i = 0; i < 32; i += 2) {
-        const int ii = base + i + hf;
-        if (ii < n) dv[ii * p.aux_v_row_stride] = hf ? x[i + 1] : x[i];
-      }
-    }
-  };
-  save(x0, 0);
-  if constexpr (NP == 64) save(x1, 32);
-  __syncthreads();
-
-  // ---- 9. o = e^G rq Cq + Pq vn in the 16x16 layout; Pq is lower triangular,
-  // so row tile mt needs nodes m < 16(mt+1) only.
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      f32x4 cqv = cq[mt][t];
-      if constexpr (NP == 64)
-        cqv = *reinterpret_cast<const f32x4*>(&sm.cqs[wave * 32 * LDA + (16 * t + n16) * LDA + 16 * mt + 4 * g4]);
-      f32x4 acc;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
+      for (int e = 0; e < 8; ++e) {
+        const int mt = 2 * ks + (e >> 2), r = e & 3;
         const int i = 16 * mt + 4 * g4 + r;
-        acc[r] = sm.eG[i] * sm.rq[i] * cqv[r];
+        const float vv = bf16_bits_to_f32(sm.v[i * kQS + col]);
+        w8[e] = sm.beta[i] * (vv - sm.gc[i] * ck[mt][t][r]);
       }
+      split_bf16x8(w8, wh[ks][t], wl[ks][t]);
+    }
+  // [X; M] W: tiles mo < MT give vn, tiles mo >= MT give M W.
 #pragma unroll
-      for (int s = 0; s < 4 * (mt + 1); ++s) {
-        const float a = sm.pq[(16 * mt + n16) * LDA + 4 * s + g4];
-        const float bv = ct[(16 * t + n16) * LDA + 4 * s + g4];
-        acc = mfma_f32_16x16x4(a, bv, acc);
+  for (int mo = 0; mo < 2 * MT; ++mo) {
+    const int mt = mo % MT;
+    const float* src = mo < MT ? sm.x : sm.am;
+    f32x4 acc[2] = {f32x4{}, f32x4{}};
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      if (32 * ks > 16 * mt + 15) continue;  // both factors are lower triangular
+      float a8[8];
+      lds_f32x8_split(src + (16 * mt + n16) * LDA, 32 * ks + 4 * g4, a8);
+      bf16x8 ah, al;
+      split_bf16x8(a8, ah, al);
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        acc[t] = mfma_bf16_16x16x32(ah, wh[ks][t], acc[t]);
+        acc[t] = mfma_bf16_16x16x32(ah, wl[ks][t], acc[t]);
+        acc[t] = mfma_bf16_16x16x32(al, wh[ks][t], acc[t]);
       }
+    }
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
       const int col = 32 * wave + 16 * t + n16;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int i = 16 * mt + 4 * g4 + r;
-        if (i < n) st_f(p.o, (row0 + i) * p.o_row_stride + (int64_t)h * p.o_h_stride + col, p.o_dtype, acc[r]);
+        if (i >= n) continue;
+        if (mo < MT) {
+          if (p.aux_v) p.aux_v[(int64_t)h * p.aux_v_h_stride + (row0 + i) * p.aux_v_row_stride + col] = acc[t][r];
+        } else {
+          st_f(p.o, (row0 + i) * p.o_row_stride + (int64_t)h * p.o_h_stride + col, p.o_dtype,
+               sm.cO[i] * cq[mt][t][r] + acc[t][r]);
+        }
       }
     }
+  }
 }
 
 int launch_tree_verify(const dft_verify_args* a, hipStream_t stream) {
