@@ -39,6 +39,8 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--eager", action="store_true", help="time eager launches instead of a HIP graph")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="also run a plain 1 GiB device copy (the reference point for HBM byte counters)")
     return ap.parse_args()
 
 
@@ -88,6 +90,29 @@ class Workload:
         for l in range(L):
             self.verify(l)
         self.commit()
+
+    def conv_setup(self, dev, seed=5):
+        """Front end of one layer: tree-parent conv1d (width 4, SiLU) over the
+        pre-conv tokens, writing the verify input and each node's window."""
+        import torch
+        from dforktree_amd import ops, synth
+        C = 2 * HK * D + HV * D
+        self.cx = synth.device_randn_(torch.empty(B, N, C, device=dev, dtype=torch.bfloat16), seed)
+        self.cw = synth.device_randn_(torch.empty(C, 4, device=dev, dtype=torch.bfloat16), seed + 1, std=0.1)
+        self.cs = torch.zeros(B, C, 3, device=dev, dtype=torch.bfloat16)
+        self.cidx = ops.tree_struct(self.parent, 4, batch=B, n_nodes=N, want=("cidx",),
+                                    index_dtype=torch.int32)["cidx"].view(B, N, 4)
+        self.cy = torch.empty(B, N, C, device=dev, dtype=torch.bfloat16)
+        self.ciw = torch.empty(B, N, C, 3, device=dev, dtype=torch.bfloat16)
+
+    def conv(self):
+        from dforktree_amd import ops
+        ops.tree_conv(self.cx, self.cs, self.cw, None, self.cidx, y=self.cy, iw=self.ciw)
+
+    def conv_bytes_per_launch(self):
+        C = 2 * HK * D + HV * D
+        # tokens read once (parents' rows are re-gathered from cache), output and window written
+        return B * (N * C * 2 + N * C * 2 + N * C * 3 * 2 + N * 4 * 4) + C * 4 * 2
 
     # ---- algorithmic bytes: every mandatory tensor touched once
     def verify_bytes_per_launch(self):
@@ -207,6 +232,15 @@ def main():
     t_verify = t_verify_layers / L
     t_commit = time_graph(w.commit, reps_kernel, args.warmup, args.eager)
     t_step = time_graph(w.step, args.steps, args.warmup, args.eager)
+    w.conv_setup(dev)
+    t_conv = time_graph(w.conv, reps_kernel, args.warmup, args.eager)
+    if args.copy_calibration:
+        src = torch.ones(1 << 28, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
 
     vb, cb = w.verify_bytes_per_launch(), w.commit_bytes_per_launch()
     kernels = {
@@ -250,6 +284,8 @@ def main():
         "commit_hbm_frac": round(cb / (t_commit * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
         "state_traffic_hbm_frac": round(state_gbs / HBM_PEAK_GBS, 4),
         "verify_only_nodes_per_s_per_layer": round(B * N / (t_verify * 1e-3), 1),
+        "conv_us_per_layer": round(t_conv * 1e3, 2),
+        "conv_hbm_frac": round(w.conv_bytes_per_launch() / (t_conv * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
     }
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
