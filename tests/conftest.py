@@ -25,7 +25,7 @@ def max_abs(a, b):
     return float(np.max(np.abs(np.asarray(a, np.float64) - np.asarray(b, np.float64)))) if np.size(a) else 0.0
 
 
-# tolerances stated by the task for this path
+# tolerances of this path
 REL_L2 = 2e-3      # node outputs and committed states vs the fp32 recurrence
 MAX_ABS_BF16 = 1e-2  # bf16 outputs
 
