@@ -132,3 +132,27 @@ def test_tree_conv_fused_dropin(cuda):
     ry, _ = O.tree_conv(np32(x[0]), np32(cs2), np32(w), np32(bias), cidx[0].numpy())
     assert y.shape == (N, C) and y.dtype == torch.bfloat16
     assert max_abs(np32(y), O.bf16_round(ry)) <= MAX_ABS_BF16
+
+
+@pytest.mark.parametrize("case", ["f32_weight", "odd_channels", "fp32_state"])
+def test_conv_general_layouts(cuda, case):
+    """Layouts outside the 16-byte bf16 fast path (fp32 weights, a channel
+    count that is not a multiple of 8) and an fp32 conv state on the fast
+    path: same results, window values rounded to the window's dtype."""
+    from dforktree_amd import ops
+    announce(f"conv general layout {case}")
+    B, N = 2, 32
+    C = 1003 if case == "odd_channels" else 1024
+    x, w, cs, cidx = _conv_inputs(4, B, N, C)
+    if case == "f32_weight":
+        w = w.float()
+    if case == "fp32_state":
+        cs = torch.randn(B, C, 3) * 0.5
+    iw = torch.zeros(B, N, C, 3, dtype=torch.bfloat16, device=cuda)
+    y = ops.tree_conv(x.to(cuda), cs.to(cuda), w.to(cuda), None, cidx.to(cuda), iw=iw)
+    torch.cuda.synchronize()
+    for b in range(B):
+        ry, rwin = O.tree_conv(np32(x[b]), np32(cs[b]), np32(w), None, cidx[b].numpy())
+        want = O.bf16_round(ry)
+        assert max_abs(np32(y[b]), want) <= MAX_ABS_BF16 and rel_l2(np32(y[b]), want) <= REL_L2
+        assert np.array_equal(np32(iw[b]), O.bf16_round(rwin))
