@@ -31,24 +31,61 @@
 namespace dft {
 
 constexpr int kD = 128;
-constexpr int kQS = kD + 8;  // LDS row stride (bf16) of q/k/v rows: 272 B
+// q/k/v rows in LDS: 256-byte rows of 16 chunks of 8 bf16, chunk c of row i
+// stored at position c ^ (i & 15).  The swizzle keeps the column reads of
+// 16 consecutive rows on distinct banks without padding, so a row group is
+// one contiguous 1 KiB block that a single global->LDS load fills.
+__device__ __forceinline__ int qkv_at(int i, int c) { return i * kD + ((((c >> 3) ^ i) & 15) << 3) + (c & 7); }
+
+// s_waitcnt immediate (gfx9 encoding): wait until at most vm vector-memory
+// and lgkm LDS/scalar operations of this wave are outstanding
+constexpr unsigned waitcnt_imm(int vm, int lgkm) {
+  return (unsigned)((vm & 15) | ((vm >> 4) << 14) | (7 << 4) | ((lgkm & 15) << 8));
+}
+
+// The aligned 32-bit word holding element i of a float tensor (F32, BF16 or
+// F16), and the shift of the element within it (16 for the upper half of a
+// 16-bit pair).  The word never leaves the element's page.
+__device__ __forceinline__ const uint32_t* word_of(const void* p, int64_t i, int dt, uint32_t& sh) {
+  const char* base = static_cast<const char*>(p);
+  const int mis = (int)(reinterpret_cast<uintptr_t>(base) & 3);
+  const int64_t off = i * (dt == DFT_F32 ? 4 : 2) + mis;
+  sh = (uint32_t)(off & 2) << 3;
+  return reinterpret_cast<const uint32_t*>(base + ((off & ~(int64_t)3) - mis));
+}
+__device__ __forceinline__ float word_to_f(uint32_t w, uint32_t sh, int dt) {
+  if (dt == DFT_F32) return __uint_as_float(w);
+  const uint32_t h = (w >> sh) & 0xffffu;
+  if (dt == DFT_BF16) return __uint_as_float(h << 16);
+  return __half2float(__ushort_as_half((unsigned short)h));
+}
+
+// global -> LDS copies that bypass registers: lane l's bytes land at
+// lds + l * size
+__device__ __forceinline__ void lds_dma16(const void* g, void* lds) {
+  __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)lds, 16, 0, 0);
+}
+__device__ __forceinline__ void lds_dma4(const void* g, void* lds) {
+  __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)lds, 4, 0, 0);
+}
 
 struct VerifyParams {
   dft_verify_args a;
-  int s0_vec;    // state rows 16-byte aligned with k stride 1
+  int s0_vec;    // state rows 16-byte aligned with k stride 1 (selects the kernel)
   int auxk_vec;  // aux_k rows 16-byte aligned
 };
 
 template <int NP>
 struct VerifySmem {
   static constexpr int LDA = NP + 4;  // fp32 row pitch, rows 16-byte aligned
-  uint16_t q[NP * kQS], k[NP * kQS], v[NP * kQS];
+  uint16_t q[NP * kD], k[NP * kD], v[NP * kD];
   float am[NP * LDA];  // at[m][i] = A[i][m] until X is formed, then M[i][j]
   float pq[NP * LDA];  // Pq[i][j]
   float x[NP * LDA];   // X[i][j]
   float gc[NP];        // g, then e^G rk once G is formed
   float G[NP], beta[NP], rq[NP], rk[NP], cO[NP];
   uint64_t anc[NP];
+  uint32_t graw[6][64];  // per lane of wave 0: words of a, b, ancestry bits lo / hi, dt_bias, decay
 };
 
 __device__ __forceinline__ f32x4 mfma_bf16_16x16x32(bf16x8 a, bf16x8 b, f32x4 c) {
@@ -91,10 +128,10 @@ __device__ __forceinline__ void materialize32(const float (&x)[32]) {
                  "v"(x[i + 6]), "v"(x[i + 7]));
 }
 
-// 8 bf16 of one LDS row as two 8-byte halves at columns c0 and c0 + 16
-__device__ __forceinline__ bf16x8 lds_bf16x8_split(const uint16_t* row, int c0) {
-  const uint2 lo = *reinterpret_cast<const uint2*>(row + c0);
-  const uint2 hi = *reinterpret_cast<const uint2*>(row + c0 + 16);
+// 8 bf16 as two 8-byte halves (columns c0..c0+3 and c0+16..c0+19 of a row)
+__device__ __forceinline__ bf16x8 lds_bf16x8_split(const uint16_t* first, const uint16_t* second) {
+  const uint2 lo = *reinterpret_cast<const uint2*>(first);
+  const uint2 hi = *reinterpret_cast<const uint2*>(second);
   const uint4 w = {lo.x, lo.y, hi.x, hi.y};
   return __builtin_bit_cast(bf16x8, w);
 }
@@ -156,7 +193,7 @@ __device__ __forceinline__ void store_block(float* m, int bi, int bj, f32x4 acc,
   for (int r = 0; r < 4; ++r) m[(16 * bi + 4 * g4 + r) * LDA + 16 * bj + n16] = acc[r];
 }
 
-template <int NP>
+template <int NP, bool S0VEC>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NP == 32 ? 4 : 1)))
 tree_verify_kernel(const VerifyParams P) {
   constexpr int MT = NP / 16;  // 16-node tiles
@@ -205,9 +242,60 @@ tree_verify_kernel(const VerifyParams P) {
   }
   const float* S0 = p.state + slot * p.state_slot_stride + (int64_t)h * p.state_h_stride;
 
-  // ---- 0. state loads first: s0r[t][j] = S0[k = 16j + 4g + e][v = 32w + 16t + n]
+  // ---- 0. issue order (vector memory returns in order): the gates and
+  // ancestry bits (wave 0), the q/k/v rows straight into LDS, then the 64 KiB
+  // state tile into registers.  Phase 1 only waits for what precedes the
+  // state; the state keeps streaming underneath it.  The loads before the
+  // state are unconditional and undecoded (clamped indices, pointer selects,
+  // whole words) so that nothing reads them, and waits, before the state is
+  // issued.
+  // wave 0's lane i fetches node i's gate words and ancestry bits (rows past
+  // the tree repeat the last node; decoded after the state is issued)
+  uint32_t sha = 0, shb = 0, shdt = 0, shdec = 0;
+  if (wave == 0) {
+    const int64_t gi = row0 + (lane < n ? lane : n - 1);
+    lds_dma4(word_of(p.a, gi * p.a_row_stride + h, p.a_dtype, sha), sm.graw[0]);
+    lds_dma4(word_of(p.b, gi * p.b_row_stride + h, p.b_dtype, shb), sm.graw[1]);
+    const uint32_t* bits = p.anc_bits ? reinterpret_cast<const uint32_t*>(p.anc_bits + gi)
+                                      : static_cast<const uint32_t*>(p.y);
+    lds_dma4(bits, sm.graw[2]);
+    lds_dma4(bits + 1, sm.graw[3]);
+    lds_dma4(word_of(p.dt_bias, h, p.dt_bias_dtype, shdt), sm.graw[4]);
+    lds_dma4(word_of(p.neg_exp_A ? static_cast<const void*>(p.neg_exp_A) : p.A_log, h,
+                     p.neg_exp_A ? (int)DFT_F32 : p.A_log_dtype, shdec),
+             sm.graw[5]);
+  }
+  if (p.anc_f32) {  // dense ancestry: rows become bit masks right away
+    const float* ab = p.anc_f32 + (int64_t)b * p.anc_req_stride;
+    for (int i = wave; i < NP; i += 4) {
+      const float v = (i < n && lane < n) ? ab[i * p.anc_row_stride + lane] : 0.f;
+      const uint64_t bits = __ballot(v > 0.5f);
+      if (lane == 0) sm.anc[i] = bits & mask_upto(i);
+    }
+  }
+  constexpr int kQkvDma = 3 * (NP / 16);  // row copies per wave
+  const int KD = p.hk * kD;
+  const int64_t ys = p.y_row_stride;
+  {
+    const uint16_t* ybase = reinterpret_cast<const uint16_t*>(p.y) + row0 * ys;
+    const uint16_t* srcs[3] = {ybase + hk * kD, ybase + KD + hk * kD, ybase + 2 * KD + h * kD};
+    uint16_t* dsts[3] = {sm.q, sm.k, sm.v};
+    const int pc = lane & 15;
+#pragma unroll
+    for (int u = 0; u < NP / 16; ++u) {
+      const int blk = wave + 4 * u;  // rows 4 blk .. 4 blk + 3
+      const int i = 4 * blk + (lane >> 4);
+      const int isrc = i < n ? i : n - 1;  // rows past the tree repeat a real row (finite, masked later)
+      const int64_t goff = isrc * ys + 8 * ((pc ^ i) & 15);
+#pragma unroll
+      for (int m = 0; m < 3; ++m) lds_dma16(srcs[m] + goff, dsts[m] + 4 * blk * kD);
+    }
+  }
+  asm volatile("" ::: "memory");
+
+  // s0r[t][j] = S0[k = 16j + 4g + e][v = 32w + 16t + n]
   f32x4 s0r[2][8];
-  if (P.s0_vec) {
+  if (S0VEC) {
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
       const float* rowp = S0 + (int64_t)(32 * wave + 16 * t + n16) * p.state_v_stride + 4 * g4;
@@ -223,60 +311,48 @@ tree_verify_kernel(const VerifyParams P) {
         for (int e = 0; e < 4; ++e)
           s0r[t][j][e] = S0[(int64_t)(32 * wave + 16 * t + n16) * p.state_v_stride +
                             (int64_t)(16 * j + 4 * g4 + e) * p.state_k_stride];
+    __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 15));  // element loads: no overlap on this path
   }
+  asm volatile("" ::: "memory");
 
-  const int KD = p.hk * kD;
-  const int64_t ys = p.y_row_stride;
-  const uint16_t* ybase = reinterpret_cast<const uint16_t*>(p.y) + row0 * ys;
-  {
-    const uint16_t* yq = ybase + hk * kD;
-    const uint16_t* yk = yq + KD;
-    const uint16_t* yv = ybase + 2 * KD + h * kD;
-    for (int c = tid; c < NP * 16; c += 256) {
-      const int i = c >> 4, ch = (c & 15) * 8;
-      uint4 vq = {0u, 0u, 0u, 0u}, vk = vq, vv = vq;
+  if (wave == 0) {
+    // the gate words were wave 0's first loads: wait for them only
+    __builtin_amdgcn_s_waitcnt(waitcnt_imm(kQkvDma + 16, 15));
+    asm volatile("" ::: "memory");
+    if (lane < NP) {
+      const int i = lane;
+      float gi = 0.f, bi = 0.f;
       if (i < n) {
-        vq = *reinterpret_cast<const uint4*>(yq + i * ys + ch);
-        vk = *reinterpret_cast<const uint4*>(yk + i * ys + ch);
-        vv = *reinterpret_cast<const uint4*>(yv + i * ys + ch);
+        const float a = word_to_f(sm.graw[0][i], sha, p.a_dtype) + word_to_f(sm.graw[4][i], shdt, p.dt_bias_dtype);
+        const float sp = a > 20.f ? a : logf(1.f + expf(fminf(a, 20.f)));
+        const uint32_t wdec = sm.graw[5][i];
+        const float dec = p.neg_exp_A ? __uint_as_float(wdec) : -expf(word_to_f(wdec, shdec, p.A_log_dtype));
+        gi = dec * sp;
+        bi = 1.f / (1.f + expf(-word_to_f(sm.graw[1][i], shb, p.b_dtype)));
       }
-      *reinterpret_cast<uint4*>(&sm.q[i * kQS + ch]) = vq;
-      *reinterpret_cast<uint4*>(&sm.k[i * kQS + ch]) = vk;
-      *reinterpret_cast<uint4*>(&sm.v[i * kQS + ch]) = vv;
+      sm.gc[i] = gi;
+      sm.beta[i] = bi;
+      if (p.anc_bits) {
+        const uint64_t bits = ((uint64_t)sm.graw[3][i] << 32) | sm.graw[2][i];
+        sm.anc[i] = i < n ? (bits & mask_upto(i) & mask_below(n)) : 0ull;
+      }
     }
   }
-  if (tid < NP) {
-    const int i = tid;
-    float gi = 0.f, bi = 0.f;
-    if (i < n) {
-      const float a = ld_f(p.a, (row0 + i) * p.a_row_stride + h, p.a_dtype) + ld_f(p.dt_bias, h, p.dt_bias_dtype);
-      const float sp = a > 20.f ? a : logf(1.f + expf(fminf(a, 20.f)));
-      const float dec = p.neg_exp_A ? p.neg_exp_A[h] : -expf(ld_f(p.A_log, h, p.A_log_dtype));
-      gi = dec * sp;
-      const float bb = ld_f(p.b, (row0 + i) * p.b_row_stride + h, p.b_dtype);
-      bi = 1.f / (1.f + expf(-bb));
-    }
-    sm.gc[i] = gi;
-    sm.beta[i] = bi;
-    if (p.anc_bits) sm.anc[i] = i < n ? (p.anc_bits[row0 + i] & mask_upto(i) & mask_below(n)) : 0ull;
-  }
-  if (p.anc_f32) {
-    const float* ab = p.anc_f32 + (int64_t)b * p.anc_req_stride;
-    for (int i = wave; i < NP; i += 4) {
-      const float v = (i < n && lane < n) ? ab[i * p.anc_row_stride + lane] : 0.f;
-      const uint64_t bits = __ballot(v > 0.5f);
-      if (lane == 0) sm.anc[i] = bits & mask_upto(i);
-    }
-  }
-  __syncthreads();
+  // Wait for the row loads and gates (everything issued before the state),
+  // then make the LDS writes of all waves visible.  A plain __syncthreads()
+  // here would also drain the state loads.
+  __builtin_amdgcn_s_waitcnt(waitcnt_imm(16, 0));
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
 
   // ---- 1a. row norms and path-cumulative decay
   if (tid < 2 * NP) {
-    const uint16_t* rowp = (tid < NP ? sm.q : sm.k) + (tid % NP) * kQS;
+    const int i = tid % NP;
+    const uint16_t* rowp = (tid < NP ? sm.q : sm.k);
     float ss = 0.f;
 #pragma unroll
     for (int c = 0; c < kD; c += 8) {
-      const uint4 u = *reinterpret_cast<const uint4*>(rowp + c);
+      const uint4 u = *reinterpret_cast<const uint4*>(rowp + qkv_at(i, c));
       const uint32_t w[4] = {u.x, u.y, u.z, u.w};
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
@@ -304,7 +380,7 @@ tree_verify_kernel(const VerifyParams P) {
     float* dk = p.aux_k + (int64_t)(per_khead ? hk : h) * p.aux_k_h_stride + row0 * p.aux_k_row_stride;
     for (int c = tid; c < n * 32; c += 256) {
       const int i = c >> 5, d = (c & 31) * 4;
-      const uint2 u = *reinterpret_cast<const uint2*>(&sm.k[i * kQS + d]);
+      const uint2 u = *reinterpret_cast<const uint2*>(&sm.k[qkv_at(i, d)]);
       const float r = sm.rk[i];
       const f32x4 val = {__uint_as_float(u.x << 16) * r, __uint_as_float(u.x & 0xffff0000u) * r,
                          __uint_as_float(u.y << 16) * r, __uint_as_float(u.y & 0xffff0000u) * r};
@@ -336,8 +412,8 @@ tree_verify_kernel(const VerifyParams P) {
           f32x4 acc = {};
 #pragma unroll
           for (int s = 0; s < 4; ++s) {
-            const bf16x8 av = *reinterpret_cast<const bf16x8*>(left + (16 * it + n16) * kQS + 32 * s + 8 * g4);
-            const bf16x8 bv = *reinterpret_cast<const bf16x8*>(sm.k + (16 * jt + n16) * kQS + 32 * s + 8 * g4);
+            const bf16x8 av = *reinterpret_cast<const bf16x8*>(left + qkv_at(16 * it + n16, 32 * s + 8 * g4));
+            const bf16x8 bv = *reinterpret_cast<const bf16x8*>(sm.k + qkv_at(16 * jt + n16, 32 * s + 8 * g4));
             acc = mfma_bf16_16x16x32(av, bv, acc);
           }
           const int j = 16 * jt + n16;
@@ -430,9 +506,9 @@ tree_verify_kernel(const VerifyParams P) {
     }
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
-      const int off = (16 * mt + n16) * kQS + 32 * s + 4 * g4;
-      const bf16x8 aq = lds_bf16x8_split(sm.q, off);
-      const bf16x8 ak = lds_bf16x8_split(sm.k, off);
+      const int row = 16 * mt + n16, c0 = 32 * s + 4 * g4;
+      const bf16x8 aq = lds_bf16x8_split(sm.q + qkv_at(row, c0), sm.q + qkv_at(row, c0 + 16));
+      const bf16x8 ak = lds_bf16x8_split(sm.k + qkv_at(row, c0), sm.k + qkv_at(row, c0 + 16));
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
         cq[mt][t] = mfma_bf16_16x16x32(aq, bhi[t], cq[mt][t]);
@@ -458,7 +534,7 @@ tree_verify_kernel(const VerifyParams P) {
       for (int e = 0; e < 8; ++e) {
         const int mt = 2 * ks + (e >> 2), r = e & 3;
         const int i = 16 * mt + 4 * g4 + r;
-        const float vv = bf16_bits_to_f32(sm.v[i * kQS + col]);
+        const float vv = bf16_bits_to_f32(sm.v[qkv_at(i, col)]);
         w8[e] = sm.beta[i] * (vv - sm.gc[i] * ck[mt][t][r]);
       }
       split_bf16x8(w8, wh[ks][t], wl[ks][t]);
@@ -510,10 +586,17 @@ int launch_tree_verify(const dft_verify_args* a, hipStream_t stream) {
   P.auxk_vec = a->aux_k && (reinterpret_cast<uintptr_t>(a->aux_k) % 16) == 0 && (a->aux_k_row_stride % 4) == 0 &&
                (a->aux_k_h_stride % 4) == 0;
   const dim3 grid((unsigned)(a->batch * a->hv)), block(256);
-  if (a->n_nodes <= 32)
-    hipLaunchKernelGGL(tree_verify_kernel<32>, grid, block, 0, stream, P);
-  else
-    hipLaunchKernelGGL(tree_verify_kernel<64>, grid, block, 0, stream, P);
+  if (a->n_nodes <= 32) {
+    if (P.s0_vec)
+      hipLaunchKernelGGL((tree_verify_kernel<32, true>), grid, block, 0, stream, P);
+    else
+      hipLaunchKernelGGL((tree_verify_kernel<32, false>), grid, block, 0, stream, P);
+  } else {
+    if (P.s0_vec)
+      hipLaunchKernelGGL((tree_verify_kernel<64, true>), grid, block, 0, stream, P);
+    else
+      hipLaunchKernelGGL((tree_verify_kernel<64, false>), grid, block, 0, stream, P);
+  }
   return hipGetLastError() == hipSuccess ? DFT_OK : DFT_ERR_LAUNCH;
 }
 

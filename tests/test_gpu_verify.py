@@ -194,3 +194,14 @@ def test_verify_persistent_loop_many_heads(cuda, sizes_kind):
         sizes, kinds = synth.ragged_sizes(12, 8, 64, seed=3)  # 384 items (> 1 per CU x 256)
     batch = synth.make_batch(9, 0, sizes, hk=16, hv=32, kinds=kinds)
     check_against_oracle(batch, *run_gpu(batch, cuda, packed=(sizes_kind != "uniform32")))
+
+
+def test_verify_kmajor_state_element_loads(cuda):
+    """A k-major state ([hv, dk, dv] contiguous, v stride 1) takes the
+    element-load path of the kernel; same results."""
+    from dforktree_amd import synth
+    announce("verify k-major state")
+    batch = synth.make_batch(8, 0, [32, 17], hk=2, hv=4, kinds=["random", "chain"])
+    st = batch.state.transpose(-1, -2).contiguous()           # [B, hv, K, V]
+    o, k, v, g = run_gpu(batch, cuda, state=st.to(cuda).transpose(-1, -2), packed=True)
+    check_against_oracle(batch, o, k, v, g)
