@@ -73,7 +73,14 @@ struct VerifyParams {
   dft_verify_args a;
   int s0_vec;    // state rows 16-byte aligned with k stride 1 (selects the kernel)
   int auxk_vec;  // aux_k rows 16-byte aligned
+  int vn_stage;  // vn rows 16-byte aligned: written as whole rows through LDS
+  int o_stage;   // o is bf16 with 16-byte aligned head rows: written through LDS
 };
+
+// Output staging in the (then free) q/k/v region: vn as NP x 128 fp32 with
+// 16-byte chunk q of row i at q ^ (i & 31), o as NP x 128 bf16 with the
+// q/k/v swizzle; both keep the accumulator-layout writes conflict-free.
+__device__ __forceinline__ int vn_at(int i, int c) { return i * kD + ((((c >> 2) ^ i) & 31) << 2) + (c & 3); }
 
 template <int NP>
 struct VerifySmem {
@@ -539,6 +546,11 @@ tree_verify_kernel(const VerifyParams P) {
       }
       split_bf16x8(w8, wh[ks][t], wl[ks][t]);
     }
+  // every wave has read its v rows: the q/k/v region takes the outputs
+  __syncthreads();
+  float* vn_s = reinterpret_cast<float*>(sm.q);  // spans q and k
+  uint16_t* o_s = sm.v;
+
   // [X; M] W: tiles mo < MT give vn, tiles mo >= MT give M W.
 #pragma unroll
   for (int mo = 0; mo < 2 * MT; ++mo) {
@@ -565,13 +577,41 @@ tree_verify_kernel(const VerifyParams P) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int i = 16 * mt + 4 * g4 + r;
-        if (i >= n) continue;
         if (mo < MT) {
-          if (p.aux_v) p.aux_v[(int64_t)h * p.aux_v_h_stride + (row0 + i) * p.aux_v_row_stride + col] = acc[t][r];
+          if (P.vn_stage)
+            vn_s[vn_at(i, col)] = acc[t][r];
+          else if (p.aux_v && i < n)
+            p.aux_v[(int64_t)h * p.aux_v_h_stride + (row0 + i) * p.aux_v_row_stride + col] = acc[t][r];
         } else {
-          st_f(p.o, (row0 + i) * p.o_row_stride + (int64_t)h * p.o_h_stride + col, p.o_dtype,
-               sm.cO[i] * cq[mt][t][r] + acc[t][r]);
+          const float ov = sm.cO[i] * cq[mt][t][r] + acc[t][r];
+          if (P.o_stage)
+            o_s[qkv_at(i, col)] = f32_to_bf16_bits(ov);
+          else if (i < n)
+            st_f(p.o, (row0 + i) * p.o_row_stride + (int64_t)h * p.o_h_stride + col, p.o_dtype, ov);
         }
+      }
+    }
+  }
+  if (P.vn_stage || P.o_stage) {
+    __syncthreads();
+    if (P.vn_stage) {  // rows of 32 x 16 bytes
+      float* dst = p.aux_v + (int64_t)h * p.aux_v_h_stride + row0 * p.aux_v_row_stride;
+#pragma unroll
+      for (int u = 0; u < NP / 8; ++u) {
+        const int i = 8 * u + (tid >> 5), q = tid & 31;
+        if (i < n)
+          *reinterpret_cast<f32x4*>(dst + i * p.aux_v_row_stride + 4 * q) =
+              *reinterpret_cast<const f32x4*>(&vn_s[vn_at(i, 4 * q)]);
+      }
+    }
+    if (P.o_stage) {  // rows of 16 x 16 bytes
+      uint16_t* dst = static_cast<uint16_t*>(p.o) + row0 * p.o_row_stride + (int64_t)h * p.o_h_stride;
+#pragma unroll
+      for (int u = 0; u < NP / 16; ++u) {
+        const int i = 16 * u + (tid >> 4), q = tid & 15;
+        if (i < n)
+          *reinterpret_cast<uint4*>(dst + i * p.o_row_stride + 8 * q) =
+              *reinterpret_cast<const uint4*>(&o_s[qkv_at(i, 8 * q)]);
       }
     }
   }
@@ -585,6 +625,10 @@ int launch_tree_verify(const dft_verify_args* a, hipStream_t stream) {
              (a->state_h_stride % 4) == 0 && (a->state_slot_stride % 4) == 0;
   P.auxk_vec = a->aux_k && (reinterpret_cast<uintptr_t>(a->aux_k) % 16) == 0 && (a->aux_k_row_stride % 4) == 0 &&
                (a->aux_k_h_stride % 4) == 0;
+  P.vn_stage = a->aux_v && (reinterpret_cast<uintptr_t>(a->aux_v) % 16) == 0 && (a->aux_v_row_stride % 4) == 0 &&
+               (a->aux_v_h_stride % 4) == 0;
+  P.o_stage = a->o_dtype == DFT_BF16 && (reinterpret_cast<uintptr_t>(a->o) % 16) == 0 && (a->o_row_stride % 8) == 0 &&
+              (a->o_h_stride % 8) == 0;
   const dim3 grid((unsigned)(a->batch * a->hv)), block(256);
   if (a->n_nodes <= 32) {
     if (P.s0_vec)
