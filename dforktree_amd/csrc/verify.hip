@@ -352,14 +352,16 @@ tree_verify_kernel(const VerifyParams P) {
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
 
-  // ---- 1a. row norms and path-cumulative decay
-  if (tid < 2 * NP) {
-    const int i = tid % NP;
-    const uint16_t* rowp = (tid < NP ? sm.q : sm.k);
+  // ---- 1a. row norms (4 threads per q/k row) and path-cumulative decay
+  // (256 / NP threads per node), spread over all four waves.
+#pragma unroll
+  for (int r0 = 0; r0 < 2 * NP; r0 += 64) {
+    const int r = r0 + (tid >> 2), qd = tid & 3, i = r % NP;
+    const uint16_t* rows = r < NP ? sm.q : sm.k;
     float ss = 0.f;
 #pragma unroll
-    for (int c = 0; c < kD; c += 8) {
-      const uint4 u = *reinterpret_cast<const uint4*>(rowp + qkv_at(i, c));
+    for (int c = 32 * qd; c < 32 * qd + 32; c += 8) {
+      const uint4 u = *reinterpret_cast<const uint4*>(rows + qkv_at(i, c));
       const uint32_t w[4] = {u.x, u.y, u.z, u.w};
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
@@ -367,17 +369,27 @@ tree_verify_kernel(const VerifyParams P) {
         ss += lo * lo + hi * hi;
       }
     }
-    const float r = rsqrtf(ss + 1e-6f);
-    if (tid < NP) sm.rq[tid] = r * p.scale;
-    else sm.rk[tid - NP] = r;
-  } else if (tid < 3 * NP) {
-    const int i = tid - 2 * NP;
+    ss += __shfl_xor(ss, 1);
+    ss += __shfl_xor(ss, 2);
+    if (qd == 0) {
+      const float rn = rsqrtf(ss + 1e-6f);
+      if (r < NP) sm.rq[i] = rn * p.scale;
+      else sm.rk[i] = rn;
+    }
+  }
+  {
+    constexpr int TPN = 256 / NP;  // threads per node
+    const int i = tid / TPN, sub = tid % TPN;
     const uint64_t bits = sm.anc[i];
     float G = 0.f;
 #pragma unroll
-    for (int j = 0; j < NP; ++j)
+    for (int jj = 0; jj < NP / TPN; ++jj) {
+      const int j = jj * TPN + sub;
       if ((bits >> j) & 1ull) G += sm.gc[j];
-    sm.G[i] = G;
+    }
+#pragma unroll
+    for (int o = 1; o < TPN; o <<= 1) G += __shfl_xor(G, o);
+    if (sub == 0) sm.G[i] = G;
   }
   __syncthreads();
 
@@ -438,24 +450,22 @@ tree_verify_kernel(const VerifyParams P) {
   }
   __syncthreads();
 
-  // ---- 1c. diagonal blocks of X by forward substitution (wave 0, lane
-  // group b = block, lane j = column); the other waves zero X above the diagonal.
-  if (wave == 0) {
-    const int bb = g4, j = n16;
-    if (bb < MT) {
-      float xc[16];
+  // ---- 1c. diagonal blocks of X by forward substitution (block b on wave
+  // b, lane j = column, so the serial chains run on different SIMDs); X above
+  // the diagonal blocks is zeroed by everyone.
+  if (wave < MT && lane < 16) {
+    const int bb = wave, j = lane;
+    float xc[16];
 #pragma unroll
-      for (int i = 0; i < 16; ++i) xc[i] = (i == j) ? 1.f : 0.f;
-      solve_block16<LDA>(xc, sm.am, 16 * bb);
-      materialize16(xc);
+    for (int i = 0; i < 16; ++i) xc[i] = (i == j) ? 1.f : 0.f;
+    solve_block16<LDA>(xc, sm.am, 16 * bb);
+    materialize16(xc);
 #pragma unroll
-      for (int i = 0; i < 16; ++i) sm.x[(16 * bb + i) * LDA + 16 * bb + j] = xc[i];
-    }
-  } else {
-    for (int e = tid - 64; e < NP * NP; e += 192) {
-      const int i = e / NP, jj = e % NP;
-      if ((i >> 4) < (jj >> 4)) sm.x[i * LDA + jj] = 0.f;
-    }
+    for (int i = 0; i < 16; ++i) sm.x[(16 * bb + i) * LDA + 16 * bb + j] = xc[i];
+  }
+  for (int e = tid; e < NP * NP; e += 256) {
+    const int i = e / NP, jj = e % NP;
+    if ((i >> 4) < (jj >> 4)) sm.x[i * LDA + jj] = 0.f;
   }
   __syncthreads();
 
