@@ -41,6 +41,18 @@ class VerifyArgs(C.Structure):
     ]
 
 
+class PendingArgs(C.Structure):
+    _fields_ = [
+        ("path_cols", i32), ("k_head_div", i32), ("prev_n_nodes", i32),
+        ("path", vp), ("path_req_stride", i64), ("path_dtype", i32),
+        ("path_len", vp), ("path_len_dtype", i32),
+        ("prev_cu_seqlens", vp),
+        ("keys", vp), ("k_h_stride", i64), ("k_row_stride", i64),
+        ("values", vp), ("v_h_stride", i64), ("v_row_stride", i64),
+        ("gains", vp), ("g_h_stride", i64), ("g_row_stride", i64),
+    ]
+
+
 class ConvArgs(C.Structure):
     _fields_ = [
         ("batch", i32), ("n_nodes", i32), ("channels", i32), ("width", i32), ("silu", i32),
@@ -93,7 +105,7 @@ class TreeArgs(C.Structure):
     ]
 
 
-EXPORTS = ("dft_tree_verify", "dft_tree_conv", "dft_tree_commit", "dft_tree_struct",
+EXPORTS = ("dft_tree_verify", "dft_tree_commit_verify", "dft_tree_conv", "dft_tree_commit", "dft_tree_struct",
            "dft_block_inverse", "dft_error_string", "dft_abi_version")
 
 
@@ -120,6 +132,7 @@ def load() -> C.CDLL:
             f"{LIB_PATH} is not built; run `python -m dforktree_amd.build` (hipcc, gfx950)")
     lib = C.CDLL(str(LIB_PATH))
     for name, argt in (("dft_tree_verify", [C.POINTER(VerifyArgs), vp]),
+                       ("dft_tree_commit_verify", [C.POINTER(VerifyArgs), C.POINTER(PendingArgs), vp]),
                        ("dft_tree_conv", [C.POINTER(ConvArgs), vp]),
                        ("dft_tree_commit", [C.POINTER(CommitArgs), vp]),
                        ("dft_tree_struct", [C.POINTER(TreeArgs), vp]),

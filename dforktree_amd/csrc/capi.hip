@@ -6,6 +6,7 @@
 
 namespace dft {
 int launch_tree_verify(const dft_verify_args* a, hipStream_t stream);
+int launch_tree_commit_verify(const dft_verify_args* a, const dft_pending_commit* c, hipStream_t stream);
 int launch_block_inverse(float* x, int n_mats, int n, int64_t mat_stride, hipStream_t stream);
 int launch_tree_conv(const dft_conv_args* a, hipStream_t stream);
 int launch_tree_commit(const dft_commit_args* a, hipStream_t stream);
@@ -17,6 +18,29 @@ namespace {
 bool float_tag(int32_t t) { return t == DFT_F32 || t == DFT_BF16 || t == DFT_F16; }
 bool index_tag(int32_t t) { return t == DFT_I32 || t == DFT_I64; }
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Checks shared by the verify entry points: DFT_OK to launch, DFT_ERR_* to
+// refuse, or -1 when there is nothing to do.
+int verify_status(const dft_verify_args* a) {
+  if (!a) return DFT_ERR_INVALID;
+  if (a->batch < 0 || a->n_nodes < 0 || a->hk <= 0 || a->hv <= 0 || a->hv % a->hk != 0) return DFT_ERR_INVALID;
+  if (a->dk != 128 || a->dv != 128) return DFT_ERR_UNSUPPORTED;
+  if (a->n_nodes > 64) return DFT_ERR_UNSUPPORTED;
+  if (a->batch == 0 || a->n_nodes == 0) return -1;
+  if (!a->y || !a->a || !a->b || !a->state || !a->o) return DFT_ERR_INVALID;
+  if (!a->neg_exp_A && !a->A_log) return DFT_ERR_INVALID;
+  if (!a->dt_bias) return DFT_ERR_INVALID;
+  if ((a->anc_f32 == nullptr) == (a->anc_bits == nullptr)) return DFT_ERR_INVALID;
+  if (!float_tag(a->a_dtype) || !float_tag(a->b_dtype) || !float_tag(a->dt_bias_dtype) ||
+      (a->A_log && !float_tag(a->A_log_dtype)))
+    return DFT_ERR_INVALID;
+  if (a->o_dtype != DFT_F32 && a->o_dtype != DFT_BF16 && a->o_dtype != DFT_F16) return DFT_ERR_INVALID;
+  if (a->state_indices && !index_tag(a->state_indices_dtype)) return DFT_ERR_INVALID;
+  // q/k/v rows are copied as 16-byte pieces
+  if (!aligned16(a->y) || a->y_row_stride % 8 != 0) return DFT_ERR_INVALID;
+  if ((int64_t)a->batch * a->hv > INT32_MAX) return DFT_ERR_UNSUPPORTED;
+  return DFT_OK;
+}
 
 }  // namespace
 
@@ -35,24 +59,25 @@ const char* dft_error_string(int status) {
 }
 
 int dft_tree_verify(const dft_verify_args* a, void* stream) {
-  if (!a) return DFT_ERR_INVALID;
-  if (a->batch < 0 || a->n_nodes < 0 || a->hk <= 0 || a->hv <= 0 || a->hv % a->hk != 0) return DFT_ERR_INVALID;
-  if (a->dk != 128 || a->dv != 128) return DFT_ERR_UNSUPPORTED;
-  if (a->n_nodes > 64) return DFT_ERR_UNSUPPORTED;
-  if (a->batch == 0 || a->n_nodes == 0) return DFT_OK;
-  if (!a->y || !a->a || !a->b || !a->state || !a->o) return DFT_ERR_INVALID;
-  if (!a->neg_exp_A && !a->A_log) return DFT_ERR_INVALID;
-  if (!a->dt_bias) return DFT_ERR_INVALID;
-  if ((a->anc_f32 == nullptr) == (a->anc_bits == nullptr)) return DFT_ERR_INVALID;
-  if (!float_tag(a->a_dtype) || !float_tag(a->b_dtype) || !float_tag(a->dt_bias_dtype) ||
-      (a->A_log && !float_tag(a->A_log_dtype)))
-    return DFT_ERR_INVALID;
-  if (a->o_dtype != DFT_F32 && a->o_dtype != DFT_BF16 && a->o_dtype != DFT_F16) return DFT_ERR_INVALID;
-  if (a->state_indices && !index_tag(a->state_indices_dtype)) return DFT_ERR_INVALID;
-  // q/k rows are read as 16-byte vectors
-  if (!aligned16(a->y) || a->y_row_stride % 8 != 0) return DFT_ERR_INVALID;
-  if ((int64_t)a->batch * a->hv > INT32_MAX) return DFT_ERR_UNSUPPORTED;
+  const int st = verify_status(a);
+  if (st != DFT_OK) return st < 0 ? DFT_OK : st;
   return dft::launch_tree_verify(a, static_cast<hipStream_t>(stream));
+}
+
+int dft_tree_commit_verify(const dft_verify_args* a, const dft_pending_commit* c, void* stream) {
+  const int st = verify_status(a);
+  if (st != DFT_OK) return st < 0 ? DFT_OK : st;
+  if (!c) return DFT_ERR_INVALID;
+  if (c->path_cols < 0 || c->path_cols > 16) return DFT_ERR_UNSUPPORTED;
+  if (c->k_head_div <= 0 || a->hv % c->k_head_div != 0) return DFT_ERR_INVALID;
+  if (!c->prev_cu_seqlens && (c->prev_n_nodes < 0 || c->prev_n_nodes > 64)) return DFT_ERR_INVALID;
+  if (!c->path || !c->keys || !c->values || !c->gains) return DFT_ERR_INVALID;
+  if (!index_tag(c->path_dtype) || (c->path_len && !index_tag(c->path_len_dtype))) return DFT_ERR_INVALID;
+  // the committed tile is written back with the same 16-byte accesses that read it
+  if (a->state_k_stride != 1 || !aligned16(a->state) || a->state_v_stride % 4 || a->state_h_stride % 4 ||
+      a->state_slot_stride % 4)
+    return DFT_ERR_UNSUPPORTED;
+  return dft::launch_tree_commit_verify(a, c, static_cast<hipStream_t>(stream));
 }
 
 int dft_block_inverse(float* x, int32_t n_mats, int32_t n, int64_t mat_stride, void* stream) {

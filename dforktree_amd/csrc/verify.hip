@@ -71,6 +71,7 @@ __device__ __forceinline__ void lds_dma4(const void* g, void* lds) {
 
 struct VerifyParams {
   dft_verify_args a;
+  dft_pending_commit c;  // the fused commit -> verify form only
   int s0_vec;    // state rows 16-byte aligned with k stride 1 (selects the kernel)
   int auxk_vec;  // aux_k rows 16-byte aligned
   int vn_stage;  // vn rows 16-byte aligned: written as whole rows through LDS
@@ -82,8 +83,20 @@ struct VerifyParams {
 // q/k/v swizzle; both keep the accumulator-layout writes conflict-free.
 __device__ __forceinline__ int vn_at(int i, int c) { return i * kD + ((((c >> 2) ^ i) & 31) << 2) + (c & 3); }
 
-template <int NP>
-struct VerifySmem {
+// LDS of the fused commit -> verify form: the previous step's path keys,
+// 16 rows of 128 fp32 with 16-byte chunk q of row p at q ^ ((p & 3) << 2),
+// so the MFMA operand reads of 4 rows x 16 columns hit 64 distinct banks.
+template <bool COMMIT>
+struct PendingSmem {};
+template <>
+struct PendingSmem<true> {
+  float pkey[16 * kD];
+  uint32_t pent[4][64];  // per wave: lane l's copy of path entry l % 16
+};
+__device__ __forceinline__ int pkey_at(int p, int c) { return p * kD + ((((c >> 2) ^ ((p & 3) << 2)) & 31) << 2) + (c & 3); }
+
+template <int NP, bool COMMIT = false>
+struct VerifySmem : PendingSmem<COMMIT> {
   static constexpr int LDA = NP + 4;  // fp32 row pitch, rows 16-byte aligned
   uint16_t q[NP * kD], k[NP * kD], v[NP * kD];
   float am[NP * LDA];  // at[m][i] = A[i][m] until X is formed, then M[i][j]
@@ -200,14 +213,155 @@ __device__ __forceinline__ void store_block(float* m, int bi, int bj, f32x4 acc,
   for (int r = 0; r < 4; ++r) m[(16 * bi + 4 * g4 + r) * LDA + 16 * bj + n16] = acc[r];
 }
 
-template <int NP, bool S0VEC>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NP == 32 ? 4 : 1)))
+// ---------------------------------------------------------------------------
+// fused commit of the previous step's accepted path (dft_tree_commit_verify)
+// ---------------------------------------------------------------------------
+// The previous step's accepted path of one request.  Lane l holds path entry
+// l % 16 (loaded before anything else, as a 32-bit word: the low half of an
+// int64 entry), so slot lookups are lane shuffles, not indexed arrays.
+// Entries c < len with 0 <= e < bound are valid; u is the last valid one.
+struct Pending {
+  int ent;         // this lane's entry (an invalid one replaced by u)
+  uint32_t vmask;  // bit c: entry c valid
+  int last;        // slot of u, -1 when nothing is pending
+  int64_t prow0;   // row of the request's node 0 in the previous step's buffers
+};
+
+// Lane l copies the 32-bit word of entry l % 16 into LDS (the low half of an
+// int64 entry).  A register load would be read while the row copies are in
+// flight, and the compiler then drains every load first.
+__device__ __forceinline__ void copy_path_words(const dft_pending_commit& c, int b, int lane, uint32_t* dst) {
+  const int col = (lane & 15) < c.path_cols ? (lane & 15) : c.path_cols - 1;
+  const int esz = c.path_dtype == DFT_I64 ? 8 : 4;
+  lds_dma4(static_cast<const char*>(c.path) + ((int64_t)b * c.path_req_stride + col) * esz, dst);
+}
+
+// The request's previous rows and how many path entries count; read with
+// the block's other index loads, before any stream is issued.
+struct PendingHead {
+  int64_t prow0;
+  int bound, len;
+};
+
+__device__ __forceinline__ PendingHead pending_head(const dft_pending_commit& c, int b) {
+  PendingHead ph;
+  if (c.prev_cu_seqlens) {
+    ph.prow0 = c.prev_cu_seqlens[b];
+    ph.bound = c.prev_cu_seqlens[b + 1] - c.prev_cu_seqlens[b];
+  } else {
+    ph.prow0 = (int64_t)b * c.prev_n_nodes;
+    ph.bound = c.prev_n_nodes;
+  }
+  ph.len = c.path_cols;
+  if (c.path_len) {
+    const int64_t l = ld_i(c.path_len, b, c.path_len_dtype);
+    ph.len = l < 0 ? 0 : (l < ph.len ? (int)l : ph.len);
+  }
+  return ph;
+}
+
+__device__ __forceinline__ Pending decode_pending(const PendingHead& ph, int lane, uint32_t word) {
+  Pending pd;
+  pd.prow0 = ph.prow0;
+  const int bound = ph.bound, len = ph.len;
+  const int e = (int)word;
+  const bool ok = (lane & 15) < len && e >= 0 && e < bound;
+  pd.vmask = (uint32_t)__ballot(ok) & 0xffffu;
+  pd.last = pd.vmask ? 31 - __clz(pd.vmask) : -1;
+  const int u = __shfl(e, pd.last < 0 ? 0 : pd.last);
+  pd.ent = ok ? e : (pd.last < 0 ? 0 : u);
+  return pd;
+}
+
+// Issued right after the state tile (the same count on every lane whether or
+// not anything is pending, so the explicit waits stay exact): two 16-byte
+// pieces of the path keys per thread (row t / 16), each lane's B-operand
+// values vn_p[v] and gains G_p for path slots p = 4s + g.  With nothing
+// pending the sources are the state tile itself (valid memory, never used).
+// The keys go through registers, not global->LDS copies: a copy still in
+// flight behind the state would make every LDS read wait for the state.
+constexpr int kPendLoads = 2 + 8 + 4;
+
+__device__ __forceinline__ void issue_pending(const dft_pending_commit& c, const Pending& pd, int h, int wave, int lane,
+                                              const float* dummy, f32x4 (&kr)[2], float (&vnr)[4][2],
+                                              float (&gp)[4]) {
+  const bool any = pd.last >= 0;
+  const int n16 = lane & 15, g4 = lane >> 4;
+  const float* kb = any ? c.keys + (int64_t)(h / c.k_head_div) * c.k_h_stride + pd.prow0 * c.k_row_stride : dummy;
+  const int64_t ks = any ? c.k_row_stride : 0;
+  const int krow = __shfl(pd.ent, 4 * wave + g4);
+#pragma unroll
+  for (int m = 0; m < 2; ++m) kr[m] = *reinterpret_cast<const f32x4*>(kb + krow * ks + 4 * (n16 + 16 * m));
+  const float* vb = any ? c.values + (int64_t)h * c.v_h_stride + pd.prow0 * c.v_row_stride : dummy;
+  const float* gb = any ? c.gains + (int64_t)h * c.g_h_stride + pd.prow0 * c.g_row_stride : dummy;
+  const int64_t vs = any ? c.v_row_stride : 0, gs = any ? c.g_row_stride : 0;
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    const int row = __shfl(pd.ent, 4 * s + g4);
+#pragma unroll
+    for (int t = 0; t < 2; ++t) vnr[s][t] = vb[row * vs + 32 * wave + 16 * t + n16];
+    gp[s] = gb[row * gs];
+  }
+}
+
+// s0r <- e^{G_u} s0r + sum_p e^{G_u - G_p} k_p vn_p^T on the wave's tiles
+// (s0r[t][j] is the accumulator of a 16x16 MFMA with rows k = 16j + 4g + r and
+// columns v = 32w + 16t + n): fp32 MFMA 16x16x4, path slots as the inner
+// dimension (A = keys from LDS, B = weighted values from registers).
+// thread (w, l) holds chunks n and n + 16 of path key row 4w + g
+__device__ __forceinline__ void stage_pending_keys(float* pkey, const f32x4 (&kr)[2], int wave, int lane) {
+  const int rs = 4 * wave + (lane >> 4), n16 = lane & 15;
+#pragma unroll
+  for (int m = 0; m < 2; ++m) *reinterpret_cast<f32x4*>(&pkey[pkey_at(rs, 4 * (n16 + 16 * m))]) = kr[m];
+}
+
+__device__ __forceinline__ void apply_pending(const Pending& pd, const float* pkey, const float (&vnr)[4][2],
+                                              const float (&gp)[4], int lane, f32x4 (&s0r)[2][8]) {
+  const int n16 = lane & 15, g4 = lane >> 4;
+  const int cu = pd.last;
+  const int su = cu >> 2;
+  const float gsel = su == 0 ? gp[0] : su == 1 ? gp[1] : su == 2 ? gp[2] : gp[3];
+  const float gu = __shfl(gsel, (cu & 3) * 16);
+  const float eu = __expf(gu);
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) s0r[t][j] *= eu;
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    if (4 * s > cu) break;  // uniform
+    const int p = 4 * s + g4;
+    const float wgt = ((pd.vmask >> p) & 1u) ? __expf(gu - gp[s]) : 0.f;
+    const float bv[2] = {wgt * vnr[s][0], wgt * vnr[s][1]};
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float av = pkey[pkey_at(p, 16 * j + n16)];
+#pragma unroll
+      for (int t = 0; t < 2; ++t) s0r[t][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv[t], s0r[t][j], 0, 0, 0);
+    }
+  }
+}
+
+// the committed tile goes back where it was read (16-byte stores)
+__device__ __forceinline__ void store_state(float* S, int64_t v_stride, int wave, int lane, const f32x4 (&s0r)[2][8]) {
+  const int n16 = lane & 15, g4 = lane >> 4;
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    float* rowp = S + (int64_t)(32 * wave + 16 * t + n16) * v_stride + 4 * g4;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) __builtin_nontemporal_store(s0r[t][j], reinterpret_cast<f32x4*>(rowp + 16 * j));
+  }
+}
+
+template <int NP, bool S0VEC, bool COMMIT>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NP == 32 ? (COMMIT ? 3 : 4) : 1)))
 tree_verify_kernel(const VerifyParams P) {
   constexpr int MT = NP / 16;  // 16-node tiles
   constexpr int KS = NP / 32;  // 32-node k-steps of phase 3
-  constexpr int LDA = VerifySmem<NP>::LDA;
+  constexpr int LDA = VerifySmem<NP, COMMIT>::LDA;
+  constexpr int kPend = COMMIT ? kPendLoads : 0;  // vector-memory ops issued after the state
   const dft_verify_args& p = P.a;
-  __shared__ VerifySmem<NP> sm;
+  __shared__ VerifySmem<NP, COMMIT> sm;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int n16 = lane & 15, g4 = lane >> 4;
@@ -240,7 +394,6 @@ tree_verify_kernel(const VerifyParams P) {
     n = p.n_nodes;
   }
   n = n < 0 ? 0 : (n > NP ? NP : n);
-  if (n == 0) return;
 
   int64_t slot = b;
   if (p.state_indices) {
@@ -248,6 +401,33 @@ tree_verify_kernel(const VerifyParams P) {
     if (slot < 0) slot = 0;
   }
   const float* S0 = p.state + slot * p.state_slot_stride + (int64_t)h * p.state_h_stride;
+  PendingHead ph{};
+  if constexpr (COMMIT) ph = pending_head(P.c, b);
+  Pending pd;
+  float vnr[4][2], gp[4];
+  f32x4 kr[2];
+  if constexpr (COMMIT) {
+    copy_path_words(P.c, b, lane, sm.pent[wave]);  // the wave's first load: no wait below depends on its count
+    if (n == 0) {  // nothing to verify this step: the commit alone
+      __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 15));
+      pd = decode_pending(ph, lane, sm.pent[wave][lane]);
+      if (pd.last < 0) return;
+      f32x4 s0r[2][8];
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const float* rowp = S0 + (int64_t)(32 * wave + 16 * t + n16) * p.state_v_stride + 4 * g4;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) s0r[t][j] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(rowp + 16 * j));
+      }
+      issue_pending(P.c, pd, h, wave, lane, S0, kr, vnr, gp);
+      stage_pending_keys(sm.pkey, kr, wave, lane);
+      __syncthreads();
+      apply_pending(pd, sm.pkey, vnr, gp, lane, s0r);
+      store_state(const_cast<float*>(S0), p.state_v_stride, wave, lane, s0r);
+      return;
+    }
+  }
+  if (n == 0) return;
 
   // ---- 0. issue order (vector memory returns in order): the gates and
   // ancestry bits (wave 0), the q/k/v rows straight into LDS, then the 64 KiB
@@ -321,10 +501,19 @@ tree_verify_kernel(const VerifyParams P) {
     __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 15));  // element loads: no overlap on this path
   }
   asm volatile("" ::: "memory");
+  if constexpr (COMMIT) {
+    // the path word was this wave's first load; at most the row copies and
+    // the state may still be in flight (wave 0 also issued 6 gate copies,
+    // which land right behind the path word)
+    __builtin_amdgcn_s_waitcnt(waitcnt_imm(kQkvDma + 16, 15));
+    pd = decode_pending(ph, lane, sm.pent[wave][lane]);
+    issue_pending(P.c, pd, h, wave, lane, S0, kr, vnr, gp);
+    asm volatile("" ::: "memory");
+  }
 
   if (wave == 0) {
     // the gate words were wave 0's first loads: wait for them only
-    __builtin_amdgcn_s_waitcnt(waitcnt_imm(kQkvDma + 16, 15));
+    __builtin_amdgcn_s_waitcnt(waitcnt_imm(kQkvDma + 16 + kPend, 15));
     asm volatile("" ::: "memory");
     if (lane < NP) {
       const int i = lane;
@@ -348,7 +537,7 @@ tree_verify_kernel(const VerifyParams P) {
   // Wait for the row loads and gates (everything issued before the state),
   // then make the LDS writes of all waves visible.  A plain __syncthreads()
   // here would also drain the state loads.
-  __builtin_amdgcn_s_waitcnt(waitcnt_imm(16, 0));
+  __builtin_amdgcn_s_waitcnt(waitcnt_imm(16 + kPend, 0));
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
 
@@ -502,6 +691,17 @@ tree_verify_kernel(const VerifyParams P) {
       }
   }
 
+  if constexpr (COMMIT) {
+    // the state, the path keys and the weights have landed: commit the
+    // previous step's path into the tile and write it back
+    stage_pending_keys(sm.pkey, kr, wave, lane);
+    __syncthreads();
+    if (pd.last >= 0) {
+      apply_pending(pd, sm.pkey, vnr, gp, lane, s0r);
+      store_state(const_cast<float*>(S0), p.state_v_stride, wave, lane, s0r);
+    }
+  }
+
   // ---- 2. Cq = q_raw S0, Ck = k_raw S0 for the wave's 32 columns.  k-step s,
   // lane group g, element e -> k = 32s + 4g + e (e < 4), 32s + 16 + 4g + e-4.
   f32x4 cq[MT][2], ck[MT][2];
@@ -627,9 +827,10 @@ tree_verify_kernel(const VerifyParams P) {
   }
 }
 
-int launch_tree_verify(const dft_verify_args* a, hipStream_t stream) {
+static VerifyParams make_params(const dft_verify_args* a) {
   VerifyParams P;
   P.a = *a;
+  P.c = dft_pending_commit{};
   const uintptr_t sp = reinterpret_cast<uintptr_t>(a->state);
   P.s0_vec = a->state_k_stride == 1 && (sp % 16) == 0 && (a->state_v_stride % 4) == 0 &&
              (a->state_h_stride % 4) == 0 && (a->state_slot_stride % 4) == 0;
@@ -639,18 +840,35 @@ int launch_tree_verify(const dft_verify_args* a, hipStream_t stream) {
                (a->aux_v_h_stride % 4) == 0;
   P.o_stage = a->o_dtype == DFT_BF16 && (reinterpret_cast<uintptr_t>(a->o) % 16) == 0 && (a->o_row_stride % 8) == 0 &&
               (a->o_h_stride % 8) == 0;
+  return P;
+}
+
+int launch_tree_verify(const dft_verify_args* a, hipStream_t stream) {
+  const VerifyParams P = make_params(a);
   const dim3 grid((unsigned)(a->batch * a->hv)), block(256);
   if (a->n_nodes <= 32) {
     if (P.s0_vec)
-      hipLaunchKernelGGL((tree_verify_kernel<32, true>), grid, block, 0, stream, P);
+      hipLaunchKernelGGL((tree_verify_kernel<32, true, false>), grid, block, 0, stream, P);
     else
-      hipLaunchKernelGGL((tree_verify_kernel<32, false>), grid, block, 0, stream, P);
+      hipLaunchKernelGGL((tree_verify_kernel<32, false, false>), grid, block, 0, stream, P);
   } else {
     if (P.s0_vec)
-      hipLaunchKernelGGL((tree_verify_kernel<64, true>), grid, block, 0, stream, P);
+      hipLaunchKernelGGL((tree_verify_kernel<64, true, false>), grid, block, 0, stream, P);
     else
-      hipLaunchKernelGGL((tree_verify_kernel<64, false>), grid, block, 0, stream, P);
+      hipLaunchKernelGGL((tree_verify_kernel<64, false, false>), grid, block, 0, stream, P);
   }
+  return hipGetLastError() == hipSuccess ? DFT_OK : DFT_ERR_LAUNCH;
+}
+
+// The caller has checked that the state takes 16-byte accesses.
+int launch_tree_commit_verify(const dft_verify_args* a, const dft_pending_commit* c, hipStream_t stream) {
+  VerifyParams P = make_params(a);
+  P.c = *c;
+  const dim3 grid((unsigned)(a->batch * a->hv)), block(256);
+  if (a->n_nodes <= 32)
+    hipLaunchKernelGGL((tree_verify_kernel<32, true, true>), grid, block, 0, stream, P);
+  else
+    hipLaunchKernelGGL((tree_verify_kernel<64, true, true>), grid, block, 0, stream, P);
   return hipGetLastError() == hipSuccess ? DFT_OK : DFT_ERR_LAUNCH;
 }
 

@@ -18,7 +18,7 @@ from typing import Optional
 import torch
 
 from . import _lib
-from ._lib import (DFT_BF16, DFT_F16, DFT_F32, DFT_I32, DFT_I64, CommitArgs, ConvArgs, TreeArgs,
+from ._lib import (DFT_BF16, DFT_F16, DFT_F32, DFT_I32, DFT_I64, CommitArgs, ConvArgs, PendingArgs, TreeArgs,
                    VerifyArgs, check, load)
 
 _FLOAT_TAG = {torch.float32: DFT_F32, torch.bfloat16: DFT_BF16, torch.float16: DFT_F16}
@@ -96,6 +96,19 @@ def tree_verify(y: torch.Tensor, a: torch.Tensor, b: torch.Tensor, A_log: Option
     b*n_nodes.  Returns o [rows, hv, dv]; aux_k [hv|hk, rows, dk],
     aux_v [hv, rows, dv], aux_g [hv, rows] are filled when given.
     """
+    args, o, dev, _keep = _verify_args(
+        y, a, b, A_log, dt_bias, state, hk=hk, hv=hv, anc=anc, anc_bits=anc_bits, batch=batch, n_nodes=n_nodes,
+        cu_seqlens=cu_seqlens, scale=scale, neg_exp_A=neg_exp_A, state_indices=state_indices,
+        state_slot_stride=state_slot_stride, o=o, o_dtype=o_dtype, aux_k=aux_k, aux_v=aux_v, aux_g=aux_g,
+        aux_k_per_khead=aux_k_per_khead)
+    check("dft_tree_verify", load().dft_tree_verify(C.byref(args), _stream(dev)))
+    return o
+
+
+def _verify_args(y, a, b, A_log, dt_bias, state, *, hk, hv, anc, anc_bits, batch, n_nodes, cu_seqlens, scale,
+                 neg_exp_A, state_indices, state_slot_stride, o, o_dtype, aux_k, aux_v, aux_g, aux_k_per_khead):
+    """Validate the verify operands and fill the C descriptor; returns
+    (args, o, device, tensors that must outlive the launch call)."""
     dev = _device_of(y, a, b, A_log, dt_bias, state, anc, anc_bits, cu_seqlens, neg_exp_A,
                      state_indices, o, aux_k, aux_v, aux_g)
     if y.dim() != 2 or y.stride(1) != 1:
@@ -196,7 +209,65 @@ def tree_verify(y: torch.Tensor, a: torch.Tensor, b: torch.Tensor, A_log: Option
     if aux_g is not None:
         _check_aux(aux_g, "aux_g", torch.float32, dims=2)
         args.aux_g, args.aux_g_h_stride, args.aux_g_row_stride = aux_g.data_ptr(), aux_g.stride(0), aux_g.stride(1)
-    check("dft_tree_verify", load().dft_tree_verify(C.byref(args), _stream(dev)))
+    return args, o, dev, (y, cu_seqlens, anc, anc_bits, si)
+
+
+def tree_commit_verify(y: torch.Tensor, a: torch.Tensor, b: torch.Tensor, A_log: Optional[torch.Tensor],
+                       dt_bias: torch.Tensor, state: torch.Tensor, *, hk: int, hv: int,
+                       pending_path: torch.Tensor, pending_keys: torch.Tensor, pending_values: torch.Tensor,
+                       pending_gains: torch.Tensor, pending_path_len: Optional[torch.Tensor] = None,
+                       prev_cu_seqlens: Optional[torch.Tensor] = None, prev_n_nodes: Optional[int] = None,
+                       pending_k_head_div: int = 1, anc: Optional[torch.Tensor] = None,
+                       anc_bits: Optional[torch.Tensor] = None, batch: Optional[int] = None,
+                       n_nodes: Optional[int] = None, cu_seqlens: Optional[torch.Tensor] = None,
+                       scale: Optional[float] = None, neg_exp_A: Optional[torch.Tensor] = None,
+                       state_indices: Optional[torch.Tensor] = None, state_slot_stride: Optional[int] = None,
+                       o: Optional[torch.Tensor] = None, o_dtype: Optional[torch.dtype] = None,
+                       aux_k: Optional[torch.Tensor] = None, aux_v: Optional[torch.Tensor] = None,
+                       aux_g: Optional[torch.Tensor] = None, aux_k_per_khead: bool = False) -> torch.Tensor:
+    """``tree_verify`` with the previous step's accepted path committed into
+    each request's state slot on the way in (one read of the state, one
+    write back).  The pending_* tensors are the previous step's saves
+    (keys [hv or hk, rows, 128], values [hv, rows, 128], gains [hv, rows])
+    and its accepted path [batch, P <= 16] (-1 padded); they must not alias
+    this step's aux outputs.  Previous rows of request b start at
+    prev_cu_seqlens[b] or b * prev_n_nodes.  Returns o."""
+    args, o, dev, _keep = _verify_args(
+        y, a, b, A_log, dt_bias, state, hk=hk, hv=hv, anc=anc, anc_bits=anc_bits, batch=batch, n_nodes=n_nodes,
+        cu_seqlens=cu_seqlens, scale=scale, neg_exp_A=neg_exp_A, state_indices=state_indices,
+        state_slot_stride=state_slot_stride, o=o, o_dtype=o_dtype, aux_k=aux_k, aux_v=aux_v, aux_g=aux_g,
+        aux_k_per_khead=aux_k_per_khead)
+    _device_of(pending_path, pending_keys, pending_values, pending_gains, pending_path_len, prev_cu_seqlens, y)
+    for t, nm, dims in ((pending_keys, "pending_keys", 3), (pending_values, "pending_values", 3),
+                        (pending_gains, "pending_gains", 2)):
+        _check_aux(t, nm, torch.float32, dims=dims)
+    for out in (aux_k, aux_v, aux_g):
+        if out is not None and any(out.data_ptr() == t.data_ptr()
+                                   for t in (pending_keys, pending_values, pending_gains)):
+            raise ValueError("the pending saves must not alias this step's aux outputs")
+    path = pending_path.unsqueeze(0) if pending_path.dim() == 1 else pending_path
+    if path.stride(1) != 1:
+        path = path.contiguous()
+    if path.shape[1] > 16 or path.shape[1] < 1:
+        raise ValueError("pending paths hold 1 to 16 entries")
+    c = PendingArgs()
+    c.path_cols, c.k_head_div = path.shape[1], pending_k_head_div
+    c.path, c.path_req_stride, c.path_dtype = path.data_ptr(), path.stride(0), _itag(path, "pending_path")
+    pl, c.path_len_dtype = _idx_vec(pending_path_len, "pending_path_len")
+    c.path_len = _ptr(pl)
+    if prev_cu_seqlens is not None:
+        if prev_cu_seqlens.dtype != torch.int32:
+            raise TypeError("prev_cu_seqlens must be int32")
+        prev_cu_seqlens = prev_cu_seqlens.contiguous()
+        c.prev_cu_seqlens = prev_cu_seqlens.data_ptr()
+    else:
+        if prev_n_nodes is None:
+            raise ValueError("give prev_cu_seqlens or prev_n_nodes")
+        c.prev_n_nodes = prev_n_nodes
+    c.keys, c.k_h_stride, c.k_row_stride = pending_keys.data_ptr(), *pending_keys.stride()[:2]
+    c.values, c.v_h_stride, c.v_row_stride = pending_values.data_ptr(), *pending_values.stride()[:2]
+    c.gains, c.g_h_stride, c.g_row_stride = pending_gains.data_ptr(), *pending_gains.stride()
+    check("dft_tree_commit_verify", load().dft_tree_commit_verify(C.byref(args), C.byref(c), _stream(dev)))
     return o
 
 

@@ -223,6 +223,43 @@ typedef struct dft_commit_args {
 DFT_API int dft_tree_commit(const dft_commit_args* args, void* stream);
 
 /* ---------------------------------------------------------------------------
+ * Verify with the previous step's accepted path committed on the way in.
+ * For every (request b, v-head h) the state tile S of slot b is read once,
+ *   S <- e^{G_u} S + sum_t e^{G_u - G_t} k_t vn_t^T      (t: valid path entries)
+ * with u the last valid entry (the in-place closed commit of
+ * tree_kernels.py:111-127 / dft_tree_commit over the previous step's saved
+ * keys, values and gains), written back to the slot, and then used as S0 of
+ * the verify that `verify` describes (same fields as dft_tree_verify; the
+ * state must have k stride 1 and 16-byte aligned rows).  Requests without a
+ * valid entry verify on S unchanged and write nothing back.
+ * No counterpart in the reference: it fuses the commit that follows one
+ * verify step into the next step's verify, so the state is read once per
+ * layer and step instead of twice.  The previous step's keys / values / gains
+ * must not alias this step's aux outputs (alternate two sets), and every
+ * request's previous rows must exist in them.
+ * ------------------------------------------------------------------------- */
+typedef struct dft_pending_commit {
+  int32_t path_cols;    /* entries per request in path, <= 16 */
+  int32_t k_head_div;   /* keys head = h / k_head_div */
+  int32_t prev_n_nodes; /* previous step: rows per request (and the node-id bound) when prev_cu_seqlens is NULL */
+  const void* path;     /* [b][path_cols] previous-step node ids, negative = unused */
+  int64_t path_req_stride;
+  int32_t path_dtype;
+  const void* path_len; /* [b] entries considered, or NULL: all path_cols */
+  int32_t path_len_dtype;
+  const int32_t* prev_cu_seqlens; /* previous step's row0(b), or NULL: b * prev_n_nodes */
+
+  const float* keys; /* [h'][row][dk] */
+  int64_t k_h_stride, k_row_stride;
+  const float* values; /* [h][row][dv] */
+  int64_t v_h_stride, v_row_stride;
+  const float* gains; /* [h][row] */
+  int64_t g_h_stride, g_row_stride;
+} dft_pending_commit;
+
+DFT_API int dft_tree_commit_verify(const dft_verify_args* verify, const dft_pending_commit* pending, void* stream);
+
+/* ---------------------------------------------------------------------------
  * Tree structure from parent indices (node 0 is the root; for i >= 1 the
  * parent is max(parent[i], 0) as tree_ops.py:73 clamps it).  Exact closure
  * for any depth.  Every output is optional.

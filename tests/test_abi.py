@@ -35,7 +35,7 @@ def test_library_exports_every_declared_symbol():
 @pytest.fixture(scope="module")
 def c_layouts(tmp_path_factory):
     from dforktree_amd import _lib
-    structs = {"dft_verify_args": _lib.VerifyArgs, "dft_conv_args": _lib.ConvArgs,
+    structs = {"dft_verify_args": _lib.VerifyArgs, "dft_pending_commit": _lib.PendingArgs, "dft_conv_args": _lib.ConvArgs,
                "dft_commit_args": _lib.CommitArgs, "dft_tree_args": _lib.TreeArgs}
     lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"', "int main(void) {",
              'printf("{");']
@@ -78,6 +78,21 @@ def test_validation_rejects_bad_descriptors_without_launching():
     assert lib.dft_tree_verify(ctypes.byref(v), None) == _lib.DFT_ERR_INVALID      # null pointers
     v.batch = 0
     assert lib.dft_tree_verify(ctypes.byref(v), None) == _lib.DFT_OK                # empty batch: no-op
+    v.batch, v.n_nodes = 1, 32
+    pc = _lib.PendingArgs()
+    pc.path_cols, pc.k_head_div, pc.prev_n_nodes, pc.path_dtype = 16, 1, 32, _lib.DFT_I32
+    assert lib.dft_tree_commit_verify(ctypes.byref(v), None, None) == _lib.DFT_ERR_INVALID  # null pointers
+    v.y = v.a = v.b = v.A_log = v.dt_bias = v.state = v.o = v.anc_bits = 16
+    v.y_row_stride, v.state_k_stride, v.state_v_stride = 8, 1, 128
+    assert lib.dft_tree_commit_verify(ctypes.byref(v), None, None) == _lib.DFT_ERR_INVALID  # no pending
+    assert lib.dft_tree_commit_verify(ctypes.byref(v), ctypes.byref(pc), None) == _lib.DFT_ERR_INVALID
+    pc.path = pc.keys = pc.values = pc.gains = 16
+    pc.path_cols = 17
+    assert lib.dft_tree_commit_verify(ctypes.byref(v), ctypes.byref(pc), None) == _lib.DFT_ERR_UNSUPPORTED
+    pc.path_cols, v.state_k_stride, v.state_v_stride = 16, 128, 1  # k-major state: no 16-byte rows
+    assert lib.dft_tree_commit_verify(ctypes.byref(v), ctypes.byref(pc), None) == _lib.DFT_ERR_UNSUPPORTED
+    v.batch = 0
+    assert lib.dft_tree_commit_verify(ctypes.byref(v), ctypes.byref(pc), None) == _lib.DFT_OK  # empty: no-op
     c = _lib.CommitArgs()
     c.n_layers, c.batch, c.hv, c.dk, c.dv, c.n_nodes, c.path_cols, c.n_ends, c.k_head_div = 1, 1, 4, 128, 128, 32, 16, 3, 1
     assert lib.dft_tree_commit(ctypes.byref(c), None) == _lib.DFT_ERR_INVALID       # n_ends

@@ -1,0 +1,183 @@
+"""GPU parity of the fused commit -> verify entry point (dft_tree_commit_verify).
+
+Step 1 verifies a batch of trees and saves k, vn, G; step 2 verifies new
+trees through the fused entry, which first commits step 1's accepted paths
+into each request's state slot.  Checked against the oracle chain
+(closed-form commit of step 1, then the step-2 verify on the committed
+state): node outputs within rel-L2 2e-3 (max-abs 1e-2 on bf16), committed
+states within rel-L2 2e-3, a request without a valid path entry keeps its
+slot bit for bit.  A second test checks that the fused entry equals the
+separate in-place commit followed by the plain verify to fp32 rounding.
+"""
+import numpy as np
+import pytest
+import torch
+
+from conftest import MAX_ABS_BF16, REL_L2, announce, max_abs, rel_l2
+from _ref import np32, oracle_verify, request_slices
+from oracle import gdn_tree as O
+
+pytestmark = pytest.mark.gpu
+
+P = 16
+
+
+def _paths(batch, seed, empty=(), shorten=()):
+    """Accepted root-to-node walks of every request, -1 padded to 16 columns;
+    requests in ``empty`` get no entry, those in ``shorten`` a path_len one
+    short of their walk."""
+    from dforktree_amd import synth
+    g = torch.Generator().manual_seed(seed)
+    idx = torch.full((batch.batch, P), -1, dtype=torch.int32)
+    lens = torch.zeros(batch.batch, dtype=torch.int32)
+    walks = []
+    for r, sl in enumerate(request_slices(batch)):
+        w = synth.accepted_path(batch.parent[sl], P, g)
+        if r in empty:
+            w = w[:0]
+        idx[r, :len(w)] = w
+        lens[r] = len(w) - (1 if r in shorten and len(w) > 1 else 0)
+        walks.append(w[:int(lens[r])].tolist())
+    return idx, lens, walks
+
+
+def _committed_states(batch1, walks):
+    """Oracle: each request's state after committing its step-1 walk (k, v)."""
+    ref = oracle_verify(batch1)
+    out = []
+    for r in range(batch1.batch):
+        S0 = np32(batch1.state[r]).transpose(0, 2, 1)
+        if walks[r]:
+            out.append(O.closed_commit(S0, ref[r]["k"], ref[r]["vn"], ref[r]["G"], walks[r]))
+        else:
+            out.append(S0.copy())
+    return out
+
+
+def _run_chain(cuda, batch1, batch2, per_khead, packed, empty=(), shorten=(), path_dtype=torch.int32):
+    from dforktree_amd import ops
+    hk, hv, B = batch1.hk, batch1.hv, batch1.batch
+    pool = batch1.state.clone().to(cuda)  # [B, hv, V, K]
+    st = pool.transpose(-1, -2)
+    g1, g2 = batch1.to(cuda), batch2.to(cuda)
+    rows1, rows2 = g1.y.shape[0], g2.y.shape[0]
+    kh = hk if per_khead else hv
+    k1 = torch.zeros(kh, rows1, 128, device=cuda)
+    v1 = torch.zeros(hv, rows1, 128, device=cuda)
+    G1 = torch.zeros(hv, rows1, device=cuda)
+    k2 = torch.zeros(kh, rows2, 128, device=cuda)
+    v2 = torch.zeros(hv, rows2, 128, device=cuda)
+    G2 = torch.zeros(hv, rows2, device=cuda)
+    kw1 = dict(batch=B, n_nodes=batch1.n_max)
+    kw2 = dict(batch=B, n_nodes=batch2.n_max)
+    if packed:
+        kw1["cu_seqlens"], kw2["cu_seqlens"] = g1.cu_seqlens, g2.cu_seqlens
+    ts1 = ops.tree_struct(g1.parent, 4, cu_seqlens=g1.cu_seqlens, n_nodes=batch1.n_max, batch=B, want=("anc_bits",))
+    ts2 = ops.tree_struct(g2.parent, 4, cu_seqlens=g2.cu_seqlens, n_nodes=batch2.n_max, batch=B, want=("anc_bits",))
+    ops.tree_verify(g1.y, g1.a, g1.b, g1.A_log, g1.dt_bias, st, hk=hk, hv=hv, anc_bits=ts1["anc_bits"],
+                    aux_k=k1, aux_v=v1, aux_g=G1, aux_k_per_khead=per_khead, **kw1)
+    idx, lens, walks = _paths(batch1, 5, empty, shorten)
+    prev = dict(prev_cu_seqlens=g1.cu_seqlens) if packed else dict(prev_n_nodes=batch1.n_max)
+    o2 = ops.tree_commit_verify(g2.y, g2.a, g2.b, g2.A_log, g2.dt_bias, st, hk=hk, hv=hv,
+                                anc_bits=ts2["anc_bits"], pending_path=idx.to(path_dtype).to(cuda),
+                                pending_keys=k1, pending_values=v1, pending_gains=G1,
+                                pending_path_len=lens.to(cuda), pending_k_head_div=hv // kh,
+                                aux_k=k2, aux_v=v2, aux_g=G2, aux_k_per_khead=per_khead, **prev, **kw2)
+    torch.cuda.synchronize()
+    return pool, o2, (k2, v2, G2), walks
+
+
+def _check_chain(batch1, batch2, pool, o2, aux2, walks, empty, per_khead):
+    S1 = _committed_states(batch1, walks)
+    got = np32(pool)
+    for r in range(batch1.batch):
+        if r in empty:
+            assert np.array_equal(got[r], np32(batch1.state[r])), f"request {r}: slot touched without a path"
+        else:
+            assert rel_l2(got[r].transpose(0, 2, 1), S1[r]) <= REL_L2, f"request {r}: committed state"
+    b2 = batch2.to("cpu")
+    b2.state = torch.stack([torch.from_numpy(np.ascontiguousarray(s.transpose(0, 2, 1))) for s in S1])
+    ref = oracle_verify(b2)
+    o = np32(o2)
+    k2, v2, G2 = (np32(t) for t in aux2)
+    R = batch2.hv // batch2.hk
+    for r, sl in enumerate(request_slices(b2)):
+        want = O.bf16_round(ref[r]["o"])
+        assert rel_l2(o[sl], want) <= REL_L2 and max_abs(o[sl], want) <= MAX_ABS_BF16, f"request {r}: o"
+        assert rel_l2(v2[:, sl], ref[r]["vn"]) <= REL_L2, f"request {r}: vn"
+        kref = ref[r]["k"][::R] if per_khead else ref[r]["k"]
+        assert rel_l2(k2[:, sl], kref) <= 1e-5
+        assert rel_l2(G2[:, sl], ref[r]["G"]) <= 1e-5
+
+
+def test_commit_verify_uniform_chain(cuda):
+    from dforktree_amd import synth
+    announce("commit->verify uniform 32")
+    kinds = ["random", "chain", "bushy", "random", "chain", "bushy"]
+    batch1 = synth.make_batch(20, 0, [32] * 6, hk=2, hv=4, kinds=kinds)
+    batch2 = synth.make_batch(21, 0, [32] * 6, hk=2, hv=4, kinds=kinds[::-1])
+    empty, shorten = (2,), (4,)
+    pool, o2, aux2, walks = _run_chain(cuda, batch1, batch2, per_khead=False, packed=False, empty=empty,
+                                       shorten=shorten)
+    _check_chain(batch1, batch2, pool, o2, aux2, walks, empty, per_khead=False)
+
+
+@pytest.mark.parametrize("path_dtype", [torch.int32, torch.int64])
+def test_commit_verify_packed_ragged_per_khead(cuda, path_dtype):
+    """Packed rows of different sizes in the two steps (the 64-wide kernel),
+    keys saved once per k-head, int32 and int64 paths."""
+    from dforktree_amd import synth
+    announce(f"commit->verify packed ragged {path_dtype}")
+    sizes1, kinds = [40, 9, 64, 17, 33, 1], ["random", "chain", "bushy", "random", "chain", "bushy"]
+    sizes2 = [12, 64, 30, 1, 50, 20]
+    batch1 = synth.make_batch(22, 0, sizes1, hk=2, hv=4, kinds=kinds)
+    batch2 = synth.make_batch(23, 0, sizes2, hk=2, hv=4, kinds=kinds)
+    empty = (3,)
+    pool, o2, aux2, walks = _run_chain(cuda, batch1, batch2, per_khead=True, packed=True, empty=empty,
+                                       path_dtype=path_dtype)
+    _check_chain(batch1, batch2, pool, o2, aux2, walks, empty, per_khead=True)
+
+
+def test_commit_verify_equals_commit_then_verify(cuda):
+    """Full layer width (16 q/k heads, 32 v heads) at 32 nodes: the fused entry
+    against dft_tree_commit (in place) followed by dft_tree_verify."""
+    from dforktree_amd import ops, synth
+    announce("commit->verify vs separate kernels")
+    B, N, hk, hv = 8, 32, 16, 32
+    b1 = synth.make_batch(24, 0, [N] * B, hk=hk, hv=hv)
+    b2 = synth.make_batch(25, 0, [N] * B, hk=hk, hv=hv)
+    g1, g2 = b1.to(cuda), b2.to(cuda)
+    rows = B * N
+    k1 = torch.zeros(hk, rows, 128, device=cuda)
+    v1 = torch.zeros(hv, rows, 128, device=cuda)
+    G1 = torch.zeros(hv, rows, device=cuda)
+    pool_a = b1.state.clone().to(cuda)
+    ts1 = ops.tree_struct(g1.parent, 4, batch=B, n_nodes=N, want=("anc_bits",))["anc_bits"]
+    ts2 = ops.tree_struct(g2.parent, 4, batch=B, n_nodes=N, want=("anc_bits",))["anc_bits"]
+    ops.tree_verify(g1.y, g1.a, g1.b, g1.A_log, g1.dt_bias, pool_a.transpose(-1, -2), hk=hk, hv=hv, anc_bits=ts1,
+                    batch=B, n_nodes=N, aux_k=k1, aux_v=v1, aux_g=G1, aux_k_per_khead=True)
+    pool_b = pool_a.clone()
+    idx, lens, _ = _paths(b1, 9)
+    idx_d, lens_d = idx.to(cuda), lens.to(cuda)
+    outs = []
+    for fused, pool in ((True, pool_a), (False, pool_b)):
+        aux = (torch.zeros(hk, rows, 128, device=cuda), torch.zeros(hv, rows, 128, device=cuda),
+               torch.zeros(hv, rows, device=cuda))
+        common = dict(hk=hk, hv=hv, anc_bits=ts2, batch=B, n_nodes=N, aux_k=aux[0], aux_v=aux[1], aux_g=aux[2],
+                      aux_k_per_khead=True)
+        if fused:
+            o = ops.tree_commit_verify(g2.y, g2.a, g2.b, g2.A_log, g2.dt_bias, pool.transpose(-1, -2),
+                                       pending_path=idx_d, pending_keys=k1, pending_values=v1, pending_gains=G1,
+                                       pending_path_len=lens_d, prev_n_nodes=N, pending_k_head_div=hv // hk,
+                                       **common)
+        else:
+            ops.tree_commit(pool.unsqueeze(0), k1.unsqueeze(0), v1.unsqueeze(0), G1.unsqueeze(0), idx_d, n_nodes=N,
+                            path_len=lens_d, k_head_div=hv // hk)
+            o = ops.tree_verify(g2.y, g2.a, g2.b, g2.A_log, g2.dt_bias, pool.transpose(-1, -2), **common)
+        outs.append((o, aux))
+    torch.cuda.synchronize()
+    assert rel_l2(np32(pool_a), np32(pool_b)) <= 1e-6
+    (oa, auxa), (ob, auxb) = outs
+    assert rel_l2(np32(oa), np32(ob)) <= 1e-5
+    for x, y in zip(auxa, auxb):
+        assert rel_l2(np32(x), np32(y)) <= 1e-6
