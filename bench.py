@@ -3,16 +3,23 @@
 Workload (the state-bandwidth-bound stacked step): 24 GDN layers, batch 64,
 one random recursive 32-node tree per request, 16 q/k heads, 32 v heads,
 dk = dv = 128, a distinct fp32 2 MiB state per request per layer (3 GiB).
-One step = the tree verify of all 24 layers (one launch per layer, as the
-model runs them) followed by the closed-form in-place commit of every
-request's accepted root-to-node path (length 1-16) for all 24 layers (one
-launch).  Inputs are resident in HBM before timing starts.
+Every step verifies each layer's trees and commits each request's accepted
+root-to-node path (length 1-16) into its state, for all 24 layers.  Two
+schedules of that work are timed:
 
-Printed: one JSON line.  ``value`` = verified nodes / s / layer
-= batch * nodes / (step time / 24).  ``roofline`` is for the kernel with the
-most time per step, from HIP-event timing of that kernel alone;
-``cpu_baseline`` times the CPU oracle (numpy, the fp32 restatement of the
-reference recurrence) on one layer of the same workload.
+* pipelined (``value``): one launch per layer of dft_tree_commit_verify,
+  which commits the previous step's accepted path into the state tile as it
+  streams in, writes the committed tile back and verifies this step's tree
+  on it (steady state: one commit and one verify per layer and step);
+* separate: one dft_tree_verify launch per layer, then one dft_tree_commit
+  launch for all layers, as the reference's hooks order them.
+
+Inputs are resident in HBM before timing starts.  Printed: one JSON line.
+``value`` = verified nodes / s / layer = batch * nodes / (step time / 24).
+``roofline`` is for the kernel with the most time per step, from HIP-event
+timing of that kernel alone; ``cpu_baseline`` times the CPU oracle (numpy,
+the fp32 restatement of the reference recurrence) on one layer of the same
+workload.
 """
 from __future__ import annotations
 
@@ -75,6 +82,9 @@ class Workload:
         self.keys = torch.empty(L, HK, rows, D, device=dev)   # one key set per k-head
         self.vals = torch.empty(L, HV, rows, D, device=dev)
         self.gains = torch.empty(L, HV, rows, device=dev)
+        # the pipelined schedule reads the previous step's saves from one set
+        # and writes this step's into the other
+        self.keys2, self.vals2, self.gains2 = (torch.empty_like(t) for t in (self.keys, self.vals, self.gains))
 
     def verify(self, l):
         from dforktree_amd import ops
@@ -90,6 +100,19 @@ class Workload:
         for l in range(L):
             self.verify(l)
         self.commit()
+
+    def fused(self, l):
+        from dforktree_amd import ops
+        ops.tree_commit_verify(self.y[l], self.a[l], self.b[l], self.A_log, self.dt_bias,
+                               self.state[l].transpose(-1, -2), hk=HK, hv=HV, anc_bits=self.anc_bits, batch=B,
+                               n_nodes=N, neg_exp_A=self.neg, o=self.o[l], aux_k=self.keys2[l], aux_v=self.vals2[l],
+                               aux_g=self.gains2[l], aux_k_per_khead=True, pending_path=self.accept,
+                               pending_keys=self.keys[l], pending_values=self.vals[l], pending_gains=self.gains[l],
+                               prev_n_nodes=N, pending_k_head_div=HV // HK)
+
+    def fused_step(self):
+        for l in range(L):
+            self.fused(l)
 
     def conv_setup(self, dev, seed=5):
         """Front end of one layer: tree-parent conv1d (width 4, SiLU) over the
@@ -127,6 +150,16 @@ class Workload:
                    + HK * N * D * 4)       # normalised k fp32 write (per k-head)
         return B * per_req
 
+    def fused_bytes_per_launch(self):
+        """verify bytes + the committed tile written back + the path's saves"""
+        tot = 0
+        for ell in self.path_lens:
+            tot += (HV * D * D * 4                # state write
+                    + ell * (HK + HV) * D * 4     # path keys (per k-head) and values
+                    + ell * HV * 4                # path gains
+                    + MAX_PATH * 4)               # path indices
+        return self.verify_bytes_per_launch() + tot
+
     def commit_bytes_per_launch(self):
         tot = 0
         for ell in self.path_lens:
@@ -137,7 +170,10 @@ class Workload:
         return L * tot
 
     def state_bytes_per_step(self):
-        return L * B * 3 * HV * D * D * 4   # verify read + commit read and write
+        return L * B * 3 * HV * D * D * 4   # verify read + commit read and write, as the separate kernels need
+
+    def state_bytes_moved_pipelined(self):
+        return L * B * 2 * HV * D * D * 4   # one read and one write per request-layer
 
 
 def time_graph(fn, reps, warmup, eager=False):
@@ -228,10 +264,17 @@ def main():
     torch.cuda.synchronize()
 
     reps_kernel = max(args.steps, 10)
+    # the separate schedule first: it fills both save sets the pipelined one reads
     t_verify_layers = time_graph(lambda: [w.verify(l) for l in range(L)], reps_kernel, args.warmup, args.eager)
     t_verify = t_verify_layers / L
     t_commit = time_graph(w.commit, reps_kernel, args.warmup, args.eager)
-    t_step = time_graph(w.step, args.steps, args.warmup, args.eager)
+    t_step_sep = time_graph(w.step, args.steps, args.warmup, args.eager)
+    for l in range(L):
+        w.verify(l)
+    torch.cuda.synchronize()
+    t_fused_layers = time_graph(lambda: [w.fused(l) for l in range(L)], reps_kernel, args.warmup, args.eager)
+    t_fused = t_fused_layers / L
+    t_step = time_graph(w.fused_step, args.steps, args.warmup, args.eager)
     w.conv_setup(dev)
     t_conv = time_graph(w.conv, reps_kernel, args.warmup, args.eager)
     if args.copy_calibration:
@@ -242,11 +285,8 @@ def main():
         torch.cuda.synchronize()
         del src, dst
 
-    vb, cb = w.verify_bytes_per_launch(), w.commit_bytes_per_launch()
-    kernels = {
-        "tree_verify_kernel": dict(ms=t_verify, bytes=vb, per_step=L),
-        "tree_commit_kernel": dict(ms=t_commit, bytes=cb, per_step=1),
-    }
+    vb, cb, fb = w.verify_bytes_per_launch(), w.commit_bytes_per_launch(), w.fused_bytes_per_launch()
+    kernels = {"tree_commit_verify_kernel": dict(ms=t_fused, bytes=fb, per_step=L)}
     dom = max(kernels, key=lambda k: kernels[k]["ms"] * kernels[k]["per_step"])
     kd = kernels[dom]
     achieved = kd["bytes"] / (kd["ms"] * 1e-3) / 1e9
@@ -258,7 +298,7 @@ def main():
         except (ValueError, OSError):
             traffic = None
     value = B * N / (t_step * 1e-3 / L)
-    state_gbs = w.state_bytes_per_step() / ((L * t_verify + t_commit) * 1e-3) / 1e9
+    frac = lambda nbytes, ms: round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)  # noqa: E731
     out = {
         "metric": "GDN tree-verify nodes/sec/layer (bs64, 32-node tree) + % HBM peak",
         "value": round(value, 1),
@@ -274,18 +314,24 @@ def main():
         "data": "synthetic",
         "config": {"workload": "stacked GDN tree verify + accepted-path commit", "batch": B, "nodes": N,
                    "layers": L, "qk_heads": HK, "v_heads": HV, "dk": D, "dv": D, "tree": "random recursive",
-                   "accepted_path": "random walk, length 1-16", "timing": "eager" if args.eager else "hip graph"},
+                   "accepted_path": "random walk, length 1-16",
+                   "schedule": "pipelined: each layer's launch commits the previous step's path, then verifies",
+                   "timing": "eager" if args.eager else "hip graph"},
         "roofline": {"kernel": dom, "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "algorithmic_bytes_per_launch": kd["bytes"]},
-        "verify_us_per_layer": round(t_verify * 1e3, 2),
-        "verify_hbm_frac": round(vb / (t_verify * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-        "commit_ms": round(t_commit, 4),
-        "commit_hbm_frac": round(cb / (t_commit * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-        "state_traffic_hbm_frac": round(state_gbs / HBM_PEAK_GBS, 4),
+        "commit_verify_us_per_layer": round(t_fused * 1e3, 2),
+        # state bytes the separate kernels need (verify read + commit read and write) per unit time,
+        # and the state bytes the pipelined schedule actually moves (one read + one write)
+        "state_traffic_hbm_frac": frac(w.state_bytes_per_step(), t_step),
+        "state_moved_hbm_frac": frac(w.state_bytes_moved_pipelined(), t_step),
+        "separate": {"ms_per_step": round(t_step_sep, 4), "value": round(B * N / (t_step_sep * 1e-3 / L), 1),
+                     "verify_us_per_layer": round(t_verify * 1e3, 2), "verify_hbm_frac": frac(vb, t_verify),
+                     "commit_ms": round(t_commit, 4), "commit_hbm_frac": frac(cb, t_commit),
+                     "state_traffic_hbm_frac": frac(w.state_bytes_per_step(), L * t_verify + t_commit)},
         "verify_only_nodes_per_s_per_layer": round(B * N / (t_verify * 1e-3), 1),
         "conv_us_per_layer": round(t_conv * 1e3, 2),
-        "conv_hbm_frac": round(w.conv_bytes_per_launch() / (t_conv * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "conv_hbm_frac": frac(w.conv_bytes_per_launch(), t_conv),
     }
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(args.cpu_seconds)

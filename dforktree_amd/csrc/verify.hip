@@ -353,9 +353,9 @@ __device__ __forceinline__ void store_state(float* S, int64_t v_stride, int wave
   }
 }
 
+// The body of both verify kernels (COMMIT: the fused commit -> verify form).
 template <int NP, bool S0VEC, bool COMMIT>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NP == 32 ? (COMMIT ? 3 : 4) : 1)))
-tree_verify_kernel(const VerifyParams P) {
+__device__ __forceinline__ void verify_body(const VerifyParams& P) {
   constexpr int MT = NP / 16;  // 16-node tiles
   constexpr int KS = NP / 32;  // 32-node k-steps of phase 3
   constexpr int LDA = VerifySmem<NP, COMMIT>::LDA;
@@ -827,6 +827,18 @@ tree_verify_kernel(const VerifyParams P) {
   }
 }
 
+template <int NP, bool S0VEC>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NP == 32 ? 4 : 1)))
+tree_verify_kernel(const VerifyParams P) {
+  verify_body<NP, S0VEC, false>(P);
+}
+
+template <int NP>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NP == 32 ? 3 : 1)))
+tree_commit_verify_kernel(const VerifyParams P) {
+  verify_body<NP, true, true>(P);
+}
+
 static VerifyParams make_params(const dft_verify_args* a) {
   VerifyParams P;
   P.a = *a;
@@ -848,14 +860,14 @@ int launch_tree_verify(const dft_verify_args* a, hipStream_t stream) {
   const dim3 grid((unsigned)(a->batch * a->hv)), block(256);
   if (a->n_nodes <= 32) {
     if (P.s0_vec)
-      hipLaunchKernelGGL((tree_verify_kernel<32, true, false>), grid, block, 0, stream, P);
+      hipLaunchKernelGGL((tree_verify_kernel<32, true>), grid, block, 0, stream, P);
     else
-      hipLaunchKernelGGL((tree_verify_kernel<32, false, false>), grid, block, 0, stream, P);
+      hipLaunchKernelGGL((tree_verify_kernel<32, false>), grid, block, 0, stream, P);
   } else {
     if (P.s0_vec)
-      hipLaunchKernelGGL((tree_verify_kernel<64, true, false>), grid, block, 0, stream, P);
+      hipLaunchKernelGGL((tree_verify_kernel<64, true>), grid, block, 0, stream, P);
     else
-      hipLaunchKernelGGL((tree_verify_kernel<64, false, false>), grid, block, 0, stream, P);
+      hipLaunchKernelGGL((tree_verify_kernel<64, false>), grid, block, 0, stream, P);
   }
   return hipGetLastError() == hipSuccess ? DFT_OK : DFT_ERR_LAUNCH;
 }
@@ -866,9 +878,9 @@ int launch_tree_commit_verify(const dft_verify_args* a, const dft_pending_commit
   P.c = *c;
   const dim3 grid((unsigned)(a->batch * a->hv)), block(256);
   if (a->n_nodes <= 32)
-    hipLaunchKernelGGL((tree_verify_kernel<32, true, true>), grid, block, 0, stream, P);
+    hipLaunchKernelGGL((tree_commit_verify_kernel<32>), grid, block, 0, stream, P);
   else
-    hipLaunchKernelGGL((tree_verify_kernel<64, true, true>), grid, block, 0, stream, P);
+    hipLaunchKernelGGL((tree_commit_verify_kernel<64>), grid, block, 0, stream, P);
   return hipGetLastError() == hipSuccess ? DFT_OK : DFT_ERR_LAUNCH;
 }
 
