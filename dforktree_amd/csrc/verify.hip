@@ -353,25 +353,25 @@ __device__ __forceinline__ void store_state(float* S, int64_t v_stride, int wave
   }
 }
 
-// The body of both verify kernels (COMMIT: the fused commit -> verify form).
-template <int NP, bool S0VEC, bool COMMIT>
-__device__ __forceinline__ void verify_body(const VerifyParams& P) {
-  constexpr int MT = NP / 16;  // 16-node tiles
-  constexpr int KS = NP / 32;  // 32-node k-steps of phase 3
-  constexpr int LDA = VerifySmem<NP, COMMIT>::LDA;
-  constexpr int kPend = COMMIT ? kPendLoads : 0;  // vector-memory ops issued after the state
-  const dft_verify_args& p = P.a;
-  __shared__ VerifySmem<NP, COMMIT> sm;
+// ---------------------------------------------------------------------------
+// the verify, phase by phase.  RW holds the q/k/v rows (q, k, v), WK the
+// per-head O(N^2) work arrays (am, pq, x, gc, G, beta, rq, rk, cO, anc); the
+// caller places the barriers between phases.
+// ---------------------------------------------------------------------------
+// One (request, v-head) of a launch.
+struct Item {
+  int b, hk, rr, h;  // request, k-head, v-head within the k-head, v-head
+  int n;             // nodes (0: nothing to verify)
+  int64_t row0;      // row of node 0
+  const float* S0;   // the head's state tile (k stride 1 on the vector paths)
+};
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int n16 = lane & 15, g4 = lane >> 4;
-
-  // ---- block -> (request b, v-head h); the R v-heads sharing a k-head get
-  // block ids 8 apart so that they land on the same XCD (shared q/k in L2).
+// block id -> (request, v-head); the R v-heads sharing a k-head get ids 8
+// apart so that they land on the same XCD (shared q/k rows in its L2)
+__device__ __forceinline__ void item_heads(const dft_verify_args& p, int id, Item& it) {
   const int R = p.hv / p.hk;
   const int pairs = p.batch * p.hk;
   const int full = (pairs / 8) * 8 * R;
-  const int id = blockIdx.x;
   int pair, rr;
   if (id < full) {
     const int grp = id / (8 * R), rem = id - grp * 8 * R;
@@ -382,171 +382,135 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
     pair = (pairs / 8) * 8 + t / R;
     rr = t % R;
   }
-  const int b = pair / p.hk, hk = pair - b * p.hk, h = hk * R + rr;
+  it.b = pair / p.hk;
+  it.hk = pair - it.b * p.hk;
+  it.rr = rr;
+  it.h = it.hk * R + rr;
+}
 
-  int64_t row0;
-  int n;
+// rows, node count and state tile of a request (loads the index arrays)
+template <int NP>
+__device__ __forceinline__ void item_rows(const dft_verify_args& p, Item& it) {
   if (p.cu_seqlens) {
-    row0 = p.cu_seqlens[b];
-    n = p.cu_seqlens[b + 1] - p.cu_seqlens[b];
+    it.row0 = p.cu_seqlens[it.b];
+    it.n = p.cu_seqlens[it.b + 1] - p.cu_seqlens[it.b];
   } else {
-    row0 = (int64_t)b * p.n_nodes;
-    n = p.n_nodes;
+    it.row0 = (int64_t)it.b * p.n_nodes;
+    it.n = p.n_nodes;
   }
-  n = n < 0 ? 0 : (n > NP ? NP : n);
-
-  int64_t slot = b;
+  it.n = it.n < 0 ? 0 : (it.n > NP ? NP : it.n);
+  int64_t slot = it.b;
   if (p.state_indices) {
-    slot = ld_i(p.state_indices, b, p.state_indices_dtype);
+    slot = ld_i(p.state_indices, it.b, p.state_indices_dtype);
     if (slot < 0) slot = 0;
   }
-  const float* S0 = p.state + slot * p.state_slot_stride + (int64_t)h * p.state_h_stride;
-  PendingHead ph{};
-  if constexpr (COMMIT) ph = pending_head(P.c, b);
-  Pending pd;
-  float vnr[4][2], gp[4];
-  f32x4 kr[2];
-  if constexpr (COMMIT) {
-    copy_path_words(P.c, b, lane, sm.pent[wave]);  // the wave's first load: no wait below depends on its count
-    if (n == 0) {  // nothing to verify this step: the commit alone
-      __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 15));
-      pd = decode_pending(ph, lane, sm.pent[wave][lane]);
-      if (pd.last < 0) return;
-      f32x4 s0r[2][8];
-#pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        const float* rowp = S0 + (int64_t)(32 * wave + 16 * t + n16) * p.state_v_stride + 4 * g4;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) s0r[t][j] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(rowp + 16 * j));
-      }
-      issue_pending(P.c, pd, h, wave, lane, S0, kr, vnr, gp);
-      stage_pending_keys(sm.pkey, kr, wave, lane);
-      __syncthreads();
-      apply_pending(pd, sm.pkey, vnr, gp, lane, s0r);
-      store_state(const_cast<float*>(S0), p.state_v_stride, wave, lane, s0r);
-      return;
-    }
-  }
-  if (n == 0) return;
+  it.S0 = p.state + slot * p.state_slot_stride + (int64_t)it.h * p.state_h_stride;
+}
 
-  // ---- 0. issue order (vector memory returns in order): the gates and
-  // ancestry bits (wave 0), the q/k/v rows straight into LDS, then the 64 KiB
-  // state tile into registers.  Phase 1 only waits for what precedes the
-  // state; the state keeps streaming underneath it.  The loads before the
-  // state are unconditional and undecoded (clamped indices, pointer selects,
-  // whole words) so that nothing reads them, and waits, before the state is
-  // issued.
-  // wave 0's lane i fetches node i's gate words and ancestry bits (rows past
-  // the tree repeat the last node; decoded after the state is issued)
-  uint32_t sha = 0, shb = 0, shdt = 0, shdec = 0;
-  if (wave == 0) {
-    const int64_t gi = row0 + (lane < n ? lane : n - 1);
-    lds_dma4(word_of(p.a, gi * p.a_row_stride + h, p.a_dtype, sha), sm.graw[0]);
-    lds_dma4(word_of(p.b, gi * p.b_row_stride + h, p.b_dtype, shb), sm.graw[1]);
-    const uint32_t* bits = p.anc_bits ? reinterpret_cast<const uint32_t*>(p.anc_bits + gi)
-                                      : static_cast<const uint32_t*>(p.y);
-    lds_dma4(bits, sm.graw[2]);
-    lds_dma4(bits + 1, sm.graw[3]);
-    lds_dma4(word_of(p.dt_bias, h, p.dt_bias_dtype, shdt), sm.graw[4]);
-    lds_dma4(word_of(p.neg_exp_A ? static_cast<const void*>(p.neg_exp_A) : p.A_log, h,
-                     p.neg_exp_A ? (int)DFT_F32 : p.A_log_dtype, shdec),
-             sm.graw[5]);
+// Wave 0's lane i fetches node i's gate words and ancestry bits into graw
+// (rows past the tree repeat the last node).  The words are whole aligned
+// 32-bit words, decoded later, so nothing waits on them before the state is
+// issued.  `alt` replaces every source when the request has no rows.
+__device__ __forceinline__ void issue_gates(const dft_verify_args& p, const Item& it, int lane, const void* alt,
+                                            uint32_t (*graw)[64]) {
+  uint32_t sh;
+  const int64_t gi = it.row0 + (lane < it.n ? lane : it.n - 1);
+  const bool ok = it.n > 0;
+  lds_dma4(ok ? word_of(p.a, gi * p.a_row_stride + it.h, p.a_dtype, sh) : alt, graw[0]);
+  lds_dma4(ok ? word_of(p.b, gi * p.b_row_stride + it.h, p.b_dtype, sh) : alt, graw[1]);
+  const uint32_t* bits = (ok && p.anc_bits) ? reinterpret_cast<const uint32_t*>(p.anc_bits + gi)
+                                            : static_cast<const uint32_t*>(alt);
+  lds_dma4(bits, graw[2]);
+  lds_dma4(bits + 1, graw[3]);
+  lds_dma4(word_of(p.dt_bias, it.h, p.dt_bias_dtype, sh), graw[4]);
+  lds_dma4(word_of(p.neg_exp_A ? static_cast<const void*>(p.neg_exp_A) : p.A_log, it.h,
+                   p.neg_exp_A ? (int)DFT_F32 : p.A_log_dtype, sh),
+           graw[5]);
+}
+
+// gates of node `lane` from graw (wave 0, lanes < NP): g, beta, ancestry
+template <class WK>
+__device__ __forceinline__ void decode_gates(const dft_verify_args& p, const Item& it, int lane,
+                                             const uint32_t (*graw)[64], WK& wk) {
+  uint32_t sha, shb, shdt, shdec;
+  const int64_t gi = it.row0 + (lane < it.n ? lane : it.n - 1);
+  word_of(p.a, gi * p.a_row_stride + it.h, p.a_dtype, sha);
+  word_of(p.b, gi * p.b_row_stride + it.h, p.b_dtype, shb);
+  word_of(p.dt_bias, it.h, p.dt_bias_dtype, shdt);
+  word_of(p.neg_exp_A ? static_cast<const void*>(p.neg_exp_A) : p.A_log, it.h,
+          p.neg_exp_A ? (int)DFT_F32 : p.A_log_dtype, shdec);
+  const int i = lane;
+  float gv = 0.f, bv = 0.f;
+  if (i < it.n) {
+    const float a = word_to_f(graw[0][i], sha, p.a_dtype) + word_to_f(graw[4][i], shdt, p.dt_bias_dtype);
+    const float sp = a > 20.f ? a : logf(1.f + expf(fminf(a, 20.f)));
+    const uint32_t wdec = graw[5][i];
+    const float dec = p.neg_exp_A ? __uint_as_float(wdec) : -expf(word_to_f(wdec, shdec, p.A_log_dtype));
+    gv = dec * sp;
+    bv = 1.f / (1.f + expf(-word_to_f(graw[1][i], shb, p.b_dtype)));
   }
-  if (p.anc_f32) {  // dense ancestry: rows become bit masks right away
-    const float* ab = p.anc_f32 + (int64_t)b * p.anc_req_stride;
-    for (int i = wave; i < NP; i += 4) {
-      const float v = (i < n && lane < n) ? ab[i * p.anc_row_stride + lane] : 0.f;
-      const uint64_t bits = __ballot(v > 0.5f);
-      if (lane == 0) sm.anc[i] = bits & mask_upto(i);
-    }
+  wk.gc[i] = gv;
+  wk.beta[i] = bv;
+  if (p.anc_bits) {
+    const uint64_t bits = ((uint64_t)graw[3][i] << 32) | graw[2][i];
+    wk.anc[i] = i < it.n ? (bits & mask_upto(i) & mask_below(it.n)) : 0ull;
   }
-  constexpr int kQkvDma = 3 * (NP / 16);  // row copies per wave
+}
+
+// dense ancestry rows become bit masks (loads and waits right away: only the
+// dense form, used by the batch-1 drop-in, takes this path)
+template <int NP, class WK>
+__device__ __forceinline__ void dense_ancestry(const dft_verify_args& p, const Item& it, int wave, int lane, WK& wk) {
+  const float* ab = p.anc_f32 + (int64_t)it.b * p.anc_req_stride;
+  for (int i = wave; i < NP; i += 4) {
+    const float v = (i < it.n && lane < it.n) ? ab[i * p.anc_row_stride + lane] : 0.f;
+    const uint64_t bits = __ballot(v > 0.5f);
+    if (lane == 0) wk.anc[i] = bits & mask_upto(i);
+  }
+}
+
+// q/k/v rows -> LDS: one 1 KiB copy fills 4 swizzled rows (3 * NP/16 per wave)
+template <int NP, class RW>
+__device__ __forceinline__ void issue_rows(const dft_verify_args& p, const Item& it, int wave, int lane,
+                                           const void* alt, RW& rw) {
   const int KD = p.hk * kD;
   const int64_t ys = p.y_row_stride;
-  {
-    const uint16_t* ybase = reinterpret_cast<const uint16_t*>(p.y) + row0 * ys;
-    const uint16_t* srcs[3] = {ybase + hk * kD, ybase + KD + hk * kD, ybase + 2 * KD + h * kD};
-    uint16_t* dsts[3] = {sm.q, sm.k, sm.v};
-    const int pc = lane & 15;
+  const uint16_t* ybase = reinterpret_cast<const uint16_t*>(p.y) + it.row0 * ys;
+  const uint16_t* srcs[3] = {ybase + it.hk * kD, ybase + KD + it.hk * kD, ybase + 2 * KD + it.h * kD};
+  uint16_t* dsts[3] = {rw.q, rw.k, rw.v};
+  const int pc = lane & 15;
 #pragma unroll
-    for (int u = 0; u < NP / 16; ++u) {
-      const int blk = wave + 4 * u;  // rows 4 blk .. 4 blk + 3
-      const int i = 4 * blk + (lane >> 4);
-      const int isrc = i < n ? i : n - 1;  // rows past the tree repeat a real row (finite, masked later)
-      const int64_t goff = isrc * ys + 8 * ((pc ^ i) & 15);
+  for (int u = 0; u < NP / 16; ++u) {
+    const int blk = wave + 4 * u;  // rows 4 blk .. 4 blk + 3
+    const int i = 4 * blk + (lane >> 4);
+    const int isrc = i < it.n ? i : it.n - 1;  // rows past the tree repeat a real row (finite, masked later)
+    const int64_t goff = isrc * ys + 8 * ((pc ^ i) & 15);
 #pragma unroll
-      for (int m = 0; m < 3; ++m) lds_dma16(srcs[m] + goff, dsts[m] + 4 * blk * kD);
-    }
+    for (int m = 0; m < 3; ++m)
+      lds_dma16(it.n > 0 ? static_cast<const void*>(srcs[m] + goff) : alt, dsts[m] + 4 * blk * kD);
   }
-  asm volatile("" ::: "memory");
+}
 
-  // s0r[t][j] = S0[k = 16j + 4g + e][v = 32w + 16t + n]
-  f32x4 s0r[2][8];
-  if (S0VEC) {
+// s0r[t][j] = S0[k = 16j + 4g + e][v = 32w + 16t + n]: 16 non-temporal
+// 16-byte loads per lane, 4 lanes per 64-byte sector
+__device__ __forceinline__ void issue_state(const float* S0, int64_t v_stride, int wave, int lane, f32x4 (&s0r)[2][8]) {
+  const int n16 = lane & 15, g4 = lane >> 4;
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      const float* rowp = S0 + (int64_t)(32 * wave + 16 * t + n16) * p.state_v_stride + 4 * g4;
+  for (int t = 0; t < 2; ++t) {
+    const float* rowp = S0 + (int64_t)(32 * wave + 16 * t + n16) * v_stride + 4 * g4;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) s0r[t][j] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(rowp + 16 * j));
-    }
-  } else {
-#pragma unroll
-    for (int t = 0; t < 2; ++t)
-#pragma unroll
-      for (int j = 0; j < 8; ++j)
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-          s0r[t][j][e] = S0[(int64_t)(32 * wave + 16 * t + n16) * p.state_v_stride +
-                            (int64_t)(16 * j + 4 * g4 + e) * p.state_k_stride];
-    __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 15));  // element loads: no overlap on this path
+    for (int j = 0; j < 8; ++j) s0r[t][j] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(rowp + 16 * j));
   }
-  asm volatile("" ::: "memory");
-  if constexpr (COMMIT) {
-    // the path word was this wave's first load; at most the row copies and
-    // the state may still be in flight (wave 0 also issued 6 gate copies,
-    // which land right behind the path word)
-    __builtin_amdgcn_s_waitcnt(waitcnt_imm(kQkvDma + 16, 15));
-    pd = decode_pending(ph, lane, sm.pent[wave][lane]);
-    issue_pending(P.c, pd, h, wave, lane, S0, kr, vnr, gp);
-    asm volatile("" ::: "memory");
-  }
+}
 
-  if (wave == 0) {
-    // the gate words were wave 0's first loads: wait for them only
-    __builtin_amdgcn_s_waitcnt(waitcnt_imm(kQkvDma + 16 + kPend, 15));
-    asm volatile("" ::: "memory");
-    if (lane < NP) {
-      const int i = lane;
-      float gi = 0.f, bi = 0.f;
-      if (i < n) {
-        const float a = word_to_f(sm.graw[0][i], sha, p.a_dtype) + word_to_f(sm.graw[4][i], shdt, p.dt_bias_dtype);
-        const float sp = a > 20.f ? a : logf(1.f + expf(fminf(a, 20.f)));
-        const uint32_t wdec = sm.graw[5][i];
-        const float dec = p.neg_exp_A ? __uint_as_float(wdec) : -expf(word_to_f(wdec, shdec, p.A_log_dtype));
-        gi = dec * sp;
-        bi = 1.f / (1.f + expf(-word_to_f(sm.graw[1][i], shb, p.b_dtype)));
-      }
-      sm.gc[i] = gi;
-      sm.beta[i] = bi;
-      if (p.anc_bits) {
-        const uint64_t bits = ((uint64_t)sm.graw[3][i] << 32) | sm.graw[2][i];
-        sm.anc[i] = i < n ? (bits & mask_upto(i) & mask_below(n)) : 0ull;
-      }
-    }
-  }
-  // Wait for the row loads and gates (everything issued before the state),
-  // then make the LDS writes of all waves visible.  A plain __syncthreads()
-  // here would also drain the state loads.
-  __builtin_amdgcn_s_waitcnt(waitcnt_imm(16 + kPend, 0));
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
-
-  // ---- 1a. row norms (4 threads per q/k row) and path-cumulative decay
-  // (256 / NP threads per node), spread over all four waves.
+// 1a: row norms (4 threads per q/k row) and the path-cumulative decay
+// (256 / NP threads per node), spread over all four waves
+template <int NP, class RW, class WK>
+__device__ __forceinline__ void phase_norms(const dft_verify_args& p, int tid, const RW& rw, WK& wk) {
 #pragma unroll
   for (int r0 = 0; r0 < 2 * NP; r0 += 64) {
     const int r = r0 + (tid >> 2), qd = tid & 3, i = r % NP;
-    const uint16_t* rows = r < NP ? sm.q : sm.k;
+    const uint16_t* rows = r < NP ? rw.q : rw.k;
     float ss = 0.f;
 #pragma unroll
     for (int c = 32 * qd; c < 32 * qd + 32; c += 8) {
@@ -562,34 +526,39 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
     ss += __shfl_xor(ss, 2);
     if (qd == 0) {
       const float rn = rsqrtf(ss + 1e-6f);
-      if (r < NP) sm.rq[i] = rn * p.scale;
-      else sm.rk[i] = rn;
+      if (r < NP) wk.rq[i] = rn * p.scale;
+      else wk.rk[i] = rn;
     }
   }
-  {
-    constexpr int TPN = 256 / NP;  // threads per node
-    const int i = tid / TPN, sub = tid % TPN;
-    const uint64_t bits = sm.anc[i];
-    float G = 0.f;
+  constexpr int TPN = 256 / NP;  // threads per node
+  const int i = tid / TPN, sub = tid % TPN;
+  const uint64_t bits = wk.anc[i];
+  float G = 0.f;
 #pragma unroll
-    for (int jj = 0; jj < NP / TPN; ++jj) {
-      const int j = jj * TPN + sub;
-      if ((bits >> j) & 1ull) G += sm.gc[j];
-    }
-#pragma unroll
-    for (int o = 1; o < TPN; o <<= 1) G += __shfl_xor(G, o);
-    if (sub == 0) sm.G[i] = G;
+  for (int jj = 0; jj < NP / TPN; ++jj) {
+    const int j = jj * TPN + sub;
+    if ((bits >> j) & 1ull) G += wk.gc[j];
   }
-  __syncthreads();
+#pragma unroll
+  for (int o = 1; o < TPN; o <<= 1) G += __shfl_xor(G, o);
+  if (sub == 0) wk.G[i] = G;
+}
 
-  // ---- 1b. saves for the commit, output row scales, Gram tiles
+// 1b: saves for the commit (normalised keys, G), output row scales, and the
+// ancestor-masked Gram tiles A (transposed into am) and Pq
+template <int NP, class RW, class WK>
+__device__ __forceinline__ void phase_gram(const VerifyParams& P, const Item& it, int tid, const RW& rw, WK& wk) {
+  constexpr int MT = NP / 16;
+  constexpr int LDA = WK::LDA;
+  const dft_verify_args& p = P.a;
+  const int lane = tid & 63, wave = tid >> 6, n16 = lane & 15, g4 = lane >> 4;
   const bool per_khead = (p.flags & DFT_VERIFY_AUX_K_PER_KHEAD) != 0;
-  if (p.aux_k && (!per_khead || rr == 0)) {
-    float* dk = p.aux_k + (int64_t)(per_khead ? hk : h) * p.aux_k_h_stride + row0 * p.aux_k_row_stride;
-    for (int c = tid; c < n * 32; c += 256) {
+  if (p.aux_k && (!per_khead || it.rr == 0)) {
+    float* dk = p.aux_k + (int64_t)(per_khead ? it.hk : it.h) * p.aux_k_h_stride + it.row0 * p.aux_k_row_stride;
+    for (int c = tid; c < it.n * 32; c += 256) {
       const int i = c >> 5, d = (c & 31) * 4;
-      const uint2 u = *reinterpret_cast<const uint2*>(&sm.k[qkv_at(i, d)]);
-      const float r = sm.rk[i];
+      const uint2 u = *reinterpret_cast<const uint2*>(&rw.k[qkv_at(i, d)]);
+      const float r = wk.rk[i];
       const f32x4 val = {__uint_as_float(u.x << 16) * r, __uint_as_float(u.x & 0xffff0000u) * r,
                          __uint_as_float(u.y << 16) * r, __uint_as_float(u.y & 0xffff0000u) * r};
       float* dst = dk + i * p.aux_k_row_stride + d;
@@ -602,109 +571,112 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
     }
   }
   if (tid < NP) {
-    const float eG = __expf(sm.G[tid]);
-    sm.gc[tid] = eG * sm.rk[tid];  // g is no longer needed
-    sm.cO[tid] = eG * sm.rq[tid];
-    if (p.aux_g && tid < n) p.aux_g[(int64_t)h * p.aux_g_h_stride + (row0 + tid) * p.aux_g_row_stride] = sm.G[tid];
+    const float eG = __expf(wk.G[tid]);
+    wk.gc[tid] = eG * wk.rk[tid];  // g is no longer needed
+    wk.cO[tid] = eG * wk.rq[tid];
+    if (p.aux_g && tid < it.n)
+      p.aux_g[(int64_t)it.h * p.aux_g_h_stride + (it.row0 + tid) * p.aux_g_row_stride] = wk.G[tid];
   }
-  {
-    int item = 0;
+  int item = 0;
 #pragma unroll
-    for (int which = 0; which < 2; ++which)
+  for (int which = 0; which < 2; ++which)
 #pragma unroll
-      for (int it = 0; it < MT; ++it)
+    for (int ti = 0; ti < MT; ++ti)
 #pragma unroll
-        for (int jt = 0; jt <= it; ++jt, ++item) {
-          if ((item & 3) != wave) continue;
-          const uint16_t* left = which == 0 ? sm.k : sm.q;
-          f32x4 acc = {};
+      for (int tj = 0; tj <= ti; ++tj, ++item) {
+        if ((item & 3) != wave) continue;
+        const uint16_t* left = which == 0 ? rw.k : rw.q;
+        f32x4 acc = {};
 #pragma unroll
-          for (int s = 0; s < 4; ++s) {
-            const bf16x8 av = *reinterpret_cast<const bf16x8*>(left + qkv_at(16 * it + n16, 32 * s + 8 * g4));
-            const bf16x8 bv = *reinterpret_cast<const bf16x8*>(sm.k + qkv_at(16 * jt + n16, 32 * s + 8 * g4));
-            acc = mfma_bf16_16x16x32(av, bv, acc);
-          }
-          const int j = 16 * jt + n16;
-          const float rkj = sm.rk[j], Gj = sm.G[j];
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int i = 16 * it + 4 * g4 + r;
-            const bool on = (sm.anc[i] >> j) & 1ull;
-            if (which == 0)
-              sm.am[j * LDA + i] = (on && j < i) ? sm.beta[i] * sm.rk[i] * rkj * acc[r] * __expf(sm.G[i] - Gj) : 0.f;
-            else
-              sm.pq[i * LDA + j] = on ? sm.rq[i] * rkj * acc[r] * __expf(sm.G[i] - Gj) : 0.f;
-          }
+        for (int s = 0; s < 4; ++s) {
+          const bf16x8 av = *reinterpret_cast<const bf16x8*>(left + qkv_at(16 * ti + n16, 32 * s + 8 * g4));
+          const bf16x8 bv = *reinterpret_cast<const bf16x8*>(rw.k + qkv_at(16 * tj + n16, 32 * s + 8 * g4));
+          acc = mfma_bf16_16x16x32(av, bv, acc);
         }
-  }
-  __syncthreads();
+        const int j = 16 * tj + n16;
+        const float rkj = wk.rk[j], Gj = wk.G[j];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int i = 16 * ti + 4 * g4 + r;
+          const bool on = (wk.anc[i] >> j) & 1ull;
+          if (which == 0)
+            wk.am[j * LDA + i] = (on && j < i) ? wk.beta[i] * wk.rk[i] * rkj * acc[r] * __expf(wk.G[i] - Gj) : 0.f;
+          else
+            wk.pq[i * LDA + j] = on ? wk.rq[i] * rkj * acc[r] * __expf(wk.G[i] - Gj) : 0.f;
+        }
+      }
+}
 
-  // ---- 1c. diagonal blocks of X by forward substitution (block b on wave
-  // b, lane j = column, so the serial chains run on different SIMDs); X above
-  // the diagonal blocks is zeroed by everyone.
+// 1c: diagonal 16x16 blocks of X by forward substitution (block b on wave b,
+// lane j = column, so the serial chains run on different SIMDs); X above the
+// diagonal blocks is zeroed by everyone
+template <int NP, class WK>
+__device__ __forceinline__ void phase_diag(int tid, WK& wk) {
+  constexpr int MT = NP / 16;
+  constexpr int LDA = WK::LDA;
+  const int lane = tid & 63, wave = tid >> 6;
   if (wave < MT && lane < 16) {
     const int bb = wave, j = lane;
     float xc[16];
 #pragma unroll
     for (int i = 0; i < 16; ++i) xc[i] = (i == j) ? 1.f : 0.f;
-    solve_block16<LDA>(xc, sm.am, 16 * bb);
+    solve_block16<LDA>(xc, wk.am, 16 * bb);
     materialize16(xc);
 #pragma unroll
-    for (int i = 0; i < 16; ++i) sm.x[(16 * bb + i) * LDA + 16 * bb + j] = xc[i];
+    for (int i = 0; i < 16; ++i) wk.x[(16 * bb + i) * LDA + 16 * bb + j] = xc[i];
   }
   for (int e = tid; e < NP * NP; e += 256) {
     const int i = e / NP, jj = e % NP;
-    if ((i >> 4) < (jj >> 4)) sm.x[i * LDA + jj] = 0.f;
+    if ((i >> 4) < (jj >> 4)) wk.x[i * LDA + jj] = 0.f;
   }
-  __syncthreads();
+}
 
-  // ---- 1d. off-diagonal blocks X_ij = -D_i sum_{m=j}^{i-1} A_im X_mj, by
-  // distance d = i - j (each level needs the previous ones)
+// 1d, one level: off-diagonal blocks X_ij = -D_i sum_{m=j}^{i-1} A_im X_mj at
+// distance d = i - j (each level needs the previous ones)
+template <int NP, class WK>
+__device__ __forceinline__ void phase_offdiag(int tid, int d, WK& wk) {
+  constexpr int MT = NP / 16;
+  constexpr int LDA = WK::LDA;
+  const int lane = tid & 63, wave = tid >> 6, n16 = lane & 15, g4 = lane >> 4;
+  const int bj = wave, bi = wave + d;
+  if (bi < MT) {
+    f32x4 T = {};
 #pragma unroll
-  for (int d = 1; d < MT; ++d) {
-    const int bj = wave, bi = wave + d;
-    if (bi < MT) {
-      f32x4 T = {};
-#pragma unroll
-      for (int bm = 0; bm < MT; ++bm)
-        if (bm >= bj && bm < bi) T = block_mma<LDA, true>(T, sm.am, bi, bm, sm.x, bj, n16, g4);
-      store_block<LDA>(sm.x, bi, bj, neg_diag_times<LDA>(sm.x, bi, T, n16, g4), n16, g4);
-    }
-    __syncthreads();
+    for (int bm = 0; bm < MT; ++bm)
+      if (bm >= bj && bm < bi) T = block_mma<LDA, true>(T, wk.am, bi, bm, wk.x, bj, n16, g4);
+    store_block<LDA>(wk.x, bi, bj, neg_diag_times<LDA>(wk.x, bi, T, n16, g4), n16, g4);
   }
+}
 
-  // ---- 1e. M = Pq X (block lower triangular; overwrites A)
-  {
-    int blk = 0;
+// 1e: M = Pq X (block lower triangular; overwrites A)
+template <int NP, class WK>
+__device__ __forceinline__ void phase_m(int tid, WK& wk) {
+  constexpr int MT = NP / 16;
+  constexpr int LDA = WK::LDA;
+  const int lane = tid & 63, wave = tid >> 6, n16 = lane & 15, g4 = lane >> 4;
+  int blk = 0;
 #pragma unroll
-    for (int bi = 0; bi < MT; ++bi)
+  for (int bi = 0; bi < MT; ++bi)
 #pragma unroll
-      for (int bj = 0; bj < MT; ++bj, ++blk) {
-        if ((blk & 3) != wave) continue;
-        f32x4 acc = {};
-        if (bj <= bi) {
+    for (int bj = 0; bj < MT; ++bj, ++blk) {
+      if ((blk & 3) != wave) continue;
+      f32x4 acc = {};
+      if (bj <= bi) {
 #pragma unroll
-          for (int bm = 0; bm < MT; ++bm)
-            if (bm >= bj && bm <= bi) acc = block_mma<LDA, false>(acc, sm.pq, bi, bm, sm.x, bj, n16, g4);
-        }
-        store_block<LDA>(sm.am, bi, bj, acc, n16, g4);
+        for (int bm = 0; bm < MT; ++bm)
+          if (bm >= bj && bm <= bi) acc = block_mma<LDA, false>(acc, wk.pq, bi, bm, wk.x, bj, n16, g4);
       }
-  }
-
-  if constexpr (COMMIT) {
-    // the state, the path keys and the weights have landed: commit the
-    // previous step's path into the tile and write it back
-    stage_pending_keys(sm.pkey, kr, wave, lane);
-    __syncthreads();
-    if (pd.last >= 0) {
-      apply_pending(pd, sm.pkey, vnr, gp, lane, s0r);
-      store_state(const_cast<float*>(S0), p.state_v_stride, wave, lane, s0r);
+      store_block<LDA>(wk.am, bi, bj, acc, n16, g4);
     }
-  }
+}
 
-  // ---- 2. Cq = q_raw S0, Ck = k_raw S0 for the wave's 32 columns.  k-step s,
-  // lane group g, element e -> k = 32s + 4g + e (e < 4), 32s + 16 + 4g + e-4.
-  f32x4 cq[MT][2], ck[MT][2];
+// 2: Cq = q_raw S0, Ck = k_raw S0 for the wave's 32 columns.  k-step s, lane
+// group g, element e -> k = 32s + 4g + e (e < 4), 32s + 16 + 4g + e-4
+template <int NP, class RW>
+__device__ __forceinline__ void phase_cq_ck(int lane, const RW& rw, const f32x4 (&s0r)[2][8], f32x4 (&cq)[NP / 16][2],
+                                            f32x4 (&ck)[NP / 16][2]) {
+  constexpr int MT = NP / 16;
+  const int n16 = lane & 15, g4 = lane >> 4;
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
@@ -724,8 +696,8 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
       const int row = 16 * mt + n16, c0 = 32 * s + 4 * g4;
-      const bf16x8 aq = lds_bf16x8_split(sm.q + qkv_at(row, c0), sm.q + qkv_at(row, c0 + 16));
-      const bf16x8 ak = lds_bf16x8_split(sm.k + qkv_at(row, c0), sm.k + qkv_at(row, c0 + 16));
+      const bf16x8 aq = lds_bf16x8_split(rw.q + qkv_at(row, c0), rw.q + qkv_at(row, c0 + 16));
+      const bf16x8 ak = lds_bf16x8_split(rw.k + qkv_at(row, c0), rw.k + qkv_at(row, c0 + 16));
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
         cq[mt][t] = mfma_bf16_16x16x32(aq, bhi[t], cq[mt][t]);
@@ -735,12 +707,16 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
       }
     }
   }
-  __syncthreads();  // X and M complete
+}
 
-  // ---- 3. W = beta (v - e^G rk Ck) in the accumulator layout, split into
-  // bf16 hi/lo B operands: k-step ks, lane group g, element e -> node
-  // 32ks + 4g + e (e < 4), 32ks + 16 + 4g + e-4, i.e. registers of tiles 2ks, 2ks+1.
-  bf16x8 wh[KS][2], wl[KS][2];
+// 3a: W = beta (v - e^G rk Ck) in the accumulator layout, split into bf16
+// hi/lo B operands: k-step ks, lane group g, element e -> node 32ks + 4g + e
+// (e < 4), 32ks + 16 + 4g + e-4, i.e. registers of tiles 2ks, 2ks+1
+template <int NP, class RW, class WK>
+__device__ __forceinline__ void phase_w(int lane, int wave, const RW& rw, const WK& wk, const f32x4 (&ck)[NP / 16][2],
+                                        bf16x8 (&wh)[NP / 32][2], bf16x8 (&wl)[NP / 32][2]) {
+  constexpr int KS = NP / 32;
+  const int n16 = lane & 15, g4 = lane >> 4;
 #pragma unroll
   for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
@@ -751,21 +727,31 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
       for (int e = 0; e < 8; ++e) {
         const int mt = 2 * ks + (e >> 2), r = e & 3;
         const int i = 16 * mt + 4 * g4 + r;
-        const float vv = bf16_bits_to_f32(sm.v[qkv_at(i, col)]);
-        w8[e] = sm.beta[i] * (vv - sm.gc[i] * ck[mt][t][r]);
+        const float vv = bf16_bits_to_f32(rw.v[qkv_at(i, col)]);
+        w8[e] = wk.beta[i] * (vv - wk.gc[i] * ck[mt][t][r]);
       }
       split_bf16x8(w8, wh[ks][t], wl[ks][t]);
     }
-  // every wave has read its v rows: the q/k/v region takes the outputs
-  __syncthreads();
-  float* vn_s = reinterpret_cast<float*>(sm.q);  // spans q and k
-  uint16_t* o_s = sm.v;
+}
 
-  // [X; M] W: tiles mo < MT give vn, tiles mo >= MT give M W.
+// 3b: [X; M] W, tiles mo < MT give vn and tiles mo >= MT give M W (o adds
+// cO * Cq).  Staged into the (then free) q/k/v region of rw when the flags
+// allow, else stored directly.
+template <int NP, class RW, class WK>
+__device__ __forceinline__ void phase_out(const VerifyParams& P, const Item& it, int lane, int wave, RW& rw,
+                                          const WK& wk, const f32x4 (&cq)[NP / 16][2],
+                                          const bf16x8 (&wh)[NP / 32][2], const bf16x8 (&wl)[NP / 32][2]) {
+  constexpr int MT = NP / 16;
+  constexpr int KS = NP / 32;
+  constexpr int LDA = WK::LDA;
+  const dft_verify_args& p = P.a;
+  const int n16 = lane & 15, g4 = lane >> 4;
+  float* vn_s = reinterpret_cast<float*>(rw.q);  // spans q and k
+  uint16_t* o_s = rw.v;
 #pragma unroll
   for (int mo = 0; mo < 2 * MT; ++mo) {
     const int mt = mo % MT;
-    const float* src = mo < MT ? sm.x : sm.am;
+    const float* src = mo < MT ? wk.x : wk.am;
     f32x4 acc[2] = {f32x4{}, f32x4{}};
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
@@ -790,40 +776,169 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
         if (mo < MT) {
           if (P.vn_stage)
             vn_s[vn_at(i, col)] = acc[t][r];
-          else if (p.aux_v && i < n)
-            p.aux_v[(int64_t)h * p.aux_v_h_stride + (row0 + i) * p.aux_v_row_stride + col] = acc[t][r];
+          else if (p.aux_v && i < it.n)
+            p.aux_v[(int64_t)it.h * p.aux_v_h_stride + (it.row0 + i) * p.aux_v_row_stride + col] = acc[t][r];
         } else {
-          const float ov = sm.cO[i] * cq[mt][t][r] + acc[t][r];
+          const float ov = wk.cO[i] * cq[mt][t][r] + acc[t][r];
           if (P.o_stage)
             o_s[qkv_at(i, col)] = f32_to_bf16_bits(ov);
-          else if (i < n)
-            st_f(p.o, (row0 + i) * p.o_row_stride + (int64_t)h * p.o_h_stride + col, p.o_dtype, ov);
+          else if (i < it.n)
+            st_f(p.o, (it.row0 + i) * p.o_row_stride + (int64_t)it.h * p.o_h_stride + col, p.o_dtype, ov);
         }
       }
     }
   }
+}
+
+// 3c: staged vn and o as whole 16-byte row pieces
+template <int NP, class RW>
+__device__ __forceinline__ void phase_stores(const VerifyParams& P, const Item& it, int tid, const RW& rw) {
+  const dft_verify_args& p = P.a;
+  const float* vn_s = reinterpret_cast<const float*>(rw.q);
+  const uint16_t* o_s = rw.v;
+  if (P.vn_stage) {  // rows of 32 x 16 bytes
+    float* dst = p.aux_v + (int64_t)it.h * p.aux_v_h_stride + it.row0 * p.aux_v_row_stride;
+#pragma unroll
+    for (int u = 0; u < NP / 8; ++u) {
+      const int i = 8 * u + (tid >> 5), q = tid & 31;
+      if (i < it.n)
+        *reinterpret_cast<f32x4*>(dst + i * p.aux_v_row_stride + 4 * q) =
+            *reinterpret_cast<const f32x4*>(&vn_s[vn_at(i, 4 * q)]);
+    }
+  }
+  if (P.o_stage) {  // rows of 16 x 16 bytes
+    uint16_t* dst = static_cast<uint16_t*>(p.o) + it.row0 * p.o_row_stride + (int64_t)it.h * p.o_h_stride;
+#pragma unroll
+    for (int u = 0; u < NP / 16; ++u) {
+      const int i = 16 * u + (tid >> 4), q = tid & 15;
+      if (i < it.n)
+        *reinterpret_cast<uint4*>(dst + i * p.o_row_stride + 8 * q) =
+            *reinterpret_cast<const uint4*>(&o_s[qkv_at(i, 8 * q)]);
+    }
+  }
+}
+
+// The body of the one-head-per-workgroup kernels (COMMIT: the fused commit ->
+// verify form).
+template <int NP, bool S0VEC, bool COMMIT>
+__device__ __forceinline__ void verify_body(const VerifyParams& P) {
+  constexpr int MT = NP / 16;
+  constexpr int kPend = COMMIT ? kPendLoads : 0;  // vector-memory ops issued after the state
+  constexpr int kQkvDma = 3 * (NP / 16);          // row copies per wave
+  const dft_verify_args& p = P.a;
+  __shared__ VerifySmem<NP, COMMIT> sm;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int n16 = lane & 15, g4 = lane >> 4;
+
+  Item it;
+  item_heads(p, blockIdx.x, it);
+  item_rows<NP>(p, it);
+  const float* S0 = it.S0;
+  PendingHead ph{};
+  if constexpr (COMMIT) ph = pending_head(P.c, it.b);
+  Pending pd;
+  float vnr[4][2], gp[4];
+  f32x4 kr[2];
+  if constexpr (COMMIT) {
+    copy_path_words(P.c, it.b, lane, sm.pent[wave]);  // the wave's first load: no wait below depends on its count
+    if (it.n == 0) {  // nothing to verify this step: the commit alone
+      __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 15));
+      pd = decode_pending(ph, lane, sm.pent[wave][lane]);
+      if (pd.last < 0) return;
+      f32x4 s0r[2][8];
+      issue_state(S0, p.state_v_stride, wave, lane, s0r);
+      issue_pending(P.c, pd, it.h, wave, lane, S0, kr, vnr, gp);
+      stage_pending_keys(sm.pkey, kr, wave, lane);
+      __syncthreads();
+      apply_pending(pd, sm.pkey, vnr, gp, lane, s0r);
+      store_state(const_cast<float*>(S0), p.state_v_stride, wave, lane, s0r);
+      return;
+    }
+  }
+  if (it.n == 0) return;
+
+  // ---- 0. issue order (vector memory returns in order): the gates and
+  // ancestry bits (wave 0), the q/k/v rows straight into LDS, then the 64 KiB
+  // state tile into registers.  Phase 1 only waits for what precedes the
+  // state; the state keeps streaming underneath it.
+  if (wave == 0) issue_gates(p, it, lane, S0, sm.graw);
+  if (p.anc_f32) dense_ancestry<NP>(p, it, wave, lane, sm);
+  issue_rows<NP>(p, it, wave, lane, S0, sm);
+  asm volatile("" ::: "memory");
+
+  f32x4 s0r[2][8];
+  if (S0VEC) {
+    issue_state(S0, p.state_v_stride, wave, lane, s0r);
+  } else {
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          s0r[t][j][e] = S0[(int64_t)(32 * wave + 16 * t + n16) * p.state_v_stride +
+                            (int64_t)(16 * j + 4 * g4 + e) * p.state_k_stride];
+    __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 15));  // element loads: no overlap on this path
+  }
+  asm volatile("" ::: "memory");
+  if constexpr (COMMIT) {
+    // the path word was this wave's first load; at most the row copies and
+    // the state may still be in flight (wave 0 also issued 6 gate copies,
+    // which land right behind the path word)
+    __builtin_amdgcn_s_waitcnt(waitcnt_imm(kQkvDma + 16, 15));
+    pd = decode_pending(ph, lane, sm.pent[wave][lane]);
+    issue_pending(P.c, pd, it.h, wave, lane, S0, kr, vnr, gp);
+    asm volatile("" ::: "memory");
+  }
+
+  if (wave == 0) {
+    // the gate words were wave 0's first loads: wait for them only
+    __builtin_amdgcn_s_waitcnt(waitcnt_imm(kQkvDma + 16 + kPend, 15));
+    asm volatile("" ::: "memory");
+    if (lane < NP) decode_gates(p, it, lane, sm.graw, sm);
+  }
+  // Wait for the row loads and gates (everything issued before the state),
+  // then make the LDS writes of all waves visible.  A plain __syncthreads()
+  // here would also drain the state loads.
+  __builtin_amdgcn_s_waitcnt(waitcnt_imm(16 + kPend, 0));
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+
+  phase_norms<NP>(p, tid, sm, sm);
+  __syncthreads();
+  phase_gram<NP>(P, it, tid, sm, sm);
+  __syncthreads();
+  phase_diag<NP>(tid, sm);
+  __syncthreads();
+#pragma unroll
+  for (int d = 1; d < MT; ++d) {
+    phase_offdiag<NP>(tid, d, sm);
+    __syncthreads();
+  }
+  phase_m<NP>(tid, sm);
+
+  if constexpr (COMMIT) {
+    // the state, the path keys and the weights have landed: commit the
+    // previous step's path into the tile and write it back
+    stage_pending_keys(sm.pkey, kr, wave, lane);
+    __syncthreads();
+    if (pd.last >= 0) {
+      apply_pending(pd, sm.pkey, vnr, gp, lane, s0r);
+      store_state(const_cast<float*>(S0), p.state_v_stride, wave, lane, s0r);
+    }
+  }
+
+  f32x4 cq[MT][2], ck[MT][2];
+  phase_cq_ck<NP>(lane, sm, s0r, cq, ck);
+  __syncthreads();  // X and M complete
+  bf16x8 wh[NP / 32][2], wl[NP / 32][2];
+  phase_w<NP>(lane, wave, sm, sm, ck, wh, wl);
+  __syncthreads();  // every wave has read its v rows: the q/k/v region takes the outputs
+  phase_out<NP>(P, it, lane, wave, sm, sm, cq, wh, wl);
   if (P.vn_stage || P.o_stage) {
     __syncthreads();
-    if (P.vn_stage) {  // rows of 32 x 16 bytes
-      float* dst = p.aux_v + (int64_t)h * p.aux_v_h_stride + row0 * p.aux_v_row_stride;
-#pragma unroll
-      for (int u = 0; u < NP / 8; ++u) {
-        const int i = 8 * u + (tid >> 5), q = tid & 31;
-        if (i < n)
-          *reinterpret_cast<f32x4*>(dst + i * p.aux_v_row_stride + 4 * q) =
-              *reinterpret_cast<const f32x4*>(&vn_s[vn_at(i, 4 * q)]);
-      }
-    }
-    if (P.o_stage) {  // rows of 16 x 16 bytes
-      uint16_t* dst = static_cast<uint16_t*>(p.o) + row0 * p.o_row_stride + (int64_t)h * p.o_h_stride;
-#pragma unroll
-      for (int u = 0; u < NP / 16; ++u) {
-        const int i = 16 * u + (tid >> 4), q = tid & 15;
-        if (i < n)
-          *reinterpret_cast<uint4*>(dst + i * p.o_row_stride + 8 * q) =
-              *reinterpret_cast<const uint4*>(&o_s[qkv_at(i, 8 * q)]);
-      }
-    }
+    phase_stores<NP>(P, it, tid, sm);
   }
 }
 
