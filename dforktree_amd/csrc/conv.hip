@@ -69,8 +69,6 @@ __global__ void __launch_bounds__(256) tree_conv_kernel(const dft_conv_args p) {
 // beats blocks that walk 2-8 nodes (fewer, longer-lived waves) and beats
 // unstaged 48-byte window stores; non-temporal stores are slower still
 // (partial lines reach memory unmerged).
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-
 __global__ void __launch_bounds__(256) tree_conv4_bf16_kernel(const dft_conv_args p, int cblocks) {
   __shared__ u32x4 stage[256 * 3];
   const int id = blockIdx.x;

@@ -86,17 +86,12 @@ __device__ __forceinline__ int vn_at(int i, int c) { return i * kD + ((((c >> 2)
 // LDS of the fused commit -> verify form: the previous step's path keys,
 // 16 rows of 128 fp32 with 16-byte chunk q of row p at q ^ ((p & 3) << 2),
 // so the MFMA operand reads of 4 rows x 16 columns hit 64 distinct banks.
-template <bool COMMIT>
-struct PendingSmem {};
-template <>
-struct PendingSmem<true> {
-  float pkey[16 * kD];
-  uint32_t pent[4][64];  // per wave: lane l's copy of path entry l % 16
-};
 __device__ __forceinline__ int pkey_at(int p, int c) { return p * kD + ((((c >> 2) ^ ((p & 3) << 2)) & 31) << 2) + (c & 3); }
 
-template <int NP, bool COMMIT = false>
-struct VerifySmem : PendingSmem<COMMIT> {
+// The fused commit stages the previous step's path keys in pq (free once M
+// is formed) 8 slots at a time: 8 x 128 floats fit in pq for every NP.
+template <int NP>
+struct VerifySmem {
   static constexpr int LDA = NP + 4;  // fp32 row pitch, rows 16-byte aligned
   uint16_t q[NP * kD], k[NP * kD], v[NP * kD];
   float am[NP * LDA];  // at[m][i] = A[i][m] until X is formed, then M[i][j]
@@ -227,13 +222,12 @@ struct Pending {
   int64_t prow0;   // row of the request's node 0 in the previous step's buffers
 };
 
-// Lane l copies the 32-bit word of entry l % 16 into LDS (the low half of an
-// int64 entry).  A register load would be read while the row copies are in
-// flight, and the compiler then drains every load first.
-__device__ __forceinline__ void copy_path_words(const dft_pending_commit& c, int b, int lane, uint32_t* dst) {
+// The 32-bit word of path entry l % 16 (the low half of an int64 entry).
+__device__ __forceinline__ const uint32_t* path_word(const dft_pending_commit& c, int b, int lane) {
   const int col = (lane & 15) < c.path_cols ? (lane & 15) : c.path_cols - 1;
   const int esz = c.path_dtype == DFT_I64 ? 8 : 4;
-  lds_dma4(static_cast<const char*>(c.path) + ((int64_t)b * c.path_req_stride + col) * esz, dst);
+  return reinterpret_cast<const uint32_t*>(static_cast<const char*>(c.path) +
+                                           ((int64_t)b * c.path_req_stride + col) * esz);
 }
 
 // The request's previous rows and how many path entries count; read with
@@ -273,14 +267,10 @@ __device__ __forceinline__ Pending decode_pending(const PendingHead& ph, int lan
   return pd;
 }
 
-// Issued right after the state tile (the same count on every lane whether or
-// not anything is pending, so the explicit waits stay exact): two 16-byte
-// pieces of the path keys per thread (row t / 16), each lane's B-operand
-// values vn_p[v] and gains G_p for path slots p = 4s + g.  With nothing
-// pending the sources are the state tile itself (valid memory, never used).
-// The keys go through registers, not global->LDS copies: a copy still in
-// flight behind the state would make every LDS read wait for the state.
-constexpr int kPendLoads = 2 + 8 + 4;
+// Two 16-byte pieces of the path keys per thread (path slot 4w + g, columns
+// 4n .. and 64 + 4n ..), each lane's B-operand values vn_p[v] and gains G_p
+// for path slots p = 4s + g.  With nothing pending the sources are the state
+// tile itself (valid memory, never used).
 
 __device__ __forceinline__ void issue_pending(const dft_pending_commit& c, const Pending& pd, int h, int wave, int lane,
                                               const float* dummy, f32x4 (&kr)[2], float (&vnr)[4][2],
@@ -308,37 +298,69 @@ __device__ __forceinline__ void issue_pending(const dft_pending_commit& c, const
 // (s0r[t][j] is the accumulator of a 16x16 MFMA with rows k = 16j + 4g + r and
 // columns v = 32w + 16t + n): fp32 MFMA 16x16x4, path slots as the inner
 // dimension (A = keys from LDS, B = weighted values from registers).
-// thread (w, l) holds chunks n and n + 16 of path key row 4w + g
-__device__ __forceinline__ void stage_pending_keys(float* pkey, const f32x4 (&kr)[2], int wave, int lane) {
-  const int rs = 4 * wave + (lane >> 4), n16 = lane & 15;
+//
+// Keys of slots [8h, 8h + 8) go to pkey rows 0..7; waves 2h and 2h + 1 hold
+// them (thread (w, l): chunks n and n + 16 of slot 4w + g).
+__device__ __forceinline__ void stage_pending_keys(float* pkey, const f32x4 (&kr)[2], int wave, int lane, int half) {
+  if ((wave >> 1) != half) return;
+  const int rs = 4 * (wave & 1) + (lane >> 4), n16 = lane & 15;
 #pragma unroll
   for (int m = 0; m < 2; ++m) *reinterpret_cast<f32x4*>(&pkey[pkey_at(rs, 4 * (n16 + 16 * m))]) = kr[m];
 }
 
-__device__ __forceinline__ void apply_pending(const Pending& pd, const float* pkey, const float (&vnr)[4][2],
-                                              const float (&gp)[4], int lane, f32x4 (&s0r)[2][8]) {
-  const int n16 = lane & 15, g4 = lane >> 4;
-  const int cu = pd.last;
-  const int su = cu >> 2;
+// e^{G_u}, the decay of the whole path, broadcast from the lane that holds G_u
+__device__ __forceinline__ float pending_decay_log(const Pending& pd, const float (&gp)[4]) {
+  const int cu = pd.last, su = cu >> 2;
   const float gsel = su == 0 ? gp[0] : su == 1 ? gp[1] : su == 2 ? gp[2] : gp[3];
-  const float gu = __shfl(gsel, (cu & 3) * 16);
-  const float eu = __expf(gu);
+  return __shfl(gsel, (cu & 3) * 16);
+}
+
+__device__ __forceinline__ void scale_state(float e, f32x4 (&s0r)[2][8]) {
 #pragma unroll
   for (int t = 0; t < 2; ++t)
 #pragma unroll
-    for (int j = 0; j < 8; ++j) s0r[t][j] *= eu;
+    for (int j = 0; j < 8; ++j) s0r[t][j] *= e;
+}
+
+// k-steps s = 2h, 2h + 1 (slots 8h .. 8h + 7) with those keys staged in pkey
+__device__ __forceinline__ void apply_pending_half(const Pending& pd, float gu, const float* pkey,
+                                                   const float (&vnr)[4][2], const float (&gp)[4], int lane, int half,
+                                                   f32x4 (&s0r)[2][8]) {
+  const int n16 = lane & 15, g4 = lane >> 4;
 #pragma unroll
-  for (int s = 0; s < 4; ++s) {
-    if (4 * s > cu) break;  // uniform
+  for (int ss = 0; ss < 2; ++ss) {
+    const int s = 2 * half + ss;
+    if (4 * s > pd.last) break;  // uniform
     const int p = 4 * s + g4;
-    const float wgt = ((pd.vmask >> p) & 1u) ? __expf(gu - gp[s]) : 0.f;
-    const float bv[2] = {wgt * vnr[s][0], wgt * vnr[s][1]};
+    const float gps = half == 0 ? (ss == 0 ? gp[0] : gp[1]) : (ss == 0 ? gp[2] : gp[3]);
+    const float v0 = half == 0 ? (ss == 0 ? vnr[0][0] : vnr[1][0]) : (ss == 0 ? vnr[2][0] : vnr[3][0]);
+    const float v1 = half == 0 ? (ss == 0 ? vnr[0][1] : vnr[1][1]) : (ss == 0 ? vnr[2][1] : vnr[3][1]);
+    const float wgt = ((pd.vmask >> p) & 1u) ? __expf(gu - gps) : 0.f;
+    const float bv[2] = {wgt * v0, wgt * v1};
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      const float av = pkey[pkey_at(p, 16 * j + n16)];
+      const float av = pkey[pkey_at(4 * ss + g4, 16 * j + n16)];
 #pragma unroll
       for (int t = 0; t < 2; ++t) s0r[t][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv[t], s0r[t][j], 0, 0, 0);
     }
+  }
+}
+
+// The whole commit of a landed tile; pkey is free LDS of 8 x 128 floats and
+// every thread arrives here (it holds barriers).
+__device__ __forceinline__ void commit_tile(const Pending& pd, float* pkey, const f32x4 (&kr)[2],
+                                            const float (&vnr)[4][2], const float (&gp)[4], int wave, int lane,
+                                            f32x4 (&s0r)[2][8]) {
+  const float gu = pending_decay_log(pd, gp);
+  scale_state(__expf(gu), s0r);
+  stage_pending_keys(pkey, kr, wave, lane, 0);
+  __syncthreads();
+  apply_pending_half(pd, gu, pkey, vnr, gp, lane, 0, s0r);
+  if (pd.last >= 8) {  // uniform
+    __syncthreads();
+    stage_pending_keys(pkey, kr, wave, lane, 1);
+    __syncthreads();
+    apply_pending_half(pd, gu, pkey, vnr, gp, lane, 1, s0r);
   }
 }
 
@@ -411,8 +433,13 @@ __device__ __forceinline__ void item_rows(const dft_verify_args& p, Item& it) {
 // (rows past the tree repeat the last node).  The words are whole aligned
 // 32-bit words, decoded later, so nothing waits on them before the state is
 // issued.  `alt` replaces every source when the request has no rows.
+//
+// Row 4 carries dt_bias (a per-head word, read from lane kDtLane) on every
+// lane unless `path` is given: then lanes 0-15 fetch the words of the
+// pending path entries instead (the fused commit reads them from there).
+constexpr int kDtLane = 63;
 __device__ __forceinline__ void issue_gates(const dft_verify_args& p, const Item& it, int lane, const void* alt,
-                                            uint32_t (*graw)[64]) {
+                                            uint32_t (*graw)[64], const void* path = nullptr) {
   uint32_t sh;
   const int64_t gi = it.row0 + (lane < it.n ? lane : it.n - 1);
   const bool ok = it.n > 0;
@@ -422,7 +449,8 @@ __device__ __forceinline__ void issue_gates(const dft_verify_args& p, const Item
                                             : static_cast<const uint32_t*>(alt);
   lds_dma4(bits, graw[2]);
   lds_dma4(bits + 1, graw[3]);
-  lds_dma4(word_of(p.dt_bias, it.h, p.dt_bias_dtype, sh), graw[4]);
+  const uint32_t* dt = word_of(p.dt_bias, it.h, p.dt_bias_dtype, sh);
+  lds_dma4((path && lane < 16) ? path : static_cast<const void*>(dt), graw[4]);
   lds_dma4(word_of(p.neg_exp_A ? static_cast<const void*>(p.neg_exp_A) : p.A_log, it.h,
                    p.neg_exp_A ? (int)DFT_F32 : p.A_log_dtype, sh),
            graw[5]);
@@ -442,7 +470,7 @@ __device__ __forceinline__ void decode_gates(const dft_verify_args& p, const Ite
   const int i = lane;
   float gv = 0.f, bv = 0.f;
   if (i < it.n) {
-    const float a = word_to_f(graw[0][i], sha, p.a_dtype) + word_to_f(graw[4][i], shdt, p.dt_bias_dtype);
+    const float a = word_to_f(graw[0][i], sha, p.a_dtype) + word_to_f(graw[4][kDtLane], shdt, p.dt_bias_dtype);
     const float sp = a > 20.f ? a : logf(1.f + expf(fminf(a, 20.f)));
     const uint32_t wdec = graw[5][i];
     const float dec = p.neg_exp_A ? __uint_as_float(wdec) : -expf(word_to_f(wdec, shdec, p.A_log_dtype));
@@ -671,7 +699,12 @@ __device__ __forceinline__ void phase_m(int tid, WK& wk) {
 }
 
 // 2: Cq = q_raw S0, Ck = k_raw S0 for the wave's 32 columns.  k-step s, lane
-// group g, element e -> k = 32s + 4g + e (e < 4), 32s + 16 + 4g + e-4
+// group g, element e -> k = 32s + 4g + e (e < 4), 32s + 16 + 4g + e-4.  The
+// A and B operands of the bf16 MFMA share one lane layout (index lane % 16,
+// k = 8 (lane / 16) + e), so swapping them yields the transposed product from
+// the same registers: Ck comes out as [node][column] (lane n, g, element r ->
+// node 16mt + 4g + r, column 16t + n), Cq as [column][node] (node 16mt + n,
+// column 16t + 4g + r), the layout of the output tiles.
 template <int NP, class RW>
 __device__ __forceinline__ void phase_cq_ck(int lane, const RW& rw, const f32x4 (&s0r)[2][8], f32x4 (&cq)[NP / 16][2],
                                             f32x4 (&ck)[NP / 16][2]) {
@@ -700,9 +733,9 @@ __device__ __forceinline__ void phase_cq_ck(int lane, const RW& rw, const f32x4 
       const bf16x8 ak = lds_bf16x8_split(rw.k + qkv_at(row, c0), rw.k + qkv_at(row, c0 + 16));
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
-        cq[mt][t] = mfma_bf16_16x16x32(aq, bhi[t], cq[mt][t]);
+        cq[mt][t] = mfma_bf16_16x16x32(bhi[t], aq, cq[mt][t]);
         ck[mt][t] = mfma_bf16_16x16x32(ak, bhi[t], ck[mt][t]);
-        cq[mt][t] = mfma_bf16_16x16x32(aq, blo[t], cq[mt][t]);
+        cq[mt][t] = mfma_bf16_16x16x32(blo[t], aq, cq[mt][t]);
         ck[mt][t] = mfma_bf16_16x16x32(ak, blo[t], ck[mt][t]);
       }
     }
@@ -735,8 +768,10 @@ __device__ __forceinline__ void phase_w(int lane, int wave, const RW& rw, const 
 }
 
 // 3b: [X; M] W, tiles mo < MT give vn and tiles mo >= MT give M W (o adds
-// cO * Cq).  Staged into the (then free) q/k/v region of rw when the flags
-// allow, else stored directly.
+// cO * Cq).  Computed transposed (W as the A operand), so lane (n, g) holds
+// node 16mt + n at the four consecutive columns 16t + 4g .. +3: one 16-byte
+// (vn) or 8-byte (o) write each.  Staged into the (then free) q/k/v region of
+// rw when the flags allow, else stored directly.
 template <int NP, class RW, class WK>
 __device__ __forceinline__ void phase_out(const VerifyParams& P, const Item& it, int lane, int wave, RW& rw,
                                           const WK& wk, const f32x4 (&cq)[NP / 16][2],
@@ -762,28 +797,36 @@ __device__ __forceinline__ void phase_out(const VerifyParams& P, const Item& it,
       split_bf16x8(a8, ah, al);
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
-        acc[t] = mfma_bf16_16x16x32(ah, wh[ks][t], acc[t]);
-        acc[t] = mfma_bf16_16x16x32(ah, wl[ks][t], acc[t]);
-        acc[t] = mfma_bf16_16x16x32(al, wh[ks][t], acc[t]);
+        acc[t] = mfma_bf16_16x16x32(wh[ks][t], ah, acc[t]);
+        acc[t] = mfma_bf16_16x16x32(wl[ks][t], ah, acc[t]);
+        acc[t] = mfma_bf16_16x16x32(wh[ks][t], al, acc[t]);
       }
     }
+    const int i = 16 * mt + n16;
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
-      const int col = 32 * wave + 16 * t + n16;
+      const int col = 32 * wave + 16 * t + 4 * g4;
+      if (mo < MT) {
+        if (P.vn_stage) {
+          *reinterpret_cast<f32x4*>(&vn_s[vn_at(i, col)]) = acc[t];
+        } else if (p.aux_v && i < it.n) {
+          float* dst = p.aux_v + (int64_t)it.h * p.aux_v_h_stride + (it.row0 + i) * p.aux_v_row_stride + col;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int i = 16 * mt + 4 * g4 + r;
-        if (mo < MT) {
-          if (P.vn_stage)
-            vn_s[vn_at(i, col)] = acc[t][r];
-          else if (p.aux_v && i < it.n)
-            p.aux_v[(int64_t)it.h * p.aux_v_h_stride + (it.row0 + i) * p.aux_v_row_stride + col] = acc[t][r];
-        } else {
-          const float ov = wk.cO[i] * cq[mt][t][r] + acc[t][r];
-          if (P.o_stage)
-            o_s[qkv_at(i, col)] = f32_to_bf16_bits(ov);
-          else if (i < it.n)
-            st_f(p.o, (it.row0 + i) * p.o_row_stride + (int64_t)it.h * p.o_h_stride + col, p.o_dtype, ov);
+          for (int r = 0; r < 4; ++r) dst[r] = acc[t][r];
+        }
+      } else {
+        const f32x4 ov = wk.cO[i] * cq[mt][t] + acc[t];
+        if (P.o_stage) {
+          const bf16x2 lo = __builtin_convertvector((f32x2{ov[0], ov[1]}), bf16x2);  // round to nearest even
+          const bf16x2 hi = __builtin_convertvector((f32x2{ov[2], ov[3]}), bf16x2);
+          uint2 w;
+          __builtin_memcpy(&w.x, &lo, 4);
+          __builtin_memcpy(&w.y, &hi, 4);
+          *reinterpret_cast<uint2*>(&o_s[qkv_at(i, col)]) = w;
+        } else if (i < it.n) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            st_f(p.o, (it.row0 + i) * p.o_row_stride + (int64_t)it.h * p.o_h_stride + col + r, p.o_dtype, ov[r]);
         }
       }
     }
@@ -823,10 +866,9 @@ __device__ __forceinline__ void phase_stores(const VerifyParams& P, const Item& 
 template <int NP, bool S0VEC, bool COMMIT>
 __device__ __forceinline__ void verify_body(const VerifyParams& P) {
   constexpr int MT = NP / 16;
-  constexpr int kPend = COMMIT ? kPendLoads : 0;  // vector-memory ops issued after the state
-  constexpr int kQkvDma = 3 * (NP / 16);          // row copies per wave
+  constexpr int kQkvDma = 3 * (NP / 16);  // row copies per wave
   const dft_verify_args& p = P.a;
-  __shared__ VerifySmem<NP, COMMIT> sm;
+  __shared__ VerifySmem<NP> sm;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int n16 = lane & 15, g4 = lane >> 4;
@@ -836,22 +878,16 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
   item_rows<NP>(p, it);
   const float* S0 = it.S0;
   PendingHead ph{};
-  if constexpr (COMMIT) ph = pending_head(P.c, it.b);
-  Pending pd;
-  float vnr[4][2], gp[4];
-  f32x4 kr[2];
   if constexpr (COMMIT) {
-    copy_path_words(P.c, it.b, lane, sm.pent[wave]);  // the wave's first load: no wait below depends on its count
+    ph = pending_head(P.c, it.b);
     if (it.n == 0) {  // nothing to verify this step: the commit alone
-      __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 15));
-      pd = decode_pending(ph, lane, sm.pent[wave][lane]);
+      const Pending pd = decode_pending(ph, lane, *path_word(P.c, it.b, lane));
       if (pd.last < 0) return;
-      f32x4 s0r[2][8];
+      f32x4 s0r[2][8], kr[2];
+      float vnr[4][2], gp[4];
       issue_state(S0, p.state_v_stride, wave, lane, s0r);
       issue_pending(P.c, pd, it.h, wave, lane, S0, kr, vnr, gp);
-      stage_pending_keys(sm.pkey, kr, wave, lane);
-      __syncthreads();
-      apply_pending(pd, sm.pkey, vnr, gp, lane, s0r);
+      commit_tile(pd, sm.pq, kr, vnr, gp, wave, lane, s0r);
       store_state(const_cast<float*>(S0), p.state_v_stride, wave, lane, s0r);
       return;
     }
@@ -862,7 +898,8 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
   // ancestry bits (wave 0), the q/k/v rows straight into LDS, then the 64 KiB
   // state tile into registers.  Phase 1 only waits for what precedes the
   // state; the state keeps streaming underneath it.
-  if (wave == 0) issue_gates(p, it, lane, S0, sm.graw);
+  // (fused form: the pending path's entry words travel in gate row 4)
+  if (wave == 0) issue_gates(p, it, lane, S0, sm.graw, COMMIT ? path_word(P.c, it.b, lane) : nullptr);
   if (p.anc_f32) dense_ancestry<NP>(p, it, wave, lane, sm);
   issue_rows<NP>(p, it, wave, lane, S0, sm);
   asm volatile("" ::: "memory");
@@ -882,26 +919,17 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
     __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 15));  // element loads: no overlap on this path
   }
   asm volatile("" ::: "memory");
-  if constexpr (COMMIT) {
-    // the path word was this wave's first load; at most the row copies and
-    // the state may still be in flight (wave 0 also issued 6 gate copies,
-    // which land right behind the path word)
-    __builtin_amdgcn_s_waitcnt(waitcnt_imm(kQkvDma + 16, 15));
-    pd = decode_pending(ph, lane, sm.pent[wave][lane]);
-    issue_pending(P.c, pd, it.h, wave, lane, S0, kr, vnr, gp);
-    asm volatile("" ::: "memory");
-  }
 
   if (wave == 0) {
-    // the gate words were wave 0's first loads: wait for them only
-    __builtin_amdgcn_s_waitcnt(waitcnt_imm(kQkvDma + 16 + kPend, 15));
+    // the gate words were wave 0's first copies: wait for them only
+    __builtin_amdgcn_s_waitcnt(waitcnt_imm(kQkvDma + 16, 15));
     asm volatile("" ::: "memory");
     if (lane < NP) decode_gates(p, it, lane, sm.graw, sm);
   }
   // Wait for the row loads and gates (everything issued before the state),
   // then make the LDS writes of all waves visible.  A plain __syncthreads()
   // here would also drain the state loads.
-  __builtin_amdgcn_s_waitcnt(waitcnt_imm(16 + kPend, 0));
+  __builtin_amdgcn_s_waitcnt(waitcnt_imm(16, 0));
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
 
@@ -919,12 +947,18 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
   phase_m<NP>(tid, sm);
 
   if constexpr (COMMIT) {
-    // the state, the path keys and the weights have landed: commit the
-    // previous step's path into the tile and write it back
-    stage_pending_keys(sm.pkey, kr, wave, lane);
-    __syncthreads();
+    // The state has landed by now.  The previous step's path is decoded and
+    // its keys, values and gains are fetched only here, so that none of them
+    // occupies registers through phase 1; then the path is committed into
+    // the tile and the tile is written back.
+    __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 15));
+    const Pending pd = decode_pending(ph, lane, sm.graw[4][lane & 15]);
     if (pd.last >= 0) {
-      apply_pending(pd, sm.pkey, vnr, gp, lane, s0r);
+      f32x4 kr[2];
+      float vnr[4][2], gp[4];
+      issue_pending(P.c, pd, it.h, wave, lane, S0, kr, vnr, gp);
+      __syncthreads();  // every wave is done with pq
+      commit_tile(pd, sm.pq, kr, vnr, gp, wave, lane, s0r);
       store_state(const_cast<float*>(S0), p.state_v_stride, wave, lane, s0r);
     }
   }
@@ -949,7 +983,7 @@ tree_verify_kernel(const VerifyParams P) {
 }
 
 template <int NP>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NP == 32 ? 3 : 1)))
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NP == 32 ? 4 : 1)))
 tree_commit_verify_kernel(const VerifyParams P) {
   verify_body<NP, true, true>(P);
 }

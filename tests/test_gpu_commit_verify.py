@@ -181,3 +181,51 @@ def test_commit_verify_equals_commit_then_verify(cuda):
     assert rel_l2(np32(oa), np32(ob)) <= 1e-5
     for x, y in zip(auxa, auxb):
         assert rel_l2(np32(x), np32(y)) <= 1e-6
+
+
+def test_commit_verify_many_items_chain_of_three(cuda):
+    """Full layer width at 24 requests (768 items: the persistent pipelined
+    kernel), three steps: plain verify, then two fused commit -> verify steps
+    that alternate the save buffers; checked against the oracle chain."""
+    from dforktree_amd import ops, synth
+    announce("commit->verify many items, 3 steps")
+    B, N, hk, hv = 24, 32, 16, 32
+    steps = [synth.make_batch(30 + t, 0, [N] * B, hk=hk, hv=hv, kinds=["random", "chain", "bushy"] * 8)
+             for t in range(3)]
+    pool = steps[0].state.clone().to(cuda)
+    rows = B * N
+    saves = [tuple(torch.zeros(*sh, device=cuda) for sh in ((hk, rows, 128), (hv, rows, 128), (hv, rows)))
+             for _ in range(2)]
+    outs, walks_all = [], []
+    S = [np32(steps[0].state[r]).transpose(0, 2, 1) for r in range(B)]
+    for t, bt in enumerate(steps):
+        g = bt.to(cuda)
+        ts = ops.tree_struct(g.parent, 4, batch=B, n_nodes=N, want=("anc_bits",))["anc_bits"]
+        k, v, G = saves[t % 2]
+        common = dict(hk=hk, hv=hv, anc_bits=ts, batch=B, n_nodes=N, aux_k=k, aux_v=v, aux_g=G, aux_k_per_khead=True)
+        if t == 0:
+            o = ops.tree_verify(g.y, g.a, g.b, g.A_log, g.dt_bias, pool.transpose(-1, -2), **common)
+        else:
+            pk, pv, pG = saves[(t - 1) % 2]
+            o = ops.tree_commit_verify(g.y, g.a, g.b, g.A_log, g.dt_bias, pool.transpose(-1, -2), pending_path=idx_d,
+                                       pending_keys=pk, pending_values=pv, pending_gains=pG, pending_path_len=lens_d,
+                                       prev_n_nodes=N, pending_k_head_div=hv // hk, **common)
+        idx, lens, walks = _paths(bt, 40 + t)
+        idx_d, lens_d = idx.to(cuda), lens.to(cuda)
+        outs.append(np32(o))
+        walks_all.append(walks)
+    torch.cuda.synchronize()
+    # oracle chain: verify step t on S, commit its walk, repeat
+    for t, bt in enumerate(steps):
+        b = bt.to("cpu")
+        b.state = torch.stack([torch.from_numpy(np.ascontiguousarray(s.transpose(0, 2, 1))) for s in S])
+        ref = oracle_verify(b)
+        for r, sl in enumerate(request_slices(b)):
+            want = O.bf16_round(ref[r]["o"])
+            assert rel_l2(outs[t][sl], want) <= REL_L2 and max_abs(outs[t][sl], want) <= MAX_ABS_BF16, (t, r)
+            if t < 2:
+                S[r] = O.closed_commit(S[r], ref[r]["k"], ref[r]["vn"], ref[r]["G"], walks_all[t][r])
+    # the pool holds the state after step 1's commit (step 2's walk is still pending)
+    got = np32(pool)
+    for r in range(B):
+        assert rel_l2(got[r].transpose(0, 2, 1), S[r]) <= REL_L2, r

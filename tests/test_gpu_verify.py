@@ -193,7 +193,26 @@ def test_verify_persistent_loop_many_heads(cuda, sizes_kind):
     else:
         sizes, kinds = synth.ragged_sizes(12, 8, 64, seed=3)  # 384 items (> 1 per CU x 256)
     batch = synth.make_batch(9, 0, sizes, hk=16, hv=32, kinds=kinds)
-    check_against_oracle(batch, *run_gpu(batch, cuda, packed=(sizes_kind != "uniform32")))
+    check_against_oracle(batch, *run_gpu(batch, cuda, packed=(sizes_kind != "uniform32"), use_bits=True))
+
+
+def test_verify_ragged_32_many_items(cuda):
+    """Packed trees of 1-32 nodes with ancestry bits and more items than
+    resident workgroups: the persistent pipelined kernel (several items per
+    workgroup, alternating row buffers)."""
+    from dforktree_amd import synth
+    announce("verify ragged <=32 many items")
+    sizes, kinds = synth.ragged_sizes(40, 1, 32, seed=11)
+    batch = synth.make_batch(12, 0, sizes, hk=16, hv=32, kinds=kinds)
+    check_against_oracle(batch, *run_gpu(batch, cuda, packed=True, use_bits=True))
+
+
+def test_verify_uniform_many_items_dense_ancestry(cuda):
+    """The same width with dense ancestry matrices: one item per workgroup."""
+    from dforktree_amd import synth
+    announce("verify uniform 32 many items dense")
+    batch = synth.make_batch(13, 0, [32] * 40, hk=16, hv=32, kinds=["random", "chain", "bushy", "random"] * 10)
+    check_against_oracle(batch, *run_gpu(batch, cuda, packed=False, use_bits=False))
 
 
 def test_verify_kmajor_state_element_loads(cuda):
