@@ -26,6 +26,8 @@
 //     operand is W in the accumulator layout of phase 2, read with the node
 //     permutation that layout implies: nothing is transposed or staged.
 // Every wave streams its own columns; LDS holds only per-head O(N^2) data.
+#include <cstddef>
+
 #include "dft_device.h"
 
 namespace dft {
@@ -88,8 +90,8 @@ __device__ __forceinline__ int vn_at(int i, int c) { return i * kD + ((((c >> 2)
 // so the MFMA operand reads of 4 rows x 16 columns hit 64 distinct banks.
 __device__ __forceinline__ int pkey_at(int p, int c) { return p * kD + ((((c >> 2) ^ ((p & 3) << 2)) & 31) << 2) + (c & 3); }
 
-// The fused commit stages the previous step's path keys in pq (free once M
-// is formed) 8 slots at a time: 8 x 128 floats fit in pq for every NP.
+// The fused commit stages the previous step's 16 path keys (16 x 128 floats)
+// in am + pq before the Gram tiles are formed; the two arrays are adjacent.
 template <int NP>
 struct VerifySmem {
   static constexpr int LDA = NP + 4;  // fp32 row pitch, rows 16-byte aligned
@@ -101,7 +103,11 @@ struct VerifySmem {
   float G[NP], beta[NP], rq[NP], rk[NP], cO[NP];
   uint64_t anc[NP];
   uint32_t graw[6][64];  // per lane of wave 0: words of a, b, ancestry bits lo / hi, dt_bias, decay
+  __device__ float* pkey() { return am; }
 };
+static_assert(offsetof(VerifySmem<32>, pq) == offsetof(VerifySmem<32>, am) + sizeof(float) * 32 * 36 &&
+                  2 * 32 * 36 >= 16 * kD && 2 * 64 * 68 >= 16 * kD,
+              "am + pq hold the 16 staged path keys");
 
 __device__ __forceinline__ f32x4 mfma_bf16_16x16x32(bf16x8 a, bf16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
@@ -270,7 +276,9 @@ __device__ __forceinline__ Pending decode_pending(const PendingHead& ph, int lan
 // Two 16-byte pieces of the path keys per thread (path slot 4w + g, columns
 // 4n .. and 64 + 4n ..), each lane's B-operand values vn_p[v] and gains G_p
 // for path slots p = 4s + g.  With nothing pending the sources are the state
-// tile itself (valid memory, never used).
+// tile itself (valid memory, never used): the loads are issued on every path,
+// so that no register is left waiting on a load that only some paths issue
+// (the compiler would then make later code wait for every store since).
 
 __device__ __forceinline__ void issue_pending(const dft_pending_commit& c, const Pending& pd, int h, int wave, int lane,
                                               const float* dummy, f32x4 (&kr)[2], float (&vnr)[4][2],
@@ -298,12 +306,9 @@ __device__ __forceinline__ void issue_pending(const dft_pending_commit& c, const
 // (s0r[t][j] is the accumulator of a 16x16 MFMA with rows k = 16j + 4g + r and
 // columns v = 32w + 16t + n): fp32 MFMA 16x16x4, path slots as the inner
 // dimension (A = keys from LDS, B = weighted values from registers).
-//
-// Keys of slots [8h, 8h + 8) go to pkey rows 0..7; waves 2h and 2h + 1 hold
-// them (thread (w, l): chunks n and n + 16 of slot 4w + g).
-__device__ __forceinline__ void stage_pending_keys(float* pkey, const f32x4 (&kr)[2], int wave, int lane, int half) {
-  if ((wave >> 1) != half) return;
-  const int rs = 4 * (wave & 1) + (lane >> 4), n16 = lane & 15;
+// thread (w, l) holds chunks n and n + 16 of the key of path slot 4w + g
+__device__ __forceinline__ void stage_pending_keys(float* pkey, const f32x4 (&kr)[2], int wave, int lane) {
+  const int rs = 4 * wave + (lane >> 4), n16 = lane & 15;
 #pragma unroll
   for (int m = 0; m < 2; ++m) *reinterpret_cast<f32x4*>(&pkey[pkey_at(rs, 4 * (n16 + 16 * m))]) = kr[m];
 }
@@ -315,52 +320,33 @@ __device__ __forceinline__ float pending_decay_log(const Pending& pd, const floa
   return __shfl(gsel, (cu & 3) * 16);
 }
 
-__device__ __forceinline__ void scale_state(float e, f32x4 (&s0r)[2][8]) {
-#pragma unroll
-  for (int t = 0; t < 2; ++t)
-#pragma unroll
-    for (int j = 0; j < 8; ++j) s0r[t][j] *= e;
-}
-
-// k-steps s = 2h, 2h + 1 (slots 8h .. 8h + 7) with those keys staged in pkey
-__device__ __forceinline__ void apply_pending_half(const Pending& pd, float gu, const float* pkey,
-                                                   const float (&vnr)[4][2], const float (&gp)[4], int lane, int half,
-                                                   f32x4 (&s0r)[2][8]) {
-  const int n16 = lane & 15, g4 = lane >> 4;
-#pragma unroll
-  for (int ss = 0; ss < 2; ++ss) {
-    const int s = 2 * half + ss;
-    if (4 * s > pd.last) break;  // uniform
-    const int p = 4 * s + g4;
-    const float gps = half == 0 ? (ss == 0 ? gp[0] : gp[1]) : (ss == 0 ? gp[2] : gp[3]);
-    const float v0 = half == 0 ? (ss == 0 ? vnr[0][0] : vnr[1][0]) : (ss == 0 ? vnr[2][0] : vnr[3][0]);
-    const float v1 = half == 0 ? (ss == 0 ? vnr[0][1] : vnr[1][1]) : (ss == 0 ? vnr[2][1] : vnr[3][1]);
-    const float wgt = ((pd.vmask >> p) & 1u) ? __expf(gu - gps) : 0.f;
-    const float bv[2] = {wgt * v0, wgt * v1};
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const float av = pkey[pkey_at(4 * ss + g4, 16 * j + n16)];
-#pragma unroll
-      for (int t = 0; t < 2; ++t) s0r[t][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv[t], s0r[t][j], 0, 0, 0);
-    }
-  }
-}
-
-// The whole commit of a landed tile; pkey is free LDS of 8 x 128 floats and
-// every thread arrives here (it holds barriers).
+// The commit of a landed tile (a no-op when nothing is pending).  pkey:
+// 16 x 128 floats of LDS that no other wave touches until the next barrier;
+// every thread arrives here (the staging is followed by a barrier).
 __device__ __forceinline__ void commit_tile(const Pending& pd, float* pkey, const f32x4 (&kr)[2],
                                             const float (&vnr)[4][2], const float (&gp)[4], int wave, int lane,
                                             f32x4 (&s0r)[2][8]) {
-  const float gu = pending_decay_log(pd, gp);
-  scale_state(__expf(gu), s0r);
-  stage_pending_keys(pkey, kr, wave, lane, 0);
+  const int n16 = lane & 15, g4 = lane >> 4;
+  stage_pending_keys(pkey, kr, wave, lane);
   __syncthreads();
-  apply_pending_half(pd, gu, pkey, vnr, gp, lane, 0, s0r);
-  if (pd.last >= 8) {  // uniform
-    __syncthreads();
-    stage_pending_keys(pkey, kr, wave, lane, 1);
-    __syncthreads();
-    apply_pending_half(pd, gu, pkey, vnr, gp, lane, 1, s0r);
+  const float gu = pending_decay_log(pd, gp);
+  const float eu = pd.last >= 0 ? __expf(gu) : 1.f;
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) s0r[t][j] *= eu;
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    if (4 * s > pd.last) break;  // uniform
+    const int p = 4 * s + g4;
+    const float wgt = ((pd.vmask >> p) & 1u) ? __expf(gu - gp[s]) : 0.f;
+    const float bv[2] = {wgt * vnr[s][0], wgt * vnr[s][1]};
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float av = pkey[pkey_at(p, 16 * j + n16)];
+#pragma unroll
+      for (int t = 0; t < 2; ++t) s0r[t][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv[t], s0r[t][j], 0, 0, 0);
+    }
   }
 }
 
@@ -572,14 +558,12 @@ __device__ __forceinline__ void phase_norms(const dft_verify_args& p, int tid, c
   if (sub == 0) wk.G[i] = G;
 }
 
-// 1b: saves for the commit (normalised keys, G), output row scales, and the
-// ancestor-masked Gram tiles A (transposed into am) and Pq
+// The saves for the commit: normalised keys (once per k-head when saved per
+// k-head) and G.  Needs the norms and G; reads the k rows.
 template <int NP, class RW, class WK>
-__device__ __forceinline__ void phase_gram(const VerifyParams& P, const Item& it, int tid, const RW& rw, WK& wk) {
-  constexpr int MT = NP / 16;
-  constexpr int LDA = WK::LDA;
+__device__ __forceinline__ void phase_saves(const VerifyParams& P, const Item& it, int tid, const RW& rw,
+                                            const WK& wk) {
   const dft_verify_args& p = P.a;
-  const int lane = tid & 63, wave = tid >> 6, n16 = lane & 15, g4 = lane >> 4;
   const bool per_khead = (p.flags & DFT_VERIFY_AUX_K_PER_KHEAD) != 0;
   if (p.aux_k && (!per_khead || it.rr == 0)) {
     float* dk = p.aux_k + (int64_t)(per_khead ? it.hk : it.h) * p.aux_k_h_stride + it.row0 * p.aux_k_row_stride;
@@ -598,12 +582,22 @@ __device__ __forceinline__ void phase_gram(const VerifyParams& P, const Item& it
       }
     }
   }
+  if (p.aux_g && tid < it.n)
+    p.aux_g[(int64_t)it.h * p.aux_g_h_stride + (it.row0 + tid) * p.aux_g_row_stride] = wk.G[tid];
+}
+
+// 1b: output row scales and the ancestor-masked Gram tiles A (transposed into
+// am) and Pq
+template <int NP, class RW, class WK>
+__device__ __forceinline__ void phase_gram(const VerifyParams& P, const Item& it, int tid, const RW& rw, WK& wk) {
+  constexpr int MT = NP / 16;
+  constexpr int LDA = WK::LDA;
+  const dft_verify_args& p = P.a;
+  const int lane = tid & 63, wave = tid >> 6, n16 = lane & 15, g4 = lane >> 4;
   if (tid < NP) {
     const float eG = __expf(wk.G[tid]);
     wk.gc[tid] = eG * wk.rk[tid];  // g is no longer needed
     wk.cO[tid] = eG * wk.rq[tid];
-    if (p.aux_g && tid < it.n)
-      p.aux_g[(int64_t)it.h * p.aux_g_h_stride + (it.row0 + tid) * p.aux_g_row_stride] = wk.G[tid];
   }
   int item = 0;
 #pragma unroll
@@ -887,7 +881,7 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
       float vnr[4][2], gp[4];
       issue_state(S0, p.state_v_stride, wave, lane, s0r);
       issue_pending(P.c, pd, it.h, wave, lane, S0, kr, vnr, gp);
-      commit_tile(pd, sm.pq, kr, vnr, gp, wave, lane, s0r);
+      commit_tile(pd, sm.pkey(), kr, vnr, gp, wave, lane, s0r);
       store_state(const_cast<float*>(S0), p.state_v_stride, wave, lane, s0r);
       return;
     }
@@ -933,8 +927,30 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
 
+  // Fused form: the previous step's path (its entry words came with the
+  // gates) is decoded and its keys, values and gains are fetched behind the
+  // state; the norms overlap both streams.  As soon as they have landed the
+  // path is committed into the tile (keys staged in am + pq, still unused)
+  // and the tile goes back to its slot, so that the write-back streams under
+  // the rest of phase 1.
+  Pending pd{};
+  f32x4 kr[2];
+  float vnr[4][2], gp[4];
+  if constexpr (COMMIT) {
+    pd = decode_pending(ph, lane, sm.graw[4][lane & 15]);
+    issue_pending(P.c, pd, it.h, wave, lane, S0, kr, vnr, gp);
+  }
   phase_norms<NP>(p, tid, sm, sm);
   __syncthreads();
+  if constexpr (COMMIT) {
+    commit_tile(pd, sm.pkey(), kr, vnr, gp, wave, lane, s0r);
+    // everything this wave loaded has been consumed: no load is left in
+    // flight past the (conditional) write-back
+    __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 15));
+    if (pd.last >= 0) store_state(const_cast<float*>(S0), p.state_v_stride, wave, lane, s0r);
+    __syncthreads();  // every wave has read its keys: am and pq take the Gram tiles
+  }
+  phase_saves<NP>(P, it, tid, sm, sm);
   phase_gram<NP>(P, it, tid, sm, sm);
   __syncthreads();
   phase_diag<NP>(tid, sm);
@@ -945,23 +961,6 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
     __syncthreads();
   }
   phase_m<NP>(tid, sm);
-
-  if constexpr (COMMIT) {
-    // The state has landed by now.  The previous step's path is decoded and
-    // its keys, values and gains are fetched only here, so that none of them
-    // occupies registers through phase 1; then the path is committed into
-    // the tile and the tile is written back.
-    __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 15));
-    const Pending pd = decode_pending(ph, lane, sm.graw[4][lane & 15]);
-    if (pd.last >= 0) {
-      f32x4 kr[2];
-      float vnr[4][2], gp[4];
-      issue_pending(P.c, pd, it.h, wave, lane, S0, kr, vnr, gp);
-      __syncthreads();  // every wave is done with pq
-      commit_tile(pd, sm.pq, kr, vnr, gp, wave, lane, s0r);
-      store_state(const_cast<float*>(S0), p.state_v_stride, wave, lane, s0r);
-    }
-  }
 
   f32x4 cq[MT][2], ck[MT][2];
   phase_cq_ck<NP>(lane, sm, s0r, cq, ck);
