@@ -67,7 +67,8 @@ __global__ void __launch_bounds__(256) tree_commit_kernel(const CommitParams P) 
   if (P.src_vec) {
 #pragma unroll
     for (int m = 0; m < 16; ++m)
-      st[m] = *reinterpret_cast<const f32x4*>(srcp + (int64_t)(16 * rg + m) * p.src_row_stride + 4 * c4);
+      st[m] = __builtin_nontemporal_load(
+          reinterpret_cast<const f32x4*>(srcp + (int64_t)(16 * rg + m) * p.src_row_stride + 4 * c4));
   } else {
 #pragma unroll
     for (int m = 0; m < 16; ++m)
@@ -159,7 +160,7 @@ __global__ void __launch_bounds__(256) tree_commit_kernel(const CommitParams P) 
   if (P.dst_vec) {
 #pragma unroll
     for (int m = 0; m < 16; ++m)
-      *reinterpret_cast<f32x4*>(dstp + (int64_t)(16 * rg + m) * p.dst_row_stride + 4 * c4) = st[m];
+      __builtin_nontemporal_store(st[m], reinterpret_cast<f32x4*>(dstp + (int64_t)(16 * rg + m) * p.dst_row_stride + 4 * c4));
   } else {
 #pragma unroll
     for (int m = 0; m < 16; ++m)

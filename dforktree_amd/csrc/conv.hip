@@ -67,8 +67,9 @@ __global__ void __launch_bounds__(256) tree_conv_kernel(const dft_conv_args p) {
 // stay in that L2.
 // Measured at 64 requests x 32 nodes x 8192 channels: one node per block
 // beats blocks that walk 2-8 nodes (fewer, longer-lived waves) and beats
-// unstaged 48-byte window stores; non-temporal stores are slower still
-// (partial lines reach memory unmerged).
+// unstaged 48-byte window stores (non-temporal unstaged stores were slower
+// still: partial lines reach memory unmerged).  With the staged stores,
+// non-temporal y / window stores time the same as ordinary ones (within 1%).
 __global__ void __launch_bounds__(256) tree_conv4_bf16_kernel(const dft_conv_args p, int cblocks) {
   __shared__ u32x4 stage[256 * 3];
   const int id = blockIdx.x;
