@@ -34,6 +34,7 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, vendor figure
+MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA, vendor figure
 B, L, N, HK, HV, D = 64, 24, 32, 16, 32, 128
 MAX_PATH = 16
 
@@ -297,6 +298,19 @@ def main():
             traffic = json.loads(prof.read_text()).get(dom, {}).get("traffic_bytes_per_launch")
         except (ValueError, OSError):
             traffic = None
+    # MFMA work per launch of the dominant kernel, counted by rocprofv3 (MOPS x 512 FLOP, hi/lo splits included),
+    # over this run's live kernel time
+    mfma = None
+    mprof = ROOT / "profiles" / "mfma.json"
+    if mprof.exists():
+        try:
+            mf = json.loads(mprof.read_text()).get(dom, {}).get("bf16_flops_per_launch")
+        except (ValueError, OSError):
+            mf = None
+        if mf:
+            tflops = mf / (kd["ms"] * 1e-3) / 1e12
+            mfma = {"kernel": dom, "dtype": "bf16", "flops_per_launch": mf, "achieved": round(tflops, 1),
+                    "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4)}
     value = B * N / (t_step * 1e-3 / L)
     frac = lambda nbytes, ms: round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)  # noqa: E731
     out = {
@@ -320,6 +334,7 @@ def main():
         "roofline": {"kernel": dom, "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "algorithmic_bytes_per_launch": kd["bytes"]},
+        "mfma": mfma,
         "commit_verify_us_per_layer": round(t_fused * 1e3, 2),
         # state bytes the separate kernels need (verify read + commit read and write) per unit time,
         # and the state bytes the pipelined schedule actually moves (one read + one write)
