@@ -133,6 +133,25 @@ class Workload:
         from dforktree_amd import ops
         ops.tree_conv(self.cx, self.cs, self.cw, None, self.cidx, y=self.cy, iw=self.ciw)
 
+    MASK_PREFIX = 4096  # committed tokens ahead of each request's draft tree
+
+    def mask_setup(self, dev):
+        """The attention layers' packed tree mask: ones over a 4096-token
+        prefix, the ancestry over the 32 draft nodes, per request."""
+        import torch
+        self.mplen = torch.full((B,), self.MASK_PREFIX, device=dev, dtype=torch.int32)
+        nbytes = B * ((N * (self.MASK_PREFIX + N) + 7) // 8)
+        self.mout = torch.empty(nbytes, device=dev, dtype=torch.uint8)
+        self.mind = torch.empty(B + 1, device=dev, dtype=torch.int32)
+
+    def mask(self):
+        from dforktree_amd import ops
+        ops.tree_mask_pack(self.anc_bits, self.mplen, n_nodes=N, out=self.mout, out_indptr=self.mind)
+
+    def mask_bytes_per_launch(self):
+        # packed bytes written, ancestry words and prefix lengths read
+        return B * ((N * (self.MASK_PREFIX + N) + 7) // 8 + N * 8 + 4)
+
     def conv_bytes_per_launch(self):
         C = 2 * HK * D + HV * D
         # tokens read once (parents' rows are re-gathered from cache), output and window written
@@ -276,8 +295,11 @@ def main():
     t_fused_layers = time_graph(lambda: [w.fused(l) for l in range(L)], reps_kernel, args.warmup, args.eager)
     t_fused = t_fused_layers / L
     t_step = time_graph(w.fused_step, args.steps, args.warmup, args.eager)
+    # conv and mask run once per layer in a step: 24 back-to-back launches per replay, as for verify
     w.conv_setup(dev)
-    t_conv = time_graph(w.conv, reps_kernel, args.warmup, args.eager)
+    t_conv = time_graph(lambda: [w.conv() for _ in range(L)], reps_kernel, args.warmup, args.eager) / L
+    w.mask_setup(dev)
+    t_mask = time_graph(lambda: [w.mask() for _ in range(L)], reps_kernel, args.warmup, args.eager) / L
     if args.copy_calibration:
         src = torch.ones(1 << 28, device=dev)
         dst = torch.empty_like(src)
@@ -347,6 +369,8 @@ def main():
         "verify_only_nodes_per_s_per_layer": round(B * N / (t_verify * 1e-3), 1),
         "conv_us_per_layer": round(t_conv * 1e3, 2),
         "conv_hbm_frac": frac(w.conv_bytes_per_launch(), t_conv),
+        "mask_pack_us": round(t_mask * 1e3, 2),
+        "mask_pack_hbm_frac": frac(w.mask_bytes_per_launch(), t_mask),
     }
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(args.cpu_seconds)

@@ -105,8 +105,33 @@ class TreeArgs(C.Structure):
     ]
 
 
+class PackbitsArgs(C.Structure):
+    _fields_ = [
+        ("n_segments", i32), ("bit_order", i32),
+        ("x", vp), ("n", i64),
+        ("indptr", vp), ("indptr_dtype", i32),
+        ("out", vp), ("out_capacity", i64),
+        ("out_indptr", vp), ("out_indptr_dtype", i32),
+        ("status", vp),
+    ]
+
+
+class MaskArgs(C.Structure):
+    _fields_ = [
+        ("batch", i32), ("n_nodes", i32), ("bit_order", i32),
+        ("cu_seqlens", vp),
+        ("anc_bits", vp),
+        ("prefix_len", vp), ("prefix_len_dtype", i32),
+        ("out", vp), ("out_capacity", i64),
+        ("out_indptr", vp), ("out_indptr_dtype", i32),
+        ("status", vp),
+    ]
+
+
+DFT_BITS_LITTLE, DFT_BITS_BIG = 0, 1
+
 EXPORTS = ("dft_tree_verify", "dft_tree_commit_verify", "dft_tree_conv", "dft_tree_commit", "dft_tree_struct",
-           "dft_block_inverse", "dft_error_string", "dft_abi_version")
+           "dft_block_inverse", "dft_packbits", "dft_tree_mask_pack", "dft_error_string", "dft_abi_version")
 
 
 class LibraryMissing(RuntimeError):
@@ -136,6 +161,8 @@ def load() -> C.CDLL:
                        ("dft_tree_conv", [C.POINTER(ConvArgs), vp]),
                        ("dft_tree_commit", [C.POINTER(CommitArgs), vp]),
                        ("dft_tree_struct", [C.POINTER(TreeArgs), vp]),
+                       ("dft_packbits", [C.POINTER(PackbitsArgs), vp]),
+                       ("dft_tree_mask_pack", [C.POINTER(MaskArgs), vp]),
                        ("dft_block_inverse", [vp, i32, i32, i64, vp])):
         fn = getattr(lib, name)
         fn.argtypes = argt

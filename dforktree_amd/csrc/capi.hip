@@ -11,6 +11,8 @@ int launch_block_inverse(float* x, int n_mats, int n, int64_t mat_stride, hipStr
 int launch_tree_conv(const dft_conv_args* a, hipStream_t stream);
 int launch_tree_commit(const dft_commit_args* a, hipStream_t stream);
 int launch_tree_struct(const dft_tree_args* a, hipStream_t stream);
+int launch_packbits(const dft_packbits_args* a, hipStream_t stream);
+int launch_tree_mask(const dft_mask_args* a, hipStream_t stream);
 }  // namespace dft
 
 namespace {
@@ -136,6 +138,34 @@ int dft_tree_struct(const dft_tree_args* a, void* stream) {
   if (a->cidx && (!index_tag(a->cidx_dtype) || a->kc < 1)) return DFT_ERR_INVALID;
   if ((a->nxt || a->sib) && !index_tag(a->link_dtype)) return DFT_ERR_INVALID;
   return dft::launch_tree_struct(a, static_cast<hipStream_t>(stream));
+}
+
+int dft_packbits(const dft_packbits_args* a, void* stream) {
+  if (!a) return DFT_ERR_INVALID;
+  if (a->bit_order != DFT_BITS_LITTLE && a->bit_order != DFT_BITS_BIG) return DFT_ERR_INVALID;
+  if (a->out_capacity < 0) return DFT_ERR_INVALID;
+  if (a->indptr) {
+    if (a->n_segments < 0 || !index_tag(a->indptr_dtype)) return DFT_ERR_INVALID;
+    if (a->n_segments > 65535) return DFT_ERR_UNSUPPORTED;
+    if (a->n_segments == 0) return DFT_OK;
+  } else if (a->n < 0) {
+    return DFT_ERR_INVALID;
+  }
+  if (a->out_indptr && !index_tag(a->out_indptr_dtype)) return DFT_ERR_INVALID;
+  if (!a->x || !a->out) return DFT_ERR_INVALID;
+  return dft::launch_packbits(a, static_cast<hipStream_t>(stream));
+}
+
+int dft_tree_mask_pack(const dft_mask_args* a, void* stream) {
+  if (!a) return DFT_ERR_INVALID;
+  if (a->batch < 0 || a->n_nodes < 0 || a->n_nodes > 64) return DFT_ERR_INVALID;
+  if (a->bit_order != DFT_BITS_LITTLE && a->bit_order != DFT_BITS_BIG) return DFT_ERR_INVALID;
+  if (a->out_capacity < 0) return DFT_ERR_INVALID;
+  if (a->batch > 65535) return DFT_ERR_UNSUPPORTED;
+  if (a->batch == 0) return DFT_OK;
+  if (!a->anc_bits || !a->prefix_len || !a->out || !index_tag(a->prefix_len_dtype)) return DFT_ERR_INVALID;
+  if (a->out_indptr && !index_tag(a->out_indptr_dtype)) return DFT_ERR_INVALID;
+  return dft::launch_tree_mask(a, static_cast<hipStream_t>(stream));
 }
 
 }  // extern "C"

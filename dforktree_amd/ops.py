@@ -18,8 +18,8 @@ from typing import Optional
 import torch
 
 from . import _lib
-from ._lib import (DFT_BF16, DFT_F16, DFT_F32, DFT_I32, DFT_I64, CommitArgs, ConvArgs, PendingArgs, TreeArgs,
-                   VerifyArgs, check, load)
+from ._lib import (DFT_BF16, DFT_BITS_BIG, DFT_BITS_LITTLE, DFT_F16, DFT_F32, DFT_I32, DFT_I64, CommitArgs,
+                   ConvArgs, MaskArgs, PackbitsArgs, PendingArgs, TreeArgs, VerifyArgs, check, load)
 
 _FLOAT_TAG = {torch.float32: DFT_F32, torch.bfloat16: DFT_BF16, torch.float16: DFT_F16}
 _INDEX_TAG = {torch.int32: DFT_I32, torch.int64: DFT_I64}
@@ -511,3 +511,143 @@ def block_inverse_(x: torch.Tensor) -> torch.Tensor:
     mats = x.numel() // max(n * n, 1)
     check("dft_block_inverse", load().dft_block_inverse(x.data_ptr(), mats, n, n * n, _stream(dev)))
     return x
+
+
+# ---------------------------------------------------------------------------
+# bit-packed attention masks (fc1_plan.py:26, fc1_branch64.py:39)
+# ---------------------------------------------------------------------------
+_BIT_ORDER = {"little": DFT_BITS_LITTLE, "big": DFT_BITS_BIG}
+
+
+def _bit_order(bitorder: str) -> int:
+    try:
+        return _BIT_ORDER[bitorder]
+    except KeyError:
+        raise ValueError(f"bitorder must be 'little' or 'big', got {bitorder!r}") from None
+
+
+def _byte_view(x: torch.Tensor, name: str) -> torch.Tensor:
+    if x.dtype not in (torch.bool, torch.uint8, torch.int8):
+        raise TypeError(f"{name}: expected a bool or uint8 tensor, got {x.dtype}")
+    x = x.reshape(-1)
+    if not x.is_contiguous():
+        x = x.contiguous()
+    return x.view(torch.uint8)
+
+
+def _out_bytes(out: Optional[torch.Tensor], nbytes: Optional[int], dev) -> torch.Tensor:
+    if out is None:
+        return torch.empty(nbytes, device=dev, dtype=torch.uint8)
+    if out.dtype != torch.uint8 or not out.is_contiguous():
+        raise TypeError("out: expected a contiguous uint8 tensor")
+    if out.device != dev:
+        raise ValueError(f"out is on {out.device}, the input on {dev}")
+    return out
+
+
+def packbits(x: torch.Tensor, bitorder: str = "little", *, out: Optional[torch.Tensor] = None,
+             status: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """flashinfer.packbits (as fc1_plan.py:26 calls it): x (bool / uint8, any
+    shape) flattened and packed 8 elements per byte with numpy.packbits
+    semantics; returns the ceil(x.numel() / 8) bytes.  With `out` the bytes
+    are written into it (no allocation; bytes past its end are dropped and
+    `status` is set to 1)."""
+    dev = _device_of(x, out, status)
+    xb = _byte_view(x, "x")
+    nbytes = (xb.numel() + 7) // 8
+    o = _out_bytes(out, nbytes, dev)
+    a = PackbitsArgs()
+    a.n_segments, a.bit_order = 1, _bit_order(bitorder)
+    a.x, a.n = xb.data_ptr(), xb.numel()
+    a.out, a.out_capacity = o.data_ptr(), o.numel()
+    a.status = _ptr(status)
+    if xb.numel():
+        check("dft_packbits", load().dft_packbits(C.byref(a), _stream(dev)))
+    return o if out is None else o[:nbytes]
+
+
+def segment_packbits(x: torch.Tensor, indptr: torch.Tensor, bitorder: str = "little", *,
+                     out: Optional[torch.Tensor] = None, out_indptr: Optional[torch.Tensor] = None,
+                     status: Optional[torch.Tensor] = None):
+    """flashinfer.segment_packbits: segment s = x[indptr[s]:indptr[s+1]] is
+    packed on its own; returns (packed, new_indptr) with new_indptr[s] the
+    byte offset of segment s.  Without `out` the total size is read back to
+    the host once (as flashinfer does); with `out` nothing is."""
+    dev = _device_of(x, indptr, out, out_indptr, status)
+    xb = _byte_view(x, "x")
+    ip, ip_tag = _idx_vec(indptr, "indptr")
+    segs = ip.numel() - 1
+    if segs < 0:
+        raise ValueError("indptr needs at least one entry")
+    if out is None:
+        lens = (ip[1:] - ip[:-1]).clamp_min(0).to(torch.int64)
+        out = torch.empty(int(((lens + 7) // 8).sum().item()), device=dev, dtype=torch.uint8)
+    else:
+        out = _out_bytes(out, None, dev)
+    if out_indptr is None:
+        out_indptr = torch.zeros(segs + 1, device=dev, dtype=ip.dtype)
+    a = PackbitsArgs()
+    a.n_segments, a.bit_order = segs, _bit_order(bitorder)
+    a.x, a.n = xb.data_ptr(), xb.numel()
+    a.indptr, a.indptr_dtype = ip.data_ptr(), ip_tag
+    a.out, a.out_capacity = out.data_ptr(), out.numel()
+    a.out_indptr, a.out_indptr_dtype = out_indptr.data_ptr(), _itag(out_indptr, "out_indptr")
+    a.status = _ptr(status)
+    if segs:
+        check("dft_packbits", load().dft_packbits(C.byref(a), _stream(dev)))
+    return out, out_indptr
+
+
+def tree_mask_pack(anc_bits: torch.Tensor, prefix_len: torch.Tensor, *, batch: Optional[int] = None,
+                   n_nodes: Optional[int] = None, cu_seqlens: Optional[torch.Tensor] = None,
+                   bitorder: str = "little", out: Optional[torch.Tensor] = None,
+                   out_indptr: Optional[torch.Tensor] = None, status: Optional[torch.Tensor] = None):
+    """The packed tree attention mask, straight from the ancestry bits.
+
+    Request b (nodes row0(b) ..; n_b <= 64) with prefix_len[b] committed
+    tokens contributes the row-major n_b x (plen_b + n_b) mask
+    [ones(n_b, plen_b) | Anc_b] (fc1_branch64.py:39), packed as one segment
+    (fc1_plan.py:26).  Returns (packed, mask_indptr).  Without `out` the
+    total size is computed on the host from prefix_len and cu_seqlens (one
+    read-back); the plan's preallocated buffer as `out` avoids it."""
+    dev = _device_of(anc_bits, prefix_len, cu_seqlens, out, out_indptr, status)
+    if anc_bits.dtype not in (torch.int64, torch.uint64) or not anc_bits.is_contiguous():
+        raise TypeError("anc_bits: expected a contiguous 64-bit tensor (tree_struct's anc_bits)")
+    pl, pl_tag = _idx_vec(prefix_len, "prefix_len")
+    if cu_seqlens is not None:
+        cu_seqlens = cu_seqlens.contiguous()
+        if cu_seqlens.dtype != torch.int32:
+            raise TypeError("cu_seqlens must be int32")
+        batch = cu_seqlens.numel() - 1 if batch is None else batch
+        n_nodes = MAX_NODES if n_nodes is None else n_nodes
+    else:
+        if batch is None:
+            batch = pl.numel()
+        if n_nodes is None:
+            n_nodes = anc_bits.numel() // max(batch, 1)
+    if n_nodes > MAX_NODES:
+        raise ValueError(f"at most {MAX_NODES} nodes per tree")
+    if pl.numel() < batch:
+        raise ValueError(f"prefix_len has {pl.numel()} entries for {batch} requests")
+    if out is None:
+        if cu_seqlens is not None:
+            n = (cu_seqlens[1:batch + 1] - cu_seqlens[:batch]).clamp(0, MAX_NODES).to(torch.int64)
+        else:
+            n = torch.full((batch,), n_nodes, device=dev, dtype=torch.int64)
+        bits = n * (pl[:batch].to(torch.int64).clamp_min(0) + n)
+        out = torch.empty(int(((bits + 7) // 8).sum().item()), device=dev, dtype=torch.uint8)
+    else:
+        out = _out_bytes(out, None, dev)
+    if out_indptr is None:
+        out_indptr = torch.zeros(batch + 1, device=dev, dtype=torch.int32)
+    a = MaskArgs()
+    a.batch, a.n_nodes, a.bit_order = batch, n_nodes, _bit_order(bitorder)
+    a.cu_seqlens = _ptr(cu_seqlens)
+    a.anc_bits = anc_bits.data_ptr()
+    a.prefix_len, a.prefix_len_dtype = pl.data_ptr(), pl_tag
+    a.out, a.out_capacity = out.data_ptr(), out.numel()
+    a.out_indptr, a.out_indptr_dtype = out_indptr.data_ptr(), _itag(out_indptr, "out_indptr")
+    a.status = _ptr(status)
+    if batch:
+        check("dft_tree_mask_pack", load().dft_tree_mask_pack(C.byref(a), _stream(dev)))
+    return out, out_indptr

@@ -26,6 +26,11 @@
  *   dft_tree_struct    tree_ops.tree_struct tree_ops.py:68-89 and the builder's
  *                      nxt/sib links fc1_builder.py:38-47
  *   dft_block_inverse  invert16/32/64   fc1_block_inverse.py:36-83
+ *   dft_packbits       flashinfer.packbits(mask, bitorder='little') as the
+ *                      attention plan override calls it, fc1_plan.py:26
+ *                      (and flashinfer's segment form for batches)
+ *   dft_tree_mask_pack the packed tree mask of fc1_branch64.py:39 (ones over
+ *                      the prefix, Anc over the draft nodes) + fc1_plan.py:26
  */
 #ifndef DFORKTREE_AMD_H
 #define DFORKTREE_AMD_H
@@ -283,6 +288,58 @@ typedef struct dft_tree_args {
 } dft_tree_args;
 
 DFT_API int dft_tree_struct(const dft_tree_args* args, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Bit-packed attention masks (numpy.packbits semantics).
+ *
+ * A segment of `bits` elements becomes ceil(bits / 8) bytes: element 8j + k
+ * is bit k (DFT_BITS_LITTLE) or bit 7 - k (DFT_BITS_BIG) of byte j, any
+ * non-zero element is 1, and the padding bits of the last byte are 0.
+ * Segment s starts at byte out_indptr[s] = sum_{s' < s} ceil(bits_s' / 8);
+ * out_indptr[segments] is the total (flashinfer's segment_packbits layout).
+ * out_indptr is written when given.  Nothing is written at or past
+ * out + out_capacity: bytes that do not fit are dropped and *status, when
+ * given, is set to 1 (it is never cleared).
+ * ------------------------------------------------------------------------- */
+enum dft_bit_order { DFT_BITS_LITTLE = 0, DFT_BITS_BIG = 1 };
+
+typedef struct dft_packbits_args {
+  int32_t n_segments; /* with indptr (<= 65535); one segment without */
+  int32_t bit_order;
+  const uint8_t* x; /* bool / uint8 elements */
+  int64_t n;        /* elements of the single segment when indptr is NULL */
+  const void* indptr; /* [n_segments + 1] element offsets into x, or NULL */
+  int32_t indptr_dtype;
+  uint8_t* out;
+  int64_t out_capacity; /* bytes */
+  void* out_indptr;     /* [segments + 1] byte offsets, or NULL */
+  int32_t out_indptr_dtype;
+  int32_t* status; /* optional */
+} dft_packbits_args;
+
+DFT_API int dft_packbits(const dft_packbits_args* args, void* stream);
+
+/* The packed tree mask without a boolean mask in between.  Request b with
+ * n_b nodes (rows row0(b) .. row0(b) + n_b - 1, row0 as in dft_verify_args,
+ * n_b <= 64) and plen_b committed prefix tokens is one segment: the
+ * row-major n_b x (plen_b + n_b) matrix
+ *   M[i][p] = p < plen_b  ||  bit (p - plen_b) of anc_bits[row0(b) + i]
+ * (anc_bits as dft_tree_struct writes them: ancestor-or-self). */
+typedef struct dft_mask_args {
+  int32_t batch, n_nodes; /* n_nodes: nodes per request without cu_seqlens */
+  int32_t bit_order;
+  const int32_t* cu_seqlens;
+  const uint64_t* anc_bits; /* [rows] */
+  const void* prefix_len;   /* [batch] */
+  int32_t prefix_len_dtype;
+  uint8_t* out;
+  int64_t out_capacity;
+  void* out_indptr; /* [batch + 1] byte offsets, or NULL */
+  int32_t out_indptr_dtype;
+  int32_t* status; /* optional */
+} dft_mask_args;
+
+DFT_API int dft_tree_mask_pack(const dft_mask_args* args, void* stream);
 
 /* ---------------------------------------------------------------------------
  * In-place (I + A)^-1 of n_mats strictly-lower-triangular fp32 n x n matrices

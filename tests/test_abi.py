@@ -36,7 +36,8 @@ def test_library_exports_every_declared_symbol():
 def c_layouts(tmp_path_factory):
     from dforktree_amd import _lib
     structs = {"dft_verify_args": _lib.VerifyArgs, "dft_pending_commit": _lib.PendingArgs, "dft_conv_args": _lib.ConvArgs,
-               "dft_commit_args": _lib.CommitArgs, "dft_tree_args": _lib.TreeArgs}
+               "dft_commit_args": _lib.CommitArgs, "dft_tree_args": _lib.TreeArgs,
+               "dft_packbits_args": _lib.PackbitsArgs, "dft_mask_args": _lib.MaskArgs}
     lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"', "int main(void) {",
              'printf("{");']
     first = True
@@ -106,6 +107,28 @@ def test_validation_rejects_bad_descriptors_without_launching():
     k.batch, k.n_nodes, k.channels, k.width = 1, 4, 8, 9
     assert lib.dft_tree_conv(ctypes.byref(k), None) == _lib.DFT_ERR_UNSUPPORTED
     assert lib.dft_block_inverse(None, 1, 65, 65 * 65, None) == _lib.DFT_ERR_INVALID
+    pb = _lib.PackbitsArgs()
+    pb.n, pb.bit_order = 8, 2
+    assert lib.dft_packbits(ctypes.byref(pb), None) == _lib.DFT_ERR_INVALID        # bit order
+    pb.bit_order = _lib.DFT_BITS_LITTLE
+    assert lib.dft_packbits(ctypes.byref(pb), None) == _lib.DFT_ERR_INVALID        # null pointers
+    pb.x = pb.out = 16
+    pb.out_capacity = -1
+    assert lib.dft_packbits(ctypes.byref(pb), None) == _lib.DFT_ERR_INVALID        # capacity
+    pb.out_capacity, pb.indptr, pb.indptr_dtype, pb.n_segments = 8, 16, _lib.DFT_I32, 70000
+    assert lib.dft_packbits(ctypes.byref(pb), None) == _lib.DFT_ERR_UNSUPPORTED    # > 65535 segments
+    pb.n_segments = 0
+    assert lib.dft_packbits(ctypes.byref(pb), None) == _lib.DFT_OK                 # no segment: no-op
+    mk = _lib.MaskArgs()
+    mk.batch, mk.n_nodes = 1, 65
+    assert lib.dft_tree_mask_pack(ctypes.byref(mk), None) == _lib.DFT_ERR_INVALID  # > 64 nodes
+    mk.n_nodes = 32
+    assert lib.dft_tree_mask_pack(ctypes.byref(mk), None) == _lib.DFT_ERR_INVALID  # null pointers
+    mk.anc_bits = mk.prefix_len = mk.out = 16
+    mk.prefix_len_dtype = 7
+    assert lib.dft_tree_mask_pack(ctypes.byref(mk), None) == _lib.DFT_ERR_INVALID  # prefix dtype
+    mk.batch = 0
+    assert lib.dft_tree_mask_pack(ctypes.byref(mk), None) == _lib.DFT_OK           # empty batch: no-op
     assert lib.dft_error_string(2) == b"unsupported configuration"
 
 
