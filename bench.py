@@ -196,6 +196,50 @@ class Workload:
         return L * B * 2 * HV * D * D * 4   # one read and one write per request-layer
 
 
+class RaggedWorkload:
+    """The packed ragged batch: 128 requests with trees of 8-64 nodes (a third
+    each chains, bushy depth-2 trees and random recursive trees), 24 layers of
+    distinct state; verify only, on the 64-wide path."""
+    RB = 128
+
+    def __init__(self, dev, seed=3):
+        import torch
+        from dforktree_amd import ops, synth
+        self.sizes, kinds = synth.ragged_sizes(self.RB, 8, 64, seed=seed)
+        rows = sum(self.sizes)
+        self.rows = rows
+        C = 2 * HK * D + HV * D
+        self.y = synth.device_randn_(torch.empty(L, rows, C, device=dev, dtype=torch.bfloat16), seed + 10)
+        self.a = synth.device_randn_(torch.empty(L, rows, HV, device=dev, dtype=torch.bfloat16), seed + 11)
+        self.b = synth.device_randn_(torch.empty(L, rows, HV, device=dev, dtype=torch.bfloat16), seed + 12)
+        self.A_log = torch.full((HV,), -0.6931471805599453, device=dev)
+        self.dt_bias = torch.zeros(HV, device=dev)
+        self.neg = -self.A_log.exp()
+        self.state = synth.device_randn_(torch.empty(L, self.RB, HV, D, D, device=dev), seed + 13, std=0.02)
+        g = torch.Generator().manual_seed(seed)
+        parents = torch.cat([synth.tree_parents(n, k, g) for n, k in zip(self.sizes, kinds)]).to(dev)
+        self.cu = torch.tensor([0] + torch.tensor(self.sizes).cumsum(0).tolist(), dtype=torch.int32, device=dev)
+        self.anc_bits = ops.tree_struct(parents, 4, cu_seqlens=self.cu, n_nodes=64, batch=self.RB,
+                                        want=("anc_bits",))["anc_bits"]
+        self.o = torch.empty(L, rows, HV, D, device=dev, dtype=torch.bfloat16)
+        self.keys = torch.empty(L, HK, rows, D, device=dev)
+        self.vals = torch.empty(L, HV, rows, D, device=dev)
+        self.gains = torch.empty(L, HV, rows, device=dev)
+
+    def verify(self, l):
+        from dforktree_amd import ops
+        ops.tree_verify(self.y[l], self.a[l], self.b[l], self.A_log, self.dt_bias, self.state[l].transpose(-1, -2),
+                        hk=HK, hv=HV, anc_bits=self.anc_bits, batch=self.RB, n_nodes=64, cu_seqlens=self.cu,
+                        neg_exp_A=self.neg, o=self.o[l], aux_k=self.keys[l], aux_v=self.vals[l],
+                        aux_g=self.gains[l], aux_k_per_khead=True)
+
+    def bytes_per_launch(self):
+        # per request: the 2 MiB state, and per node its y row, o, vn, key (per k-head), G, a, b, ancestry word
+        C = 2 * HK * D + HV * D
+        node = C * 2 + HV * D * 2 + HV * D * 4 + HK * D * 4 + HV * 4 + 2 * HV * 2 + 8
+        return sum(D * D * 4 * HV + n * node for n in self.sizes)
+
+
 def time_graph(fn, reps, warmup, eager=False):
     """ms per call of fn (a sequence of launches), HIP events on the current stream."""
     import torch
@@ -300,6 +344,12 @@ def main():
     t_conv = time_graph(lambda: [w.conv() for _ in range(L)], reps_kernel, args.warmup, args.eager) / L
     w.mask_setup(dev)
     t_mask = time_graph(lambda: [w.mask() for _ in range(L)], reps_kernel, args.warmup, args.eager) / L
+    rw = RaggedWorkload(dev)  # both workloads fit together (about 17 GB)
+    t_ragged = time_graph(lambda: [rw.verify(l) for l in range(L)], reps_kernel, args.warmup, args.eager) / L
+    ragged = {"workload": "packed ragged batch: 128 requests, trees of 8-64 nodes (chains / bushy / random), verify",
+              "nodes": rw.rows, "us_per_layer": round(t_ragged * 1e3, 2),
+              "nodes_per_s_per_layer": round(rw.rows / (t_ragged * 1e-3), 1),
+              "hbm_frac": round(rw.bytes_per_launch() / (t_ragged * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
     if args.copy_calibration:
         src = torch.ones(1 << 28, device=dev)
         dst = torch.empty_like(src)
@@ -371,6 +421,7 @@ def main():
         "conv_hbm_frac": frac(w.conv_bytes_per_launch(), t_conv),
         "mask_pack_us": round(t_mask * 1e3, 2),
         "mask_pack_hbm_frac": frac(w.mask_bytes_per_launch(), t_mask),
+        "ragged": ragged,
     }
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(args.cpu_seconds)

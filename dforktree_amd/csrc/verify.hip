@@ -26,6 +26,7 @@
 //     operand is W in the accumulator layout of phase 2, read with the node
 //     permutation that layout implies: nothing is transposed or staged.
 // Every wave streams its own columns; LDS holds only per-head O(N^2) data.
+#include <climits>
 #include <cstddef>
 
 #include "dft_device.h"
@@ -82,6 +83,8 @@ struct VerifyParams {
   int auxk_vec;  // aux_k rows 16-byte aligned
   int vn_stage;  // vn rows 16-byte aligned: written as whole rows through LDS
   int o_stage;   // o is bf16 with 16-byte aligned head rows: written through LDS
+  int n_lo, n_hi;  // packed launches split by tree size: this kernel takes the
+                   // requests with n_lo <= nodes <= n_hi (the others exit at once)
 };
 
 // Output staging in the (then free) q/k/v region: vn as NP x 128 fp32 with
@@ -401,8 +404,10 @@ __device__ __forceinline__ void item_heads(const dft_verify_args& p, int id, Ite
 }
 
 // rows, node count and state tile of a request (loads the index arrays)
+// Returns false when the request belongs to the other kernel of a launch
+// split by tree size (its node count outside [n_lo, n_hi]).
 template <int NP>
-__device__ __forceinline__ void item_rows(const dft_verify_args& p, Item& it) {
+__device__ __forceinline__ bool item_rows(const dft_verify_args& p, Item& it, int n_lo, int n_hi) {
   if (p.cu_seqlens) {
     it.row0 = p.cu_seqlens[it.b];
     it.n = p.cu_seqlens[it.b + 1] - p.cu_seqlens[it.b];
@@ -410,6 +415,7 @@ __device__ __forceinline__ void item_rows(const dft_verify_args& p, Item& it) {
     it.row0 = (int64_t)it.b * p.n_nodes;
     it.n = p.n_nodes;
   }
+  if (it.n < n_lo || it.n > n_hi) return false;
   it.n = it.n < 0 ? 0 : (it.n > NP ? NP : it.n);
   int64_t slot = it.b;
   if (p.state_indices) {
@@ -417,6 +423,7 @@ __device__ __forceinline__ void item_rows(const dft_verify_args& p, Item& it) {
     if (slot < 0) slot = 0;
   }
   it.S0 = p.state + slot * p.state_slot_stride + (int64_t)it.h * p.state_h_stride;
+  return true;
 }
 
 // Wave 0's lane i fetches node i's gate words and ancestry bits into graw
@@ -891,7 +898,7 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
 
   Item it;
   item_heads(p, blockIdx.x, it);
-  item_rows<NP>(p, it);
+  if (!item_rows<NP>(p, it, P.n_lo, P.n_hi)) return;
   const float* S0 = it.S0;
   PendingHead ph{};
   if constexpr (COMMIT) {
@@ -1022,22 +1029,42 @@ static VerifyParams make_params(const dft_verify_args* a) {
                (a->aux_v_h_stride % 4) == 0;
   P.o_stage = a->o_dtype == DFT_BF16 && (reinterpret_cast<uintptr_t>(a->o) % 16) == 0 && (a->o_row_stride % 8) == 0 &&
               (a->o_h_stride % 8) == 0;
+  P.n_lo = INT_MIN;
+  P.n_hi = INT_MAX;
   return P;
+}
+
+// A packed batch whose largest tree exceeds 32 nodes is split by tree size:
+// the 64-wide kernel (one workgroup per CU: its LDS) takes the requests of
+// 33-64 nodes and the 32-wide kernel (four per CU) the rest, each exiting at
+// once on the other's requests.  The sizes stay on the device.
+static void split_by_size(const dft_verify_args* a, const VerifyParams& P, VerifyParams& narrow, VerifyParams& wide,
+                          bool& split) {
+  narrow = wide = P;
+  split = a->cu_seqlens != nullptr && a->n_nodes > 32;
+  if (split) {
+    narrow.n_hi = 32;
+    wide.n_lo = 33;
+  }
 }
 
 int launch_tree_verify(const dft_verify_args* a, hipStream_t stream) {
   const VerifyParams P = make_params(a);
   const dim3 grid((unsigned)(a->batch * a->hv)), block(256);
-  if (a->n_nodes <= 32) {
+  VerifyParams narrow, wide;
+  bool split;
+  split_by_size(a, P, narrow, wide, split);
+  if (a->n_nodes > 32) {
     if (P.s0_vec)
-      hipLaunchKernelGGL((tree_verify_kernel<32, true>), grid, block, 0, stream, P);
+      hipLaunchKernelGGL((tree_verify_kernel<64, true>), grid, block, 0, stream, wide);
     else
-      hipLaunchKernelGGL((tree_verify_kernel<32, false>), grid, block, 0, stream, P);
-  } else {
+      hipLaunchKernelGGL((tree_verify_kernel<64, false>), grid, block, 0, stream, wide);
+  }
+  if (a->n_nodes <= 32 || split) {
     if (P.s0_vec)
-      hipLaunchKernelGGL((tree_verify_kernel<64, true>), grid, block, 0, stream, P);
+      hipLaunchKernelGGL((tree_verify_kernel<32, true>), grid, block, 0, stream, narrow);
     else
-      hipLaunchKernelGGL((tree_verify_kernel<64, false>), grid, block, 0, stream, P);
+      hipLaunchKernelGGL((tree_verify_kernel<32, false>), grid, block, 0, stream, narrow);
   }
   return hipGetLastError() == hipSuccess ? DFT_OK : DFT_ERR_LAUNCH;
 }
@@ -1047,10 +1074,11 @@ int launch_tree_commit_verify(const dft_verify_args* a, const dft_pending_commit
   VerifyParams P = make_params(a);
   P.c = *c;
   const dim3 grid((unsigned)(a->batch * a->hv)), block(256);
-  if (a->n_nodes <= 32)
-    hipLaunchKernelGGL((tree_commit_verify_kernel<32>), grid, block, 0, stream, P);
-  else
-    hipLaunchKernelGGL((tree_commit_verify_kernel<64>), grid, block, 0, stream, P);
+  VerifyParams narrow, wide;
+  bool split;
+  split_by_size(a, P, narrow, wide, split);
+  if (a->n_nodes > 32) hipLaunchKernelGGL((tree_commit_verify_kernel<64>), grid, block, 0, stream, wide);
+  if (a->n_nodes <= 32 || split) hipLaunchKernelGGL((tree_commit_verify_kernel<32>), grid, block, 0, stream, narrow);
   return hipGetLastError() == hipSuccess ? DFT_OK : DFT_ERR_LAUNCH;
 }
 
