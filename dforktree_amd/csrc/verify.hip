@@ -27,7 +27,6 @@
 //     permutation that layout implies: nothing is transposed or staged.
 // Every wave streams its own columns; LDS holds only per-head O(N^2) data.
 #include <climits>
-#include <cstddef>
 
 #include "dft_device.h"
 
@@ -98,23 +97,52 @@ __device__ __forceinline__ int vn_at(int i, int c) { return i * kD + ((((c >> 2)
 __device__ __forceinline__ int pkey_at(int p, int c) { return p * kD + ((((c >> 2) ^ ((p & 3) << 2)) & 31) << 2) + (c & 3); }
 
 // The fused commit stages the previous step's 16 path keys (16 x 128 floats)
-// in am + pq before the Gram tiles are formed; the two arrays are adjacent.
+// in am + x before the Gram tiles are formed; the two arrays are adjacent.
+//
+// Trees of 33-64 nodes (NP = 64) keep no v region: their v rows are copied
+// into the q region once Cq/Ck have consumed it, and o is staged in x once the
+// vn tiles have consumed X.  That keeps the workgroup under 80 KiB of LDS, so
+// two of them fit on a CU.
+template <int NP, bool LATE_V>
+struct VRegion {
+  uint16_t v[NP * kD];
+};
 template <int NP>
-struct VerifySmem {
+struct VRegion<NP, true> {};
+
+template <int NP>
+struct VerifySmem : VRegion<NP, (NP > 32)> {
   static constexpr int LDA = NP + 4;  // fp32 row pitch, rows 16-byte aligned
-  uint16_t q[NP * kD], k[NP * kD], v[NP * kD];
-  float am[NP * LDA];  // at[m][i] = A[i][m] until X is formed, then M[i][j]
-  float pq[NP * LDA];  // Pq[i][j]
-  float x[NP * LDA];   // X[i][j]
+  static constexpr bool kLateV = NP > 32;
+  uint16_t q[NP * kD], k[NP * kD];
+  // am (at[m][i] = A[i][m] until X is formed, then M[i][j]) and x (X[i][j]),
+  // one array so that the 16 staged path keys can span both
+  alignas(16) float amx[2 * NP * LDA];
   float gc[NP];        // g, then e^G rk once G is formed
   float G[NP], beta[NP], rq[NP], rk[NP], cO[NP];
   uint64_t anc[NP];
   uint32_t graw[6][64];  // per lane of wave 0: words of a, b, ancestry bits lo / hi, dt_bias, decay
-  __device__ float* pkey() { return am; }
+  __device__ float* am() { return amx; }
+  __device__ const float* am() const { return amx; }
+  __device__ float* x() { return amx + NP * LDA; }
+  __device__ const float* x() const { return amx + NP * LDA; }
+  __device__ float* pkey() { return amx; }
+  // where the v rows are read and where o is staged
+  __device__ uint16_t* vrows() {
+    if constexpr (kLateV) return q; else return this->v;
+  }
+  __device__ const uint16_t* vrows() const {
+    if constexpr (kLateV) return q; else return this->v;
+  }
+  __device__ uint16_t* ostage() {
+    if constexpr (kLateV) return reinterpret_cast<uint16_t*>(x()); else return this->v;
+  }
+  __device__ const uint16_t* ostage() const {
+    if constexpr (kLateV) return reinterpret_cast<const uint16_t*>(x()); else return this->v;
+  }
 };
-static_assert(offsetof(VerifySmem<32>, pq) == offsetof(VerifySmem<32>, am) + sizeof(float) * 32 * 36 &&
-                  2 * 32 * 36 >= 16 * kD && 2 * 64 * 68 >= 16 * kD,
-              "am + pq hold the 16 staged path keys");
+static_assert(sizeof(VerifySmem<64>) <= 80 * 1024, "two 64-wide workgroups per CU");
+static_assert(2 * 32 * 36 >= 16 * kD && 2 * 64 * 68 >= 16 * kD, "am + x hold the 16 staged path keys");
 
 __device__ __forceinline__ f32x4 mfma_bf16_16x16x32(bf16x8 a, bf16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
@@ -370,7 +398,7 @@ __device__ __forceinline__ void store_state(float* S, int64_t v_stride, int wave
 
 // ---------------------------------------------------------------------------
 // the verify, phase by phase.  RW holds the q/k/v rows (q, k, v), WK the
-// per-head O(N^2) work arrays (am, pq, x, gc, G, beta, rq, rk, cO, anc); the
+// per-head O(N^2) work arrays (am, x, gc, G, beta, rq, rk, cO, anc); the
 // caller places the barriers between phases.
 // ---------------------------------------------------------------------------
 // One (request, v-head) of a launch.
@@ -494,15 +522,16 @@ __device__ __forceinline__ void dense_ancestry(const dft_verify_args& p, const I
   }
 }
 
-// q/k/v rows -> LDS: one 1 KiB copy fills 4 swizzled rows (3 * NP/16 per wave)
-template <int NP, class RW>
+// q/k/v rows -> LDS: one 1 KiB copy fills 4 swizzled rows (NP/16 per wave and
+// plane).  Planes M0 .. M1-1 of (q, k, v).
+template <int NP, int M0, int M1, class RW>
 __device__ __forceinline__ void issue_rows(const dft_verify_args& p, const Item& it, int wave, int lane,
                                            const void* alt, RW& rw) {
   const int KD = p.hk * kD;
   const int64_t ys = p.y_row_stride;
   const uint16_t* ybase = reinterpret_cast<const uint16_t*>(p.y) + it.row0 * ys;
   const uint16_t* srcs[3] = {ybase + it.hk * kD, ybase + KD + it.hk * kD, ybase + 2 * KD + it.h * kD};
-  uint16_t* dsts[3] = {rw.q, rw.k, rw.v};
+  uint16_t* dsts[3] = {rw.q, rw.k, rw.vrows()};
   const int pc = lane & 15;
 #pragma unroll
   for (int u = 0; u < NP / 16; ++u) {
@@ -511,7 +540,7 @@ __device__ __forceinline__ void issue_rows(const dft_verify_args& p, const Item&
     const int isrc = i < it.n ? i : it.n - 1;  // rows past the tree repeat a real row (finite, masked later)
     const int64_t goff = isrc * ys + 8 * ((pc ^ i) & 15);
 #pragma unroll
-    for (int m = 0; m < 3; ++m) {
+    for (int m = M0; m < M1; ++m) {
       // q and k rows are read again by the k-head's other v-heads (same XCD,
       // same L2); each v row is read once.  Non-temporal v copies measured
       // 1.2% faster at batch 64; non-temporal q/k copies gained nothing.
@@ -612,8 +641,8 @@ __device__ __forceinline__ void phase_saves(const VerifyParams& P, const Item& i
     p.aux_g[(int64_t)it.h * p.aux_g_h_stride + (it.row0 + tid) * p.aux_g_row_stride] = wk.G[tid];
 }
 
-// 1b: output row scales and the ancestor-masked Gram tiles A (transposed into
-// am) and Pq
+// 1b: output row scales and the ancestor-masked Gram tiles of A (transposed
+// into am).  Pq is not stored: phase_m forms its tiles as it needs them.
 template <int NP, class RW, class WK>
 __device__ __forceinline__ void phase_gram(const VerifyParams& P, const Item& it, int tid, const RW& rw, WK& wk) {
   constexpr int MT = NP / 16;
@@ -627,32 +656,26 @@ __device__ __forceinline__ void phase_gram(const VerifyParams& P, const Item& it
   }
   int item = 0;
 #pragma unroll
-  for (int which = 0; which < 2; ++which)
+  for (int ti = 0; ti < MT; ++ti)
 #pragma unroll
-    for (int ti = 0; ti < MT; ++ti)
+    for (int tj = 0; tj <= ti; ++tj, ++item) {
+      if ((item & 3) != wave) continue;
+      f32x4 acc = {};
 #pragma unroll
-      for (int tj = 0; tj <= ti; ++tj, ++item) {
-        if ((item & 3) != wave) continue;
-        const uint16_t* left = which == 0 ? rw.k : rw.q;
-        f32x4 acc = {};
-#pragma unroll
-        for (int s = 0; s < 4; ++s) {
-          const bf16x8 av = *reinterpret_cast<const bf16x8*>(left + qkv_at(16 * ti + n16, 32 * s + 8 * g4));
-          const bf16x8 bv = *reinterpret_cast<const bf16x8*>(rw.k + qkv_at(16 * tj + n16, 32 * s + 8 * g4));
-          acc = mfma_bf16_16x16x32(av, bv, acc);
-        }
-        const int j = 16 * tj + n16;
-        const float rkj = wk.rk[j], Gj = wk.G[j];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int i = 16 * ti + 4 * g4 + r;
-          const bool on = (wk.anc[i] >> j) & 1ull;
-          if (which == 0)
-            wk.am[j * LDA + i] = (on && j < i) ? wk.beta[i] * wk.rk[i] * rkj * acc[r] * __expf(wk.G[i] - Gj) : 0.f;
-          else
-            wk.pq[i * LDA + j] = on ? wk.rq[i] * rkj * acc[r] * __expf(wk.G[i] - Gj) : 0.f;
-        }
+      for (int s = 0; s < 4; ++s) {
+        const bf16x8 av = *reinterpret_cast<const bf16x8*>(rw.k + qkv_at(16 * ti + n16, 32 * s + 8 * g4));
+        const bf16x8 bv = *reinterpret_cast<const bf16x8*>(rw.k + qkv_at(16 * tj + n16, 32 * s + 8 * g4));
+        acc = mfma_bf16_16x16x32(av, bv, acc);
       }
+      const int j = 16 * tj + n16;
+      const float rkj = wk.rk[j], Gj = wk.G[j];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int i = 16 * ti + 4 * g4 + r;
+        const bool on = (wk.anc[i] >> j) & 1ull;
+        wk.am()[j * LDA + i] = (on && j < i) ? wk.beta[i] * wk.rk[i] * rkj * acc[r] * __expf(wk.G[i] - Gj) : 0.f;
+      }
+    }
 }
 
 // 1c: diagonal 16x16 blocks of X by forward substitution (block b on wave b,
@@ -668,14 +691,14 @@ __device__ __forceinline__ void phase_diag(int tid, WK& wk) {
     float xc[16];
 #pragma unroll
     for (int i = 0; i < 16; ++i) xc[i] = (i == j) ? 1.f : 0.f;
-    solve_block16<LDA>(xc, wk.am, 16 * bb);
+    solve_block16<LDA>(xc, wk.am(), 16 * bb);
     materialize16(xc);
 #pragma unroll
-    for (int i = 0; i < 16; ++i) wk.x[(16 * bb + i) * LDA + 16 * bb + j] = xc[i];
+    for (int i = 0; i < 16; ++i) wk.x()[(16 * bb + i) * LDA + 16 * bb + j] = xc[i];
   }
   for (int e = tid; e < NP * NP; e += 256) {
     const int i = e / NP, jj = e % NP;
-    if ((i >> 4) < (jj >> 4)) wk.x[i * LDA + jj] = 0.f;
+    if ((i >> 4) < (jj >> 4)) wk.x()[i * LDA + jj] = 0.f;
   }
 }
 
@@ -691,14 +714,44 @@ __device__ __forceinline__ void phase_offdiag(int tid, int d, WK& wk) {
     f32x4 T = {};
 #pragma unroll
     for (int bm = 0; bm < MT; ++bm)
-      if (bm >= bj && bm < bi) T = block_mma<LDA, true>(T, wk.am, bi, bm, wk.x, bj, n16, g4);
-    store_block<LDA>(wk.x, bi, bj, neg_diag_times<LDA>(wk.x, bi, T, n16, g4), n16, g4);
+      if (bm >= bj && bm < bi) T = block_mma<LDA, true>(T, wk.am(), bi, bm, wk.x(), bj, n16, g4);
+    store_block<LDA>(wk.x(), bi, bj, neg_diag_times<LDA>(wk.x(), bi, T, n16, g4), n16, g4);
   }
 }
 
-// 1e: M = Pq X (block lower triangular; overwrites A)
-template <int NP, class WK>
-__device__ __forceinline__ void phase_m(int tid, WK& wk) {
+// Pq(bi, bm) for phase_m, in the A-operand layout of the fp32 16x16x4 MFMA
+// whose k-step s covers column 16bm + 4g + s: the Gram of the k rows of
+// block bm against the q rows of block bi.  The operands are swapped so the
+// tile comes out transposed (lane (n, g), element r -> i = 16bi + n,
+// j = 16bm + 4g + r), then masked to ancestors-or-self and scaled by
+// rq_i rk_j e^{G_i - G_j}.
+template <class RW, class WK>
+__device__ __forceinline__ f32x4 pq_tile(const RW& rw, const WK& wk, int bi, int bm, int n16, int g4) {
+  f32x4 acc = {};
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    const bf16x8 kv = *reinterpret_cast<const bf16x8*>(rw.k + qkv_at(16 * bm + n16, 32 * s + 8 * g4));
+    const bf16x8 qv = *reinterpret_cast<const bf16x8*>(rw.q + qkv_at(16 * bi + n16, 32 * s + 8 * g4));
+    acc = mfma_bf16_16x16x32(kv, qv, acc);
+  }
+  const int i = 16 * bi + n16;
+  const uint64_t ai = wk.anc[i];
+  const float rqi = wk.rq[i], Gi = wk.G[i];
+  f32x4 out;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int j = 16 * bm + 4 * g4 + r;
+    out[r] = ((ai >> j) & 1ull) ? rqi * wk.rk[j] * acc[r] * __expf(Gi - wk.G[j]) : 0.f;
+  }
+  return out;
+}
+
+// 1e: M = Pq X (block lower triangular; overwrites A).  A block's Pq tiles are
+// formed in registers (pq_tile) and fed straight to the MFMA, so Pq never
+// takes LDS; a tile shared by several M blocks of different waves is formed
+// once per block.
+template <int NP, class RW, class WK>
+__device__ __forceinline__ void phase_m(int tid, const RW& rw, WK& wk) {
   constexpr int MT = NP / 16;
   constexpr int LDA = WK::LDA;
   const int lane = tid & 63, wave = tid >> 6, n16 = lane & 15, g4 = lane >> 4;
@@ -711,10 +764,14 @@ __device__ __forceinline__ void phase_m(int tid, WK& wk) {
       f32x4 acc = {};
       if (bj <= bi) {
 #pragma unroll
-        for (int bm = 0; bm < MT; ++bm)
-          if (bm >= bj && bm <= bi) acc = block_mma<LDA, false>(acc, wk.pq, bi, bm, wk.x, bj, n16, g4);
+        for (int bm = 0; bm < MT; ++bm) {
+          if (bm < bj || bm > bi) continue;
+          const f32x4 a = pq_tile(rw, wk, bi, bm, n16, g4);
+#pragma unroll
+          for (int s = 0; s < 4; ++s) acc = mfma_f32_16x16x4(a[s], wk.x()[(16 * bm + 4 * g4 + s) * LDA + 16 * bj + n16], acc);
+        }
       }
-      store_block<LDA>(wk.am, bi, bj, acc, n16, g4);
+      store_block<LDA>(wk.am(), bi, bj, acc, n16, g4);
     }
 }
 
@@ -780,7 +837,7 @@ __device__ __forceinline__ void phase_w(int lane, int wave, const RW& rw, const 
       for (int e = 0; e < 8; ++e) {
         const int mt = 2 * ks + (e >> 2), r = e & 3;
         const int i = 16 * mt + 4 * g4 + r;
-        const float vv = bf16_bits_to_f32(rw.v[qkv_at(i, col)]);
+        const float vv = bf16_bits_to_f32(rw.vrows()[qkv_at(i, col)]);
         w8[e] = wk.beta[i] * (vv - wk.gc[i] * ck[mt][t][r]);
       }
       split_bf16x8(w8, wh[ks][t], wl[ks][t]);
@@ -788,7 +845,7 @@ __device__ __forceinline__ void phase_w(int lane, int wave, const RW& rw, const 
 }
 
 // 3b: [X; M] W, tiles mo < MT give vn and tiles mo >= MT give M W (o adds
-// cO * Cq).  Computed transposed (W as the A operand), so lane (n, g) holds
+// cO * Cq); every wave does its vn tiles before its o tiles.  Computed transposed (W as the A operand), so lane (n, g) holds
 // node 16mt + n at the four consecutive columns 16t + 4g .. +3: one 16-byte
 // (vn) or 8-byte (o) write each.  Staged into the (then free) q/k/v region of
 // rw when the flags allow, else stored directly.
@@ -802,11 +859,14 @@ __device__ __forceinline__ void phase_out(const VerifyParams& P, const Item& it,
   const dft_verify_args& p = P.a;
   const int n16 = lane & 15, g4 = lane >> 4;
   float* vn_s = reinterpret_cast<float*>(rw.q);  // spans q and k
-  uint16_t* o_s = rw.v;
+  uint16_t* o_s = rw.ostage();
 #pragma unroll
   for (int mo = 0; mo < 2 * MT; ++mo) {
+    // the late-v form stages o in x: every wave must be done with X first
+    if constexpr (RW::kLateV)
+      if (mo == MT) __syncthreads();
     const int mt = mo % MT;
-    const float* src = mo < MT ? wk.x : wk.am;
+    const float* src = mo < MT ? wk.x() : wk.am();
     f32x4 acc[2] = {f32x4{}, f32x4{}};
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
@@ -861,7 +921,7 @@ template <int NP, class RW>
 __device__ __forceinline__ void phase_stores(const VerifyParams& P, const Item& it, int tid, const RW& rw) {
   const dft_verify_args& p = P.a;
   const float* vn_s = reinterpret_cast<const float*>(rw.q);
-  const uint16_t* o_s = rw.v;
+  const uint16_t* o_s = rw.ostage();
   if (P.vn_stage) {  // rows of 32 x 16 bytes
     float* dst = p.aux_v + (int64_t)it.h * p.aux_v_h_stride + it.row0 * p.aux_v_row_stride;
 #pragma unroll
@@ -889,7 +949,8 @@ __device__ __forceinline__ void phase_stores(const VerifyParams& P, const Item& 
 template <int NP, bool S0VEC, bool COMMIT>
 __device__ __forceinline__ void verify_body(const VerifyParams& P) {
   constexpr int MT = NP / 16;
-  constexpr int kQkvDma = 3 * (NP / 16);  // row copies per wave
+  constexpr int kPlanes = VerifySmem<NP>::kLateV ? 2 : 3;  // the late form copies its v rows after Cq/Ck
+  constexpr int kQkvDma = kPlanes * (NP / 16);                // row copies per wave
   const dft_verify_args& p = P.a;
   __shared__ VerifySmem<NP> sm;
 
@@ -924,7 +985,7 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
   // (fused form: the pending path's entry words travel in gate row 4)
   if (wave == 0) issue_gates(p, it, lane, S0, sm.graw, COMMIT ? path_word(P.c, it.b, lane) : nullptr);
   if (p.anc_f32) dense_ancestry<NP>(p, it, wave, lane, sm);
-  issue_rows<NP>(p, it, wave, lane, S0, sm);
+  issue_rows<NP, 0, kPlanes>(p, it, wave, lane, S0, sm);
   asm volatile("" ::: "memory");
 
   f32x4 s0r[2][8];
@@ -959,7 +1020,7 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
   // Fused form: the previous step's path (its entry words came with the
   // gates) is decoded and its keys, values and gains are fetched behind the
   // state; the norms overlap both streams.  As soon as they have landed the
-  // path is committed into the tile (keys staged in am + pq, still unused)
+  // path is committed into the tile (keys staged in am + x, still unused)
   // and the tile goes back to its slot, so that the write-back streams under
   // the rest of phase 1.
   Pending pd{};
@@ -977,7 +1038,7 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
     // flight past the (conditional) write-back
     __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 15));
     if (pd.last >= 0) store_state(const_cast<float*>(S0), p.state_v_stride, wave, lane, s0r);
-    __syncthreads();  // every wave has read its keys: am and pq take the Gram tiles
+    __syncthreads();  // every wave has read its keys: am and x take the Gram tiles and X
   }
   phase_saves<NP>(P, it, tid, sm, sm);
   phase_gram<NP>(P, it, tid, sm, sm);
@@ -989,11 +1050,16 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
     phase_offdiag<NP>(tid, d, sm);
     __syncthreads();
   }
-  phase_m<NP>(tid, sm);
+  phase_m<NP>(tid, sm, sm);
 
   f32x4 cq[MT][2], ck[MT][2];
   phase_cq_ck<NP>(lane, sm, s0r, cq, ck);
-  __syncthreads();  // X and M complete
+  __syncthreads();  // X and M complete (every wave is done with the q rows)
+  if constexpr (VerifySmem<NP>::kLateV) {
+    issue_rows<NP, 2, 3>(p, it, wave, lane, S0, sm);  // the v rows, into the q region
+    __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 15));
+    __syncthreads();
+  }
   bf16x8 wh[NP / 32][2], wl[NP / 32][2];
   phase_w<NP>(lane, wave, sm, sm, ck, wh, wl);
   __syncthreads();  // every wave has read its v rows: the q/k/v region takes the outputs
