@@ -18,14 +18,19 @@
 //     v_mfma_f32_16x16x32_bf16 (lane (n = l%16, g = l/16) loads 16 bytes at
 //     k = 16j + 4g of state row n: the 4 lanes of a row cover a 64-byte
 //     sector per instruction); q/k/v rows, gates and ancestry go to LDS.
-//  1. while the state is in flight: norms, G, the Gram tiles (A, Pq), the
+//  1. while the state is in flight: norms, G, the Gram tiles of A, the
 //     blocked inverse X (16x16 diagonal blocks by forward substitution,
-//     off-diagonal blocks X_ij = -D_i sum_m A_im X_mj by fp32 MFMA) and M.
+//     off-diagonal blocks X_ij = -D_i sum_m A_im X_mj by fp32 MFMA) and
+//     M = Pq X with the Pq tiles formed in registers as they are consumed.
 //  2. Cq, Ck on the wave's 32 value columns.
-//  3. [X; M] W as one bf16x3 MFMA product (hi*hi + hi*lo + lo*hi) whose B
+//  3. [X; M] W as one bf16x3 MFMA product (hi*hi + hi*lo + lo*hi) whose A
 //     operand is W in the accumulator layout of phase 2, read with the node
-//     permutation that layout implies: nothing is transposed or staged.
-// Every wave streams its own columns; LDS holds only per-head O(N^2) data.
+//     permutation that layout implies; the product comes out transposed, so
+//     vn and o leave through LDS as whole row pieces.
+// Every wave streams its own columns of the state; LDS holds the q/k/v rows
+// and the per-head O(N^2) arrays.  The fused commit -> verify form commits
+// the previous step's accepted path into the tile as soon as it has landed
+// and writes it back before the Gram phase.
 #include <climits>
 
 #include "dft_device.h"
@@ -641,66 +646,69 @@ __device__ __forceinline__ void phase_saves(const VerifyParams& P, const Item& i
     p.aux_g[(int64_t)it.h * p.aux_g_h_stride + (it.row0 + tid) * p.aux_g_row_stride] = wk.G[tid];
 }
 
-// 1b: output row scales and the ancestor-masked Gram tiles of A (transposed
-// into am).  Pq is not stored: phase_m forms its tiles as it needs them.
+// 1b/1c: output row scales, the ancestor-masked Gram tiles of A (transposed
+// into am) and the diagonal 16x16 blocks of X.  Wave b < NP/16 forms tile
+// (b, b) and solves it at once by forward substitution (lane j = column j):
+// the solve reads only LDS this wave wrote, and one wave's LDS operations
+// are ordered, so no workgroup barrier stands between the two.  The
+// off-diagonal tiles follow, spread over the waves, and X above the
+// diagonal blocks is zeroed by everyone.  Pq is not stored: phase_m forms
+// its tiles as it needs them.
 template <int NP, class RW, class WK>
-__device__ __forceinline__ void phase_gram(const VerifyParams& P, const Item& it, int tid, const RW& rw, WK& wk) {
+__device__ __forceinline__ void a_tile(const RW& rw, WK& wk, int ti, int tj, int n16, int g4) {
+  constexpr int LDA = WK::LDA;
+  f32x4 acc = {};
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    const bf16x8 av = *reinterpret_cast<const bf16x8*>(rw.k + qkv_at(16 * ti + n16, 32 * s + 8 * g4));
+    const bf16x8 bv = *reinterpret_cast<const bf16x8*>(rw.k + qkv_at(16 * tj + n16, 32 * s + 8 * g4));
+    acc = mfma_bf16_16x16x32(av, bv, acc);
+  }
+  const int j = 16 * tj + n16;
+  const float rkj = wk.rk[j], Gj = wk.G[j];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int i = 16 * ti + 4 * g4 + r;
+    const bool on = (wk.anc[i] >> j) & 1ull;
+    wk.am()[j * LDA + i] = (on && j < i) ? wk.beta[i] * wk.rk[i] * rkj * acc[r] * __expf(wk.G[i] - Gj) : 0.f;
+  }
+}
+
+template <int NP, class RW, class WK>
+__device__ __forceinline__ void phase_gram_diag(int tid, const RW& rw, WK& wk) {
   constexpr int MT = NP / 16;
   constexpr int LDA = WK::LDA;
-  const dft_verify_args& p = P.a;
   const int lane = tid & 63, wave = tid >> 6, n16 = lane & 15, g4 = lane >> 4;
   if (tid < NP) {
     const float eG = __expf(wk.G[tid]);
     wk.gc[tid] = eG * wk.rk[tid];  // g is no longer needed
     wk.cO[tid] = eG * wk.rq[tid];
   }
+  if (wave < MT) {
+    a_tile<NP>(rw, wk, wave, wave, n16, g4);
+    if (lane < 16) {
+      const int bb = wave, j = lane;
+      float xc[16];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) xc[i] = (i == j) ? 1.f : 0.f;
+      solve_block16<LDA>(xc, wk.am(), 16 * bb);
+      materialize16(xc);
+#pragma unroll
+      for (int i = 0; i < 16; ++i) wk.x()[(16 * bb + i) * LDA + 16 * bb + j] = xc[i];
+    }
+  }
   int item = 0;
 #pragma unroll
-  for (int ti = 0; ti < MT; ++ti)
+  for (int ti = 1; ti < MT; ++ti)
 #pragma unroll
-    for (int tj = 0; tj <= ti; ++tj, ++item) {
-      if ((item & 3) != wave) continue;
-      f32x4 acc = {};
-#pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const bf16x8 av = *reinterpret_cast<const bf16x8*>(rw.k + qkv_at(16 * ti + n16, 32 * s + 8 * g4));
-        const bf16x8 bv = *reinterpret_cast<const bf16x8*>(rw.k + qkv_at(16 * tj + n16, 32 * s + 8 * g4));
-        acc = mfma_bf16_16x16x32(av, bv, acc);
-      }
-      const int j = 16 * tj + n16;
-      const float rkj = wk.rk[j], Gj = wk.G[j];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int i = 16 * ti + 4 * g4 + r;
-        const bool on = (wk.anc[i] >> j) & 1ull;
-        wk.am()[j * LDA + i] = (on && j < i) ? wk.beta[i] * wk.rk[i] * rkj * acc[r] * __expf(wk.G[i] - Gj) : 0.f;
-      }
-    }
-}
-
-// 1c: diagonal 16x16 blocks of X by forward substitution (block b on wave b,
-// lane j = column, so the serial chains run on different SIMDs); X above the
-// diagonal blocks is zeroed by everyone
-template <int NP, class WK>
-__device__ __forceinline__ void phase_diag(int tid, WK& wk) {
-  constexpr int MT = NP / 16;
-  constexpr int LDA = WK::LDA;
-  const int lane = tid & 63, wave = tid >> 6;
-  if (wave < MT && lane < 16) {
-    const int bb = wave, j = lane;
-    float xc[16];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) xc[i] = (i == j) ? 1.f : 0.f;
-    solve_block16<LDA>(xc, wk.am(), 16 * bb);
-    materialize16(xc);
-#pragma unroll
-    for (int i = 0; i < 16; ++i) wk.x()[(16 * bb + i) * LDA + 16 * bb + j] = xc[i];
-  }
+    for (int tj = 0; tj < ti; ++tj, ++item)
+      if (((MT + item) & 3) == wave) a_tile<NP>(rw, wk, ti, tj, n16, g4);
   for (int e = tid; e < NP * NP; e += 256) {
     const int i = e / NP, jj = e % NP;
     if ((i >> 4) < (jj >> 4)) wk.x()[i * LDA + jj] = 0.f;
   }
 }
+
 
 // 1d, one level: off-diagonal blocks X_ij = -D_i sum_{m=j}^{i-1} A_im X_mj at
 // distance d = i - j (each level needs the previous ones)
@@ -1041,9 +1049,7 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
     __syncthreads();  // every wave has read its keys: am and x take the Gram tiles and X
   }
   phase_saves<NP>(P, it, tid, sm, sm);
-  phase_gram<NP>(P, it, tid, sm, sm);
-  __syncthreads();
-  phase_diag<NP>(tid, sm);
+  phase_gram_diag<NP>(tid, sm, sm);
   __syncthreads();
 #pragma unroll
   for (int d = 1; d < MT; ++d) {
