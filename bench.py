@@ -45,6 +45,7 @@ def parse():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-ragged", action="store_true", help="skip the packed ragged workload's line")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--eager", action="store_true", help="time eager launches instead of a HIP graph")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -344,12 +345,15 @@ def main():
     t_conv = time_graph(lambda: [w.conv() for _ in range(L)], reps_kernel, args.warmup, args.eager) / L
     w.mask_setup(dev)
     t_mask = time_graph(lambda: [w.mask() for _ in range(L)], reps_kernel, args.warmup, args.eager) / L
-    rw = RaggedWorkload(dev)  # both workloads fit together (about 17 GB)
-    t_ragged = time_graph(lambda: [rw.verify(l) for l in range(L)], reps_kernel, args.warmup, args.eager) / L
-    ragged = {"workload": "packed ragged batch: 128 requests, trees of 8-64 nodes (chains / bushy / random), verify",
-              "nodes": rw.rows, "us_per_layer": round(t_ragged * 1e3, 2),
-              "nodes_per_s_per_layer": round(rw.rows / (t_ragged * 1e-3), 1),
-              "hbm_frac": round(rw.bytes_per_launch() / (t_ragged * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+    ragged = None
+    if not args.no_ragged:
+        rw = RaggedWorkload(dev)  # both workloads fit together (about 17 GB)
+        t_ragged = time_graph(lambda: [rw.verify(l) for l in range(L)], reps_kernel, args.warmup, args.eager) / L
+        ragged = {"workload": "packed ragged batch: 128 requests, trees of 8-64 nodes (chains / bushy / random), "
+                              "verify",
+                  "nodes": rw.rows, "us_per_layer": round(t_ragged * 1e3, 2),
+                  "nodes_per_s_per_layer": round(rw.rows / (t_ragged * 1e-3), 1),
+                  "hbm_frac": round(rw.bytes_per_launch() / (t_ragged * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
     if args.copy_calibration:
         src = torch.ones(1 << 28, device=dev)
         dst = torch.empty_like(src)
