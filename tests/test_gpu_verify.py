@@ -224,3 +224,26 @@ def test_verify_kmajor_state_element_loads(cuda):
     st = batch.state.transpose(-1, -2).contiguous()           # [B, hv, K, V]
     o, k, v, g = run_gpu(batch, cuda, state=st.to(cuda).transpose(-1, -2), packed=True)
     check_against_oracle(batch, o, k, v, g)
+
+
+def test_verify_kmajor_state_64_wide_split(cuda):
+    """Element loads on the 64-wide kernel (late v rows, o staged in X) and
+    the size split: a packed batch whose trees straddle 32 nodes."""
+    from dforktree_amd import synth
+    announce("verify k-major state, 64-wide split")
+    batch = synth.make_batch(18, 0, [64, 9, 40, 33, 32, 1], hk=2, hv=4,
+                             kinds=["chain", "random", "bushy", "random", "chain", "random"])
+    st = batch.state.transpose(-1, -2).contiguous()
+    o, k, v, g = run_gpu(batch, cuda, state=st.to(cuda).transpose(-1, -2), packed=True)
+    check_against_oracle(batch, o, k, v, g)
+
+
+@pytest.mark.parametrize("o_dtype", [torch.bfloat16, torch.float32])
+def test_verify_64_wide_output_forms(cuda, o_dtype):
+    """The 64-wide kernel with staged bf16 output (o staged in X) and with
+    direct fp32 stores, trees of 33-64 nodes only."""
+    from dforktree_amd import synth
+    announce(f"verify 64-wide {o_dtype}")
+    batch = synth.make_batch(19, 0, [64, 48, 33, 57], hk=2, hv=4, kinds=["random", "chain", "bushy", "random"])
+    o, k, v, g = run_gpu(batch, cuda, o_dtype=o_dtype, packed=True)
+    check_against_oracle(batch, o, k, v, g, o_bf16=(o_dtype == torch.bfloat16))
