@@ -807,17 +807,20 @@ __device__ __forceinline__ void phase_m(int tid, const RW& rw, WK& wk) {
 // the same registers: Ck comes out as [node][column] (lane n, g, element r ->
 // node 16mt + 4g + r, column 16t + n), Cq as [column][node] (node 16mt + n,
 // column 16t + 4g + r), the layout of the output tiles.
-template <int NP, class RW>
+// WHICH: 3 = both products, 1 = Cq only, 2 = Ck only (a two-pass form that
+// splits the state into hi/lo twice but frees the q rows after the first).
+template <int NP, int WHICH = 3, class RW>
 __device__ __forceinline__ void phase_cq_ck(int lane, const RW& rw, const f32x4 (&s0r)[2][8], f32x4 (&cq)[NP / 16][2],
                                             f32x4 (&ck)[NP / 16][2]) {
   constexpr int MT = NP / 16;
+  constexpr bool DQ = (WHICH & 1) != 0, DK = (WHICH & 2) != 0;
   const int n16 = lane & 15, g4 = lane >> 4;
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
-      cq[mt][t] = f32x4{};
-      ck[mt][t] = f32x4{};
+      if (DQ) cq[mt][t] = f32x4{};
+      if (DK) ck[mt][t] = f32x4{};
     }
 #pragma unroll
   for (int s = 0; s < 4; ++s) {
@@ -831,14 +834,15 @@ __device__ __forceinline__ void phase_cq_ck(int lane, const RW& rw, const f32x4 
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
       const int row = 16 * mt + n16, c0 = 32 * s + 4 * g4;
-      const bf16x8 aq = lds_bf16x8_split(rw.q + qkv_at(row, c0), rw.q + qkv_at(row, c0 + 16));
-      const bf16x8 ak = lds_bf16x8_split(rw.k + qkv_at(row, c0), rw.k + qkv_at(row, c0 + 16));
+      bf16x8 aq{}, ak{};
+      if (DQ) aq = lds_bf16x8_split(rw.q + qkv_at(row, c0), rw.q + qkv_at(row, c0 + 16));
+      if (DK) ak = lds_bf16x8_split(rw.k + qkv_at(row, c0), rw.k + qkv_at(row, c0 + 16));
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
-        cq[mt][t] = mfma_bf16_16x16x32(bhi[t], aq, cq[mt][t]);
-        ck[mt][t] = mfma_bf16_16x16x32(ak, bhi[t], ck[mt][t]);
-        cq[mt][t] = mfma_bf16_16x16x32(blo[t], aq, cq[mt][t]);
-        ck[mt][t] = mfma_bf16_16x16x32(ak, blo[t], ck[mt][t]);
+        if (DQ) cq[mt][t] = mfma_bf16_16x16x32(bhi[t], aq, cq[mt][t]);
+        if (DK) ck[mt][t] = mfma_bf16_16x16x32(ak, bhi[t], ck[mt][t]);
+        if (DQ) cq[mt][t] = mfma_bf16_16x16x32(blo[t], aq, cq[mt][t]);
+        if (DK) ck[mt][t] = mfma_bf16_16x16x32(ak, blo[t], ck[mt][t]);
       }
     }
   }
@@ -1087,12 +1091,18 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
   phase_m<NP>(tid, sm, sm);
 
   f32x4 cq[MT][2], ck[MT][2];
-  phase_cq_ck<NP>(lane, sm, s0r, cq, ck);
-  __syncthreads();  // X and M complete (every wave is done with the q rows)
   if constexpr (VerifySmem<NP>::kLateV) {
-    issue_rows<NP, 2, 3>(p, it, wave, lane, S0, sm);  // the v rows, into the q region
+    // Cq first; once every wave is done with the q rows, the v rows are
+    // copied into their region while Ck computes
+    phase_cq_ck<NP, 1>(lane, sm, s0r, cq, ck);
+    __syncthreads();  // X and M complete, the q rows consumed
+    issue_rows<NP, 2, 3>(p, it, wave, lane, S0, sm);
+    phase_cq_ck<NP, 2>(lane, sm, s0r, cq, ck);
     __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 15));
     __syncthreads();
+  } else {
+    phase_cq_ck<NP>(lane, sm, s0r, cq, ck);
+    __syncthreads();  // X and M complete
   }
   bf16x8 wh[NP / 32][2], wl[NP / 32][2];
   phase_w<NP>(lane, wave, sm, sm, ck, wh, wl);
