@@ -771,6 +771,19 @@ __device__ __forceinline__ f32x4 pq_tile(const RW& rw, const WK& wk, int bi, int
   return out;
 }
 
+// Wave that forms M block (bi, bj).  Block (bi, bj <= bi) sums bi - bj + 1
+// Pq X terms.  For 2 x 2 blocks every wave takes one block; for 4 x 4 (20
+// terms) every wave takes 5, where a column per wave would give wave 0 ten.
+template <int MT>
+__device__ __forceinline__ constexpr int m_owner(int bi, int bj) {
+  if constexpr (MT == 4) {
+    constexpr int own[4][4] = {{0, 1, 2, 3}, {1, 3, 0, 1}, {2, 3, 3, 2}, {0, 1, 2, 3}};
+    return own[bi][bj];
+  } else {
+    return (bi * MT + bj) & 3;
+  }
+}
+
 // 1e: M = Pq X (block lower triangular; overwrites A).  A block's Pq tiles are
 // formed in registers (pq_tile) and fed straight to the MFMA, so Pq never
 // takes LDS; a tile shared by several M blocks of different waves is formed
@@ -780,12 +793,11 @@ __device__ __forceinline__ void phase_m(int tid, const RW& rw, WK& wk) {
   constexpr int MT = NP / 16;
   constexpr int LDA = WK::LDA;
   const int lane = tid & 63, wave = tid >> 6, n16 = lane & 15, g4 = lane >> 4;
-  int blk = 0;
 #pragma unroll
   for (int bi = 0; bi < MT; ++bi)
 #pragma unroll
-    for (int bj = 0; bj < MT; ++bj, ++blk) {
-      if ((blk & 3) != wave) continue;
+    for (int bj = 0; bj < MT; ++bj) {
+      if (m_owner<MT>(bi, bj) != wave) continue;
       f32x4 acc = {};
       if (bj <= bi) {
 #pragma unroll
