@@ -668,9 +668,14 @@ __device__ __forceinline__ void phase_saves(const VerifyParams& P, const Item& i
 // (b, b) and solves it at once by forward substitution (lane j = column j):
 // the solve reads only LDS this wave wrote, and one wave's LDS operations
 // are ordered, so no workgroup barrier stands between the two.  The
-// off-diagonal tiles follow, spread over the waves, and X above the
-// diagonal blocks is zeroed by everyone.  Pq is not stored: phase_m forms
-// its tiles as it needs them.
+// off-diagonal tiles follow, spread over the waves.  Pq is not stored:
+// phase_m forms its tiles as it needs them.
+//
+// Of X above its diagonal blocks only blocks (b, b + 1), b even, are ever
+// read: phase_out's 32-wide k-steps pair block columns 2s and 2s + 1 and skip
+// the steps wholly above the diagonal.  Each thread zeroes one element of each.
+// ZERO_ALL zeroes everything above the diagonal blocks instead: with the
+// shorter form the fused 32-wide kernel (at its 128-register budget) spills.
 template <int NP, class RW, class WK>
 __device__ __forceinline__ void a_tile(const RW& rw, WK& wk, int ti, int tj, int n16, int g4) {
   constexpr int LDA = WK::LDA;
@@ -691,7 +696,7 @@ __device__ __forceinline__ void a_tile(const RW& rw, WK& wk, int ti, int tj, int
   }
 }
 
-template <int NP, class RW, class WK>
+template <int NP, bool ZERO_ALL, class RW, class WK>
 __device__ __forceinline__ void phase_gram_diag(int tid, const RW& rw, WK& wk) {
   constexpr int MT = NP / 16;
   constexpr int LDA = WK::LDA;
@@ -720,9 +725,14 @@ __device__ __forceinline__ void phase_gram_diag(int tid, const RW& rw, WK& wk) {
 #pragma unroll
     for (int tj = 0; tj < ti; ++tj, ++item)
       if (((MT + item) & 3) == wave) a_tile<NP>(rw, wk, ti, tj, n16, g4);
-  for (int e = tid; e < NP * NP; e += 256) {
-    const int i = e / NP, jj = e % NP;
-    if ((i >> 4) < (jj >> 4)) wk.x()[i * LDA + jj] = 0.f;
+  if constexpr (ZERO_ALL) {
+    for (int e = tid; e < NP * NP; e += 256) {
+      const int i = e / NP, jj = e % NP;
+      if ((i >> 4) < (jj >> 4)) wk.x()[i * LDA + jj] = 0.f;
+    }
+  } else {
+#pragma unroll
+    for (int b = 0; b + 1 < MT; b += 2) wk.x()[(16 * b + (tid >> 4)) * LDA + 16 * (b + 1) + (tid & 15)] = 0.f;
   }
 }
 
@@ -787,7 +797,8 @@ __device__ __forceinline__ constexpr int m_owner(int bi, int bj) {
 // 1e: M = Pq X (block lower triangular; overwrites A).  A block's Pq tiles are
 // formed in registers (pq_tile) and fed straight to the MFMA, so Pq never
 // takes LDS; a tile shared by several M blocks of different waves is formed
-// once per block.
+// once per block.  Above the diagonal only the zero blocks (b, b + 1), b
+// even, are written: phase_out reads no others (as for X).
 template <int NP, class RW, class WK>
 __device__ __forceinline__ void phase_m(int tid, const RW& rw, WK& wk) {
   constexpr int MT = NP / 16;
@@ -797,6 +808,7 @@ __device__ __forceinline__ void phase_m(int tid, const RW& rw, WK& wk) {
   for (int bi = 0; bi < MT; ++bi)
 #pragma unroll
     for (int bj = 0; bj < MT; ++bj) {
+      if (bj > bi && (bj != bi + 1 || (bi & 1))) continue;
       if (m_owner<MT>(bi, bj) != wave) continue;
       f32x4 acc = {};
       if (bj <= bi) {
@@ -1091,7 +1103,7 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
   }
   if constexpr (kSplit) issue_state_group<false>(S0, p.state_v_stride, wave, lane, 1, s0r);
   phase_saves<NP>(P, it, tid, sm, sm);
-  phase_gram_diag<NP>(tid, sm, sm);
+  phase_gram_diag<NP, COMMIT && NP == 32>(tid, sm, sm);
   if constexpr (kSplit) issue_state_group<false>(S0, p.state_v_stride, wave, lane, 2, s0r);
   __syncthreads();
 #pragma unroll
