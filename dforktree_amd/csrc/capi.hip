@@ -21,6 +21,10 @@ bool float_tag(int32_t t) { return t == DFT_F32 || t == DFT_BF16 || t == DFT_F16
 bool index_tag(int32_t t) { return t == DFT_I32 || t == DFT_I64; }
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// A grid's x extent counts work-items in 32 bits: at most this many
+// workgroups of `threads` threads.
+constexpr int64_t max_blocks(int threads) { return (int64_t)0xffffffffll / threads; }
+
 // Checks shared by the verify entry points: DFT_OK to launch, DFT_ERR_* to
 // refuse, or -1 when there is nothing to do.
 int verify_status(const dft_verify_args* a) {
@@ -40,7 +44,7 @@ int verify_status(const dft_verify_args* a) {
   if (a->state_indices && !index_tag(a->state_indices_dtype)) return DFT_ERR_INVALID;
   // q/k/v rows are copied as 16-byte pieces
   if (!aligned16(a->y) || a->y_row_stride % 8 != 0) return DFT_ERR_INVALID;
-  if ((int64_t)a->batch * a->hv > INT32_MAX) return DFT_ERR_UNSUPPORTED;
+  if ((int64_t)a->batch * a->hv > max_blocks(256)) return DFT_ERR_UNSUPPORTED;
   return DFT_OK;
 }
 
@@ -86,6 +90,7 @@ int dft_block_inverse(float* x, int32_t n_mats, int32_t n, int64_t mat_stride, v
   if (n_mats < 0 || n < 0 || n > 64) return DFT_ERR_INVALID;
   if (n_mats == 0 || n == 0) return DFT_OK;
   if (!x || mat_stride < (int64_t)n * n) return DFT_ERR_INVALID;
+  if (n_mats > max_blocks(64)) return DFT_ERR_UNSUPPORTED;
   return dft::launch_block_inverse(x, n_mats, n, mat_stride, static_cast<hipStream_t>(stream));
 }
 
@@ -95,6 +100,9 @@ int dft_tree_conv(const dft_conv_args* a, void* stream) {
   if (a->width < 1 || a->width > 8) return DFT_ERR_UNSUPPORTED;
   if (a->batch == 0 || a->n_nodes == 0 || a->channels == 0) return DFT_OK;
   if (a->n_nodes > 65535 || a->batch > 65535) return DFT_ERR_UNSUPPORTED;
+  // the width-4 bf16 path launches one workgroup per (request, node, 2048 channels), rounded to 8 requests
+  const int64_t pairs8 = ((int64_t)a->batch * ((a->channels + 2047) / 2048) + 7) / 8;
+  if (pairs8 * 8 * a->n_nodes > max_blocks(256)) return DFT_ERR_UNSUPPORTED;
   if (!a->x || !a->conv_state || !a->weight || !a->cidx || !a->y) return DFT_ERR_INVALID;
   if (!float_tag(a->x_dtype) || !float_tag(a->cs_dtype) || !float_tag(a->w_dtype) || !float_tag(a->y_dtype))
     return DFT_ERR_INVALID;
@@ -124,7 +132,7 @@ int dft_tree_commit(const dft_commit_args* a, void* stream) {
   // several ends writing one in-place state would race
   if (a->dst == a->src && a->n_ends != 1) return DFT_ERR_INVALID;
   const int64_t blocks = (int64_t)a->n_layers * a->batch * a->hv * a->n_ends;
-  if (blocks > INT32_MAX) return DFT_ERR_UNSUPPORTED;
+  if (blocks > max_blocks(256)) return DFT_ERR_UNSUPPORTED;
   return dft::launch_tree_commit(a, static_cast<hipStream_t>(stream));
 }
 
@@ -133,6 +141,7 @@ int dft_tree_struct(const dft_tree_args* a, void* stream) {
   if (a->batch < 0 || a->n_nodes < 0 || a->n_nodes > 64) return DFT_ERR_INVALID;
   if (a->kc < 0 || a->kc > 16) return DFT_ERR_UNSUPPORTED;
   if (a->batch == 0) return DFT_OK;
+  if (((int64_t)a->batch + 3) / 4 > max_blocks(256)) return DFT_ERR_UNSUPPORTED;  // a wave per request
   if (!a->parent || !index_tag(a->parent_dtype)) return DFT_ERR_INVALID;
   if (a->depth && !index_tag(a->depth_dtype)) return DFT_ERR_INVALID;
   if (a->cidx && (!index_tag(a->cidx_dtype) || a->kc < 1)) return DFT_ERR_INVALID;

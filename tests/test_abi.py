@@ -132,6 +132,38 @@ def test_validation_rejects_bad_descriptors_without_launching():
     assert lib.dft_error_string(2) == b"unsupported configuration"
 
 
+def test_validation_refuses_grids_past_the_launch_limit():
+    """A grid's x extent counts work-items in 32 bits, so at most
+    (2**32 - 1) // 256 workgroups of 256 threads: larger batches are refused
+    as unsupported on the host instead of failing at launch."""
+    from dforktree_amd import _lib
+    lib = _lib.load()
+    limit = (2**32 - 1) // 256
+    v = _lib.VerifyArgs()
+    v.n_nodes, v.hk, v.hv, v.dk, v.dv = 32, 1, 8, 128, 128
+    v.y = v.a = v.b = v.A_log = v.dt_bias = v.state = v.o = v.anc_bits = 16
+    v.a_dtype = v.b_dtype = v.dt_bias_dtype = v.A_log_dtype = v.o_dtype = _lib.DFT_F32
+    v.y_row_stride = 8
+    v.batch = limit // 8 + 1  # batch * hv workgroups
+    assert lib.dft_tree_verify(ctypes.byref(v), None) == _lib.DFT_ERR_UNSUPPORTED
+    c = _lib.CommitArgs()
+    c.n_layers, c.batch, c.hv, c.dk, c.dv, c.n_nodes, c.path_cols, c.n_ends, c.k_head_div = 24, 1, 32, 128, 128, 32, 16, 1, 1
+    c.path = c.keys = c.values = c.gains = c.src = c.dst = 16
+    c.path_dtype = _lib.DFT_I32
+    c.batch = limit // (24 * 32) + 1  # layers * batch * heads workgroups
+    assert lib.dft_tree_commit(ctypes.byref(c), None) == _lib.DFT_ERR_UNSUPPORTED
+    k = _lib.ConvArgs()
+    k.batch, k.n_nodes, k.channels, k.width = 65535, 65535, 8192, 4  # 4 workgroups per (request, node)
+    k.x = k.conv_state = k.weight = k.cidx = k.y = 16
+    k.cidx_dtype = _lib.DFT_I32
+    assert lib.dft_tree_conv(ctypes.byref(k), None) == _lib.DFT_ERR_UNSUPPORTED
+    assert lib.dft_block_inverse(16, 2**31 - 1, 64, 64 * 64, None) == _lib.DFT_ERR_UNSUPPORTED  # 64-thread groups
+    t = _lib.TreeArgs()
+    t.batch, t.n_nodes, t.kc = 2**31 - 1, 32, 4  # four requests per workgroup
+    t.parent, t.parent_dtype = 16, _lib.DFT_I32
+    assert lib.dft_tree_struct(ctypes.byref(t), None) == _lib.DFT_ERR_UNSUPPORTED
+
+
 def test_python_layer_refuses_cpu_tensors():
     """No CPU fallback: the operators take device tensors only."""
     import torch
