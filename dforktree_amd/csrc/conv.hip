@@ -55,8 +55,12 @@ __global__ void __launch_bounds__(256) tree_conv_kernel(const dft_conv_args p) {
 // / window, channel-contiguous rows.  A block of 256 threads covers 2048
 // channels of one node; a thread owns 8 consecutive channels, so every
 // gathered token row, the weights (8 channels x 4 taps) and the output are
-// 16-byte accesses.  The gather columns are uniform over the block (scalar
-// loads), and the token loads are issued before anything else is fetched.
+// 16-byte accesses.  The gather columns are uniform over the block: the four
+// come in one batch of scalar loads (the index width is a template
+// parameter, so no load waits behind a dtype branch), the weights go out
+// meanwhile, and the four token loads are issued unconditionally (a tap
+// outside the tokens reads row 0 and is discarded).  Against a preamble of
+// dependent dtype-switched index loads this measured 41.0 -> 40.5 us.
 // The node's window over the block's channels is one contiguous run
 // (iw[n][c][0..2]): the threads' 48-byte pieces go through LDS so that each
 // store instruction writes 4 KiB of consecutive bytes (whole lines) instead
@@ -70,6 +74,7 @@ __global__ void __launch_bounds__(256) tree_conv_kernel(const dft_conv_args p) {
 // unstaged 48-byte window stores (non-temporal unstaged stores were slower
 // still: partial lines reach memory unmerged).  With the staged stores,
 // non-temporal y / window stores time the same as ordinary ones (within 1%).
+template <bool CIDX64>
 __global__ void __launch_bounds__(256) tree_conv4_bf16_kernel(const dft_conv_args p, int cblocks) {
   __shared__ u32x4 stage[256 * 3];
   const int id = blockIdx.x;
@@ -82,27 +87,42 @@ __global__ void __launch_bounds__(256) tree_conv4_bf16_kernel(const dft_conv_arg
   const bool active = (int)threadIdx.x < nact;
   const int c0 = (cb * 256 + threadIdx.x) * 8;
 
-  int64_t slot = b, dst = b;
-  if (p.cs_indices) slot = ld_i(p.cs_indices, b, p.cs_indices_dtype);
-  if (p.iw_indices) dst = ld_i(p.iw_indices, b, p.iw_indices_dtype);
+  // the node's four tap columns: independent loads, one wait
   const int64_t cbase = (int64_t)b * p.cidx_req_stride + (int64_t)n * p.cidx_node_stride;
   int64_t col[4];
+  if constexpr (CIDX64) {
+    const int64_t* ci = static_cast<const int64_t*>(p.cidx) + cbase;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) col[j] = ld_i(p.cidx, cbase + j, p.cidx_dtype);
+    for (int j = 0; j < 4; ++j) col[j] = ci[j];
+  } else {
+    const int32_t* ci = static_cast<const int32_t*>(p.cidx) + cbase;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) col[j] = ci[j];
+  }
+  // the weights (8 channels x 4 taps) do not depend on them
+  const int cw = active ? c0 : 0;
+  const u32x4* wp = reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(p.weight) + (int64_t)cw * 4);
+  uint16_t w[32];  // w[4 e + j]: channel c0 + e, tap j
+#pragma unroll
+  for (int q = 0; q < 4; ++q) *reinterpret_cast<u32x4*>(&w[8 * q]) = wp[q];
+  int64_t slot = b, dst = b;
 
   if (active) {
     const uint16_t* xb = static_cast<const uint16_t*>(p.x) + (int64_t)b * p.x_req_stride + c0;
+    // token rows: every load is issued (a tap outside the tokens reads row 0
+    // and is discarded), so none waits on a branch
     u32x4 raw[4];
+    bool tok[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      raw[j] = u32x4{0u, 0u, 0u, 0u};
-      if (col[j] >= 3 && col[j] < 3 + p.n_nodes)
-        raw[j] = *reinterpret_cast<const u32x4*>(xb + (col[j] - 3) * p.x_node_stride);
+      tok[j] = col[j] >= 3 && col[j] < 3 + p.n_nodes;
+      raw[j] = *reinterpret_cast<const u32x4*>(xb + (tok[j] ? col[j] - 3 : 0) * p.x_node_stride);
     }
-    const u32x4* wp = reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(p.weight) + (int64_t)c0 * 4);
-    uint16_t w[32];  // w[4 e + j]: channel c0 + e, tap j
 #pragma unroll
-    for (int q = 0; q < 4; ++q) *reinterpret_cast<u32x4*>(&w[8 * q]) = wp[q];
+    for (int j = 0; j < 4; ++j)
+      if (!tok[j]) raw[j] = u32x4{0u, 0u, 0u, 0u};
+    // the state slot (needed by conv-state taps only)
+    if (p.cs_indices) slot = ld_i(p.cs_indices, b, p.cs_indices_dtype);
 
     float acc[8];
 #pragma unroll
@@ -139,6 +159,7 @@ __global__ void __launch_bounds__(256) tree_conv4_bf16_kernel(const dft_conv_arg
     }
   }
   if (p.iw) {
+    if (p.iw_indices) dst = ld_i(p.iw_indices, b, p.iw_indices_dtype);
     __syncthreads();
     u32x4* iw = reinterpret_cast<u32x4*>(static_cast<uint16_t*>(p.iw) + dst * p.iw_slot_stride +
                                          (int64_t)n * p.iw_node_stride + (int64_t)cb * 2048 * 3);
@@ -170,8 +191,11 @@ int launch_tree_conv(const dft_conv_args* a, hipStream_t stream) {
   if (conv4_bf16_ok(a)) {
     const int cblocks = (a->channels + 2047) / 2048;
     const int64_t pairs8 = ((int64_t)a->batch * cblocks + 7) / 8;
-    hipLaunchKernelGGL(tree_conv4_bf16_kernel, dim3((unsigned)(pairs8 * 8 * a->n_nodes)), dim3(256), 0, stream, *a,
-                       cblocks);
+    const dim3 grid((unsigned)(pairs8 * 8 * a->n_nodes));
+    if (a->cidx_dtype == DFT_I64)
+      hipLaunchKernelGGL(tree_conv4_bf16_kernel<true>, grid, dim3(256), 0, stream, *a, cblocks);
+    else
+      hipLaunchKernelGGL(tree_conv4_bf16_kernel<false>, grid, dim3(256), 0, stream, *a, cblocks);
   } else {
     const dim3 grid((unsigned)((a->channels + 255) / 256), (unsigned)a->n_nodes, (unsigned)a->batch);
     hipLaunchKernelGGL(tree_conv_kernel, grid, dim3(256), 0, stream, *a);

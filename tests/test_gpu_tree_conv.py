@@ -134,11 +134,12 @@ def test_tree_conv_fused_dropin(cuda):
     assert max_abs(np32(y), O.bf16_round(ry)) <= MAX_ABS_BF16
 
 
-@pytest.mark.parametrize("case", ["f32_weight", "odd_channels", "fp32_state"])
+@pytest.mark.parametrize("case", ["f32_weight", "odd_channels", "fp32_state", "int64_cidx"])
 def test_conv_general_layouts(cuda, case):
     """Layouts outside the 16-byte bf16 fast path (fp32 weights, a channel
-    count that is not a multiple of 8) and an fp32 conv state on the fast
-    path: same results, window values rounded to the window's dtype."""
+    count that is not a multiple of 8), an fp32 conv state and 64-bit gather
+    indices on the fast path: same results, window values rounded to the
+    window's dtype."""
     from dforktree_amd import ops
     announce(f"conv general layout {case}")
     B, N = 2, 32
@@ -148,6 +149,8 @@ def test_conv_general_layouts(cuda, case):
         w = w.float()
     if case == "fp32_state":
         cs = torch.randn(B, C, 3) * 0.5
+    if case == "int64_cidx":
+        cidx = cidx.long()
     iw = torch.zeros(B, N, C, 3, dtype=torch.bfloat16, device=cuda)
     y = ops.tree_conv(x.to(cuda), cs.to(cuda), w.to(cuda), None, cidx.to(cuda), iw=iw)
     torch.cuda.synchronize()
