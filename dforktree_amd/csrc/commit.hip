@@ -54,11 +54,15 @@ __global__ void __launch_bounds__(256) tree_commit_kernel(const CommitParams P) 
     if (u_end < 0 || u_end >= n) return;  // nothing to commit for this end
   }
 
+  // A negative destination slot (in place: a negative source slot), e.g. a
+  // padded request, commits nothing; a negative source slot with a separate
+  // destination reads slot 0, as the verify reads its S0.
   int64_t slot = b;
-  if (p.src_slots) {
-    slot = ld_i(p.src_slots, b, p.src_slots_dtype);
-    if (slot < 0) slot = 0;
-  }
+  if (p.src_slots) slot = ld_i(p.src_slots, b, p.src_slots_dtype);
+  int64_t dslot = slot;
+  if (p.dst_slots) dslot = ld_i(p.dst_slots, b, p.dst_slots_dtype);
+  if (dslot < 0) return;
+  if (slot < 0) slot = 0;
 
   // ---- state tile: thread owns rows 16*rg .. 16*rg+15, cols 4*c4 .. 4*c4+3
   const int c4 = tid & 31, rg = tid >> 5;
@@ -150,11 +154,6 @@ __global__ void __launch_bounds__(256) tree_commit_kernel(const CommitParams P) 
     for (int m = 0; m < 16; ++m) st[m] += rvals[m] * cc;
   }
 
-  int64_t dslot = slot;
-  if (p.dst_slots) {
-    dslot = ld_i(p.dst_slots, b, p.dst_slots_dtype);
-    if (dslot < 0) dslot = 0;
-  }
   float* dstp = p.dst + (int64_t)l * p.dst_layer_stride + dslot * p.dst_slot_stride + (int64_t)u * p.dst_node_stride +
                 (int64_t)h * p.dst_h_stride;
   if (P.dst_vec) {

@@ -427,6 +427,7 @@ __device__ __forceinline__ void store_state(float* S, int64_t v_stride, int wave
 struct Item {
   int b, hk, rr, h;  // request, k-head, v-head within the k-head, v-head
   int n;             // nodes (0: nothing to verify)
+  bool no_slot = false;  // negative state index: S0 is read from slot 0, nothing is committed
   int64_t row0;      // row of node 0
   const float* S0;   // the head's state tile (k stride 1 on the vector paths)
 };
@@ -470,6 +471,7 @@ __device__ __forceinline__ bool item_rows(const dft_verify_args& p, Item& it, in
   int64_t slot = it.b;
   if (p.state_indices) {
     slot = ld_i(p.state_indices, it.b, p.state_indices_dtype);
+    it.no_slot = slot < 0;
     if (slot < 0) slot = 0;
   }
   it.S0 = p.state + slot * p.state_slot_stride + (int64_t)it.h * p.state_h_stride;
@@ -1017,6 +1019,7 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
   PendingHead ph{};
   if constexpr (COMMIT) {
     ph = pending_head(P.c, it.b);
+    if (it.no_slot) ph.len = 0;  // no slot of its own: nothing is committed
     if (it.n == 0) {  // nothing to verify this step: the commit alone
       const Pending pd = decode_pending(ph, lane, *path_word(P.c, it.b, lane));
       if (pd.last < 0) return;

@@ -102,7 +102,9 @@ typedef struct dft_verify_args {
   const uint64_t* anc_bits;
 
   /* initial state S0(k, v) = state[slot*slot_stride + h*h_stride + k*k_stride
-   * + v*v_stride], fp32.  slot = max(state_indices[b], 0), or b if NULL. */
+   * + v*v_stride], fp32.  slot = max(state_indices[b], 0), or b if NULL
+   * (tree_kernels.py:184).  dft_tree_commit_verify commits nothing for a
+   * request whose state index is negative. */
   const float* state;
   int64_t state_slot_stride, state_h_stride, state_k_stride, state_v_stride;
   const void* state_indices;
@@ -215,13 +217,13 @@ typedef struct dft_commit_args {
 
   const float* src; /* [l][slot][h][row][col] */
   int64_t src_layer_stride, src_slot_stride, src_h_stride, src_row_stride, src_col_stride;
-  const void* src_slots; /* slot per request (clamped >= 0), or NULL: b */
+  const void* src_slots; /* slot per request, or NULL: b.  Negative: read slot 0 (in place: nothing is written) */
   int32_t src_slots_dtype;
 
   float* dst; /* [l][slot][u][h][row][col] */
   int64_t dst_layer_stride, dst_slot_stride, dst_node_stride, dst_h_stride, dst_row_stride,
       dst_col_stride;
-  const void* dst_slots; /* dst slot per request, or NULL: same as src slot */
+  const void* dst_slots; /* dst slot per request, or NULL: same as src slot.  Negative: nothing is written */
   int32_t dst_slots_dtype;
 } dft_commit_args;
 

@@ -58,6 +58,35 @@ def test_commit_inplace_closed_form(cuda):
             assert rel_l2(got[l, b].transpose(0, 2, 1), want) <= 1e-5, (l, b)
 
 
+def test_commit_inplace_negative_slot_writes_nothing(cuda):
+    """A request whose slot index is negative (a padded request) commits
+    nothing: no slot changes for it, slot 0 included, while the other
+    requests commit into their own slots."""
+    from dforktree_amd import ops, synth
+    announce("commit in place, negative slot")
+    L, B, H, N = 2, 3, 4, 32
+    g = torch.Generator().manual_seed(5)
+    pars = [synth.tree_parents(N, "random", g) for _ in range(B)]
+    keys, vals, gains = _aux(6, L, H, B * N)
+    S = torch.randn(L, 4, H, 128, 128) * 0.02  # [L, slot, H, V, K]: slots 0 and 3 belong to nobody
+    slots = torch.tensor([2, -1, 1], dtype=torch.int32)
+    paths, idx, lens = _paths(pars, 16, 7)
+    Sg = S.to(cuda)
+    ops.tree_commit(Sg, keys.to(cuda), vals.to(cuda), gains.to(cuda), idx.to(cuda), n_nodes=N,
+                    path_len=lens.to(cuda), src_slots=slots.to(cuda))
+    torch.cuda.synchronize()
+    got = np32(Sg)
+    for s in (0, 3):
+        assert np.array_equal(got[:, s], np32(S[:, s])), f"slot {s} was written"
+    for l in range(L):
+        for b in (0, 2):
+            sl = slice(b * N, (b + 1) * N)
+            s = int(slots[b])
+            want = O.closed_commit(np32(S[l, s]).transpose(0, 2, 1), np32(keys[l, :, sl]), np32(vals[l, :, sl]),
+                                   np32(gains[l, :, sl]), paths[b].tolist())
+            assert rel_l2(got[l, s].transpose(0, 2, 1), want) <= 1e-5, (l, b)
+
+
 def test_verify_then_commit_matches_replay(cuda):
     """Config-4 shape in miniature: verify every layer on the GPU (saving k, vn,
     G), commit the accepted root-to-node walk in place, compare with an fp64

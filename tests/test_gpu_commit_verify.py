@@ -183,6 +183,49 @@ def test_commit_verify_equals_commit_then_verify(cuda):
         assert rel_l2(np32(x), np32(y)) <= 1e-6
 
 
+def test_commit_verify_negative_slot_commits_nothing(cuda):
+    """State indices [2, -1, 1] over a pool of 4 slots, every request with a
+    pending path: the request without a slot verifies on slot 0 (as the plain
+    verify does) and commits nothing, so slots 0 and 3 keep their bits; the
+    fused entry equals the separate commit (same slots) followed by the
+    plain verify."""
+    from dforktree_amd import ops, synth
+    announce("commit->verify, negative state index")
+    B, N, hk, hv = 3, 32, 2, 4
+    b1 = synth.make_batch(26, 0, [N] * B, hk=hk, hv=hv)
+    b2 = synth.make_batch(27, 0, [N] * B, hk=hk, hv=hv)
+    g1, g2 = b1.to(cuda), b2.to(cuda)
+    rows = B * N
+    slots = torch.tensor([2, -1, 1], dtype=torch.int32, device=cuda)
+    pool0 = (torch.randn(4, hv, 128, 128, generator=torch.Generator().manual_seed(28)) * 0.02).to(cuda)
+    k1 = torch.zeros(hv, rows, 128, device=cuda)
+    v1 = torch.zeros(hv, rows, 128, device=cuda)
+    G1 = torch.zeros(hv, rows, device=cuda)
+    ts1 = ops.tree_struct(g1.parent, 4, batch=B, n_nodes=N, want=("anc_bits",))["anc_bits"]
+    ts2 = ops.tree_struct(g2.parent, 4, batch=B, n_nodes=N, want=("anc_bits",))["anc_bits"]
+    ops.tree_verify(g1.y, g1.a, g1.b, g1.A_log, g1.dt_bias, pool0.transpose(-1, -2), hk=hk, hv=hv, anc_bits=ts1,
+                    batch=B, n_nodes=N, state_indices=slots, aux_k=k1, aux_v=v1, aux_g=G1)
+    idx, lens, _ = _paths(b1, 29)
+    idx_d, lens_d = idx.to(cuda), lens.to(cuda)
+    assert int(lens[1]) > 0, "the slotless request must have a pending path"
+    pool_a, pool_b = pool0.clone(), pool0.clone()
+    common = dict(hk=hk, hv=hv, anc_bits=ts2, batch=B, n_nodes=N, state_indices=slots)
+    oa = ops.tree_commit_verify(g2.y, g2.a, g2.b, g2.A_log, g2.dt_bias, pool_a.transpose(-1, -2),
+                                pending_path=idx_d, pending_keys=k1, pending_values=v1, pending_gains=G1,
+                                pending_path_len=lens_d, prev_n_nodes=N, **common)
+    ops.tree_commit(pool_b.unsqueeze(0), k1.unsqueeze(0), v1.unsqueeze(0), G1.unsqueeze(0), idx_d, n_nodes=N,
+                    path_len=lens_d, src_slots=slots)
+    ob = ops.tree_verify(g2.y, g2.a, g2.b, g2.A_log, g2.dt_bias, pool_b.transpose(-1, -2), **common)
+    torch.cuda.synchronize()
+    for s in (0, 3):
+        assert np.array_equal(np32(pool_a[s]), np32(pool0[s])), f"fused entry wrote slot {s}"
+        assert np.array_equal(np32(pool_b[s]), np32(pool0[s])), f"commit wrote slot {s}"
+    for s in (1, 2):
+        assert not np.array_equal(np32(pool_a[s]), np32(pool0[s])), f"slot {s} was not committed"
+    assert rel_l2(np32(pool_a), np32(pool_b)) <= 1e-6
+    assert rel_l2(np32(oa), np32(ob)) <= 1e-5
+
+
 def test_commit_verify_many_items_chain_of_three(cuda):
     """Full layer width at 24 requests (768 items: the persistent pipelined
     kernel), three steps: plain verify, then two fused commit -> verify steps
