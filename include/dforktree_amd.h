@@ -177,7 +177,8 @@ DFT_API int dft_tree_conv(const dft_conv_args* args, void* stream);
  * written in place (dst == src, dst_node_stride 0) or into a snapshot slot.
  * The state is addressed as rows x cols with rows = v and cols = k for the
  * V-major pool layout (src_row_stride = v stride); pass DFT_COMMIT_KV to
- * address rows = k, cols = v instead.
+ * address rows = k, cols = v instead.  The requests of one launch must write
+ * distinct destination tiles: two requests committing into one slot race.
  * ------------------------------------------------------------------------- */
 enum dft_commit_flags {
   DFT_COMMIT_KV = 1,        /* state rows are k, columns are v */
@@ -243,7 +244,8 @@ DFT_API int dft_tree_commit(const dft_commit_args* args, void* stream);
  * verify step into the next step's verify, so the state is read once per
  * layer and step instead of twice.  The previous step's keys / values / gains
  * must not alias this step's aux outputs (alternate two sets), and every
- * request's previous rows must exist in them.
+ * request's previous rows must exist in them.  Requests with a pending path
+ * must have distinct state slots (the tile is updated in place).
  * ------------------------------------------------------------------------- */
 typedef struct dft_pending_commit {
   int32_t path_cols;    /* entries per request in path, <= 16 */
