@@ -244,8 +244,9 @@ DFT_API int dft_tree_commit(const dft_commit_args* args, void* stream);
  * verify step into the next step's verify, so the state is read once per
  * layer and step instead of twice.  The previous step's keys / values / gains
  * must not alias this step's aux outputs (alternate two sets), and every
- * request's previous rows must exist in them.  Requests with a pending path
- * must have distinct state slots (the tile is updated in place).
+ * request's previous rows must exist in them.  A slot that a request commits
+ * into must not be another request's slot in the same launch (the tile is
+ * updated in place while the other request would read it).
  * ------------------------------------------------------------------------- */
 typedef struct dft_pending_commit {
   int32_t path_cols;    /* entries per request in path, <= 16 */
