@@ -138,6 +138,21 @@ def test_commit_verify_packed_ragged_per_khead(cuda, path_dtype):
     _check_chain(batch1, batch2, pool, o2, aux2, walks, empty, per_khead=True)
 
 
+def test_commit_verify_bench_shape(cuda):
+    """The measured shape: 64 requests of 32-node random trees at full width
+    (2048 items, two rounds of resident workgroups, so freed slots take
+    further items), keys saved per k-head; one request without a path and
+    one with a shortened path_len."""
+    from dforktree_amd import synth
+    announce("commit->verify bench shape 64 x 32")
+    batch1 = synth.make_batch(40, 0, [32] * 64, hk=16, hv=32, kinds="random")
+    batch2 = synth.make_batch(41, 0, [32] * 64, hk=16, hv=32, kinds="random")
+    empty, shorten = (5,), (60,)
+    pool, o2, aux2, walks = _run_chain(cuda, batch1, batch2, per_khead=True, packed=False, empty=empty,
+                                       shorten=shorten)
+    _check_chain(batch1, batch2, pool, o2, aux2, walks, empty, per_khead=True)
+
+
 def test_commit_verify_equals_commit_then_verify(cuda):
     """Full layer width (16 q/k heads, 32 v heads) at 32 nodes: the fused entry
     against dft_tree_commit (in place) followed by dft_tree_verify."""
@@ -227,9 +242,9 @@ def test_commit_verify_negative_slot_commits_nothing(cuda):
 
 
 def test_commit_verify_many_items_chain_of_three(cuda):
-    """Full layer width at 24 requests (768 items: the persistent pipelined
-    kernel), three steps: plain verify, then two fused commit -> verify steps
-    that alternate the save buffers; checked against the oracle chain."""
+    """Full layer width at 24 requests (768 items, one round of resident
+    workgroups), three steps: plain verify, then two fused commit -> verify
+    steps that alternate the save buffers; checked against the oracle chain."""
     from dforktree_amd import ops, synth
     announce("commit->verify many items, 3 steps")
     B, N, hk, hv = 24, 32, 16, 32

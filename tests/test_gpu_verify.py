@@ -182,11 +182,11 @@ def test_block_inverse_dropin(cuda):
 
 
 @pytest.mark.parametrize("sizes_kind", ["uniform32", "ragged64"])
-def test_verify_persistent_loop_many_heads(cuda, sizes_kind):
-    """More (request, head) items than resident workgroups, so every
-    workgroup runs the multi-head pipeline (prefetch of the next head)."""
+def test_verify_more_items_than_resident_workgroups(cuda, sizes_kind):
+    """More (request, head) items than resident workgroups, so freed slots
+    take further items (and a packed batch runs both size classes)."""
     from dforktree_amd import synth
-    announce(f"verify persistent loop {sizes_kind}")
+    announce(f"verify more items than slots {sizes_kind}")
     if sizes_kind == "uniform32":
         sizes = [32] * 40          # 40 x 32 heads = 1280 items (> 4 per CU x 256 CUs)
         kinds = ["random", "chain", "bushy", "random"] * 10
@@ -198,8 +198,7 @@ def test_verify_persistent_loop_many_heads(cuda, sizes_kind):
 
 def test_verify_ragged_32_many_items(cuda):
     """Packed trees of 1-32 nodes with ancestry bits and more items than
-    resident workgroups: the persistent pipelined kernel (several items per
-    workgroup, alternating row buffers)."""
+    resident workgroups of the 32-wide kernel."""
     from dforktree_amd import synth
     announce("verify ragged <=32 many items")
     sizes, kinds = synth.ragged_sizes(40, 1, 32, seed=11)
@@ -213,6 +212,15 @@ def test_verify_uniform_many_items_dense_ancestry(cuda):
     announce("verify uniform 32 many items dense")
     batch = synth.make_batch(13, 0, [32] * 40, hk=16, hv=32, kinds=["random", "chain", "bushy", "random"] * 10)
     check_against_oracle(batch, *run_gpu(batch, cuda, packed=False, use_bits=False))
+
+
+def test_verify_bench_shape(cuda):
+    """The measured shape: 64 requests of 32-node random trees at full width
+    (2048 items, two rounds of resident workgroups), against the oracle."""
+    from dforktree_amd import synth
+    announce("verify bench shape 64 x 32")
+    batch = synth.make_batch(14, 0, [32] * 64, hk=16, hv=32, kinds="random")
+    check_against_oracle(batch, *run_gpu(batch, cuda, packed=False, use_bits=True))
 
 
 def test_verify_kmajor_state_element_loads(cuda):
