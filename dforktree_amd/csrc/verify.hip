@@ -18,6 +18,8 @@
 //     v_mfma_f32_16x16x32_bf16 (lane (n = l%16, g = l/16) loads 16 bytes at
 //     k = 16j + 4g of state row n: the 4 lanes of a row cover a 64-byte
 //     sector per instruction); q/k/v rows, gates and ancestry go to LDS.
+//     The verify issues the tile in four k-step groups spread over phase 1;
+//     the 64-wide form copies its v rows only after Cq (LDS budget).
 //  1. while the state is in flight: norms, G, the Gram tiles of A, the
 //     blocked inverse X (16x16 diagonal blocks by forward substitution,
 //     off-diagonal blocks X_ij = -D_i sum_m A_im X_mj by fp32 MFMA) and
