@@ -93,6 +93,63 @@ struct VerifyParams {
                    // requests with n_lo <= nodes <= n_hi (the others exit at once)
 };
 
+// The output fields a workgroup needs only at the end of its life (the key
+// and gain saves, the staged vn and o stores).  The compiler loads kernel
+// arguments at entry; in the fused commit -> verify kernels, whose
+// registers are full, these would stay live through the whole workgroup and
+// be spilled (36 scalar registers, 284 lane reads).  There they are re-read
+// from the kernel-argument segment where they are used instead, through a
+// pointer the compiler cannot equate with the entry loads: fused kernel
+// 83.0 -> 82.0 us at batch 64.  (The verify kernels do not spill; reading
+// late there only adds latency.)
+struct OutArgs {
+  float* aux_k;
+  int64_t aux_k_h_stride, aux_k_row_stride;
+  float* aux_v;
+  int64_t aux_v_h_stride, aux_v_row_stride;
+  float* aux_g;
+  int64_t aux_g_h_stride, aux_g_row_stride;
+  void* o;
+  int64_t o_row_stride, o_h_stride;
+  int32_t flags;
+  int auxk_vec, vn_stage, o_stage;
+};
+
+template <class PP>
+__device__ __forceinline__ OutArgs out_args_of(PP P) {
+  OutArgs r;
+  r.aux_k = P->a.aux_k;
+  r.aux_k_h_stride = P->a.aux_k_h_stride;
+  r.aux_k_row_stride = P->a.aux_k_row_stride;
+  r.aux_v = P->a.aux_v;
+  r.aux_v_h_stride = P->a.aux_v_h_stride;
+  r.aux_v_row_stride = P->a.aux_v_row_stride;
+  r.aux_g = P->a.aux_g;
+  r.aux_g_h_stride = P->a.aux_g_h_stride;
+  r.aux_g_row_stride = P->a.aux_g_row_stride;
+  r.o = P->a.o;
+  r.o_row_stride = P->a.o_row_stride;
+  r.o_h_stride = P->a.o_h_stride;
+  r.flags = P->a.flags;
+  r.auxk_vec = P->auxk_vec;
+  r.vn_stage = P->vn_stage;
+  r.o_stage = P->o_stage;
+  return r;
+}
+
+template <bool LATE>
+__device__ __forceinline__ OutArgs out_args(const VerifyParams& P) {
+  if constexpr (LATE) {
+    // the kernel's only argument is the VerifyParams, at offset 0
+    typedef const __attribute__((address_space(4))) VerifyParams* KParams;
+    KParams kp = (KParams)__builtin_amdgcn_kernarg_segment_ptr();
+    asm volatile("" : "+s"(kp));
+    return out_args_of(kp);
+  } else {
+    return out_args_of(&P);
+  }
+}
+
 // Output staging in the (then free) q/k/v region: vn as NP x 128 fp32 with
 // 16-byte chunk q of row i at q ^ (i & 31), o as NP x 128 bf16 with the
 // q/k/v swizzle; both keep the accumulator-layout writes conflict-free.
@@ -641,10 +698,10 @@ __device__ __forceinline__ void phase_norms(const dft_verify_args& p, int tid, c
 
 // The saves for the commit: normalised keys (once per k-head when saved per
 // k-head) and G.  Needs the norms and G; reads the k rows.
-template <int NP, class RW, class WK>
+template <int NP, bool LATE, class RW, class WK>
 __device__ __forceinline__ void phase_saves(const VerifyParams& P, const Item& it, int tid, const RW& rw,
                                             const WK& wk) {
-  const dft_verify_args& p = P.a;
+  const OutArgs p = out_args<LATE>(P);
   const bool per_khead = (p.flags & DFT_VERIFY_AUX_K_PER_KHEAD) != 0;
   if (p.aux_k && (!per_khead || it.rr == 0)) {
     float* dk = p.aux_k + (int64_t)(per_khead ? it.hk : it.h) * p.aux_k_h_stride + it.row0 * p.aux_k_row_stride;
@@ -655,7 +712,7 @@ __device__ __forceinline__ void phase_saves(const VerifyParams& P, const Item& i
       const f32x4 val = {__uint_as_float(u.x << 16) * r, __uint_as_float(u.x & 0xffff0000u) * r,
                          __uint_as_float(u.y << 16) * r, __uint_as_float(u.y & 0xffff0000u) * r};
       float* dst = dk + i * p.aux_k_row_stride + d;
-      if (P.auxk_vec) {
+      if (p.auxk_vec) {
         __builtin_nontemporal_store(val, reinterpret_cast<f32x4*>(dst));
       } else {
 #pragma unroll
@@ -974,12 +1031,12 @@ __device__ __forceinline__ void phase_out(const VerifyParams& P, const Item& it,
 // the key saves) are written once and not read back by this launch: they go
 // out as non-temporal stores, which at batch 64 made the verify 6.6% and the
 // fused commit -> verify 3.1% faster than ordinary stores.
-template <int NP, class RW>
+template <int NP, bool LATE, class RW>
 __device__ __forceinline__ void phase_stores(const VerifyParams& P, const Item& it, int tid, const RW& rw) {
-  const dft_verify_args& p = P.a;
+  const OutArgs p = out_args<LATE>(P);
   const float* vn_s = reinterpret_cast<const float*>(rw.q);
   const uint16_t* o_s = rw.ostage();
-  if (P.vn_stage) {  // rows of 32 x 16 bytes
+  if (p.vn_stage) {  // rows of 32 x 16 bytes
     float* dst = p.aux_v + (int64_t)it.h * p.aux_v_h_stride + it.row0 * p.aux_v_row_stride;
 #pragma unroll
     for (int u = 0; u < NP / 8; ++u) {
@@ -989,7 +1046,7 @@ __device__ __forceinline__ void phase_stores(const VerifyParams& P, const Item& 
                                     reinterpret_cast<f32x4*>(dst + i * p.aux_v_row_stride + 4 * q));
     }
   }
-  if (P.o_stage) {  // rows of 16 x 16 bytes
+  if (p.o_stage) {  // rows of 16 x 16 bytes
     uint16_t* dst = static_cast<uint16_t*>(p.o) + it.row0 * p.o_row_stride + (int64_t)it.h * p.o_h_stride;
 #pragma unroll
     for (int u = 0; u < NP / 16; ++u) {
@@ -1107,7 +1164,7 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
     __syncthreads();  // every wave has read its keys: am and x take the Gram tiles and X
   }
   if constexpr (kSplit) issue_state_group<false>(S0, p.state_v_stride, wave, lane, 1, s0r);
-  phase_saves<NP>(P, it, tid, sm, sm);
+  phase_saves<NP, COMMIT>(P, it, tid, sm, sm);
   phase_gram_diag<NP, COMMIT && NP == 32>(tid, sm, sm);
   if constexpr (kSplit) issue_state_group<false>(S0, p.state_v_stride, wave, lane, 2, s0r);
   __syncthreads();
@@ -1139,7 +1196,7 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
   phase_out<NP>(P, it, lane, wave, sm, sm, cq, wh, wl);
   if (P.vn_stage || P.o_stage) {
     __syncthreads();
-    phase_stores<NP>(P, it, tid, sm);
+    phase_stores<NP, COMMIT>(P, it, tid, sm);
   }
 }
 
