@@ -735,8 +735,6 @@ __device__ __forceinline__ void phase_saves(const VerifyParams& P, const Item& i
 // Of X above its diagonal blocks only blocks (b, b + 1), b even, are ever
 // read: phase_out's 32-wide k-steps pair block columns 2s and 2s + 1 and skip
 // the steps wholly above the diagonal.  Each thread zeroes one element of each.
-// ZERO_ALL zeroes everything above the diagonal blocks instead: with the
-// shorter form the fused 32-wide kernel (at its 128-register budget) spills.
 template <int NP, class RW, class WK>
 __device__ __forceinline__ void a_tile(const RW& rw, WK& wk, int ti, int tj, int n16, int g4) {
   constexpr int LDA = WK::LDA;
@@ -757,7 +755,7 @@ __device__ __forceinline__ void a_tile(const RW& rw, WK& wk, int ti, int tj, int
   }
 }
 
-template <int NP, bool ZERO_ALL, class RW, class WK>
+template <int NP, class RW, class WK>
 __device__ __forceinline__ void phase_gram_diag(int tid, const RW& rw, WK& wk) {
   constexpr int MT = NP / 16;
   constexpr int LDA = WK::LDA;
@@ -786,15 +784,8 @@ __device__ __forceinline__ void phase_gram_diag(int tid, const RW& rw, WK& wk) {
 #pragma unroll
     for (int tj = 0; tj < ti; ++tj, ++item)
       if (((MT + item) & 3) == wave) a_tile<NP>(rw, wk, ti, tj, n16, g4);
-  if constexpr (ZERO_ALL) {
-    for (int e = tid; e < NP * NP; e += 256) {
-      const int i = e / NP, jj = e % NP;
-      if ((i >> 4) < (jj >> 4)) wk.x()[i * LDA + jj] = 0.f;
-    }
-  } else {
 #pragma unroll
-    for (int b = 0; b + 1 < MT; b += 2) wk.x()[(16 * b + (tid >> 4)) * LDA + 16 * (b + 1) + (tid & 15)] = 0.f;
-  }
+  for (int b = 0; b + 1 < MT; b += 2) wk.x()[(16 * b + (tid >> 4)) * LDA + 16 * (b + 1) + (tid & 15)] = 0.f;
 }
 
 
@@ -1165,7 +1156,7 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
   }
   if constexpr (kSplit) issue_state_group<false>(S0, p.state_v_stride, wave, lane, 1, s0r);
   phase_saves<NP, COMMIT>(P, it, tid, sm, sm);
-  phase_gram_diag<NP, COMMIT && NP == 32>(tid, sm, sm);
+  phase_gram_diag<NP>(tid, sm, sm);
   if constexpr (kSplit) issue_state_group<false>(S0, p.state_v_stride, wave, lane, 2, s0r);
   __syncthreads();
 #pragma unroll
