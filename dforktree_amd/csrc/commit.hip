@@ -22,7 +22,17 @@ struct CommitParams {
   int src_vec, dst_vec;  // 16-byte vector path usable
 };
 
-__global__ void __launch_bounds__(256) tree_commit_kernel(const CommitParams P) {
+// Five waves per SIMD (five workgroups per CU instead of four, 64 KiB more
+// state in flight per CU): 48.3 -> 46.4 us per layer at batch 64 in
+// interleaved runs.  At the 96-register budget this takes, 14 registers are
+// spilled (values of the element-wise path for layouts without 16-byte rows
+// among them); their stores add about 11% to the launch's HBM writes, and
+// the kernel is still faster.  Forms without the spills measured slower:
+// a separate 16-byte-only instantiation (47.3 us), 128-float rows addressed
+// by immediate offsets (48.9 us), the path entries read before the tile
+// (47.0 us).
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(5)))
+tree_commit_kernel(const CommitParams P) {
   const dft_commit_args& p = P.a;
   extern __shared__ float cshm[];  // rv[T][128] then cv[T][128]
   __shared__ int s_nodes[64];
