@@ -34,6 +34,7 @@
 // the previous step's accepted path into the tile as soon as it has landed
 // and writes it back before the Gram phase.
 #include <climits>
+#include <type_traits>
 
 #include "dft_device.h"
 
@@ -1197,6 +1198,9 @@ tree_verify_kernel(const VerifyParams P) {
   verify_body<NP, S0VEC, false>(P);
 }
 
+// P must stay this kernel's first (only) argument: out_args<true> reads it
+// back from offset 0 of the kernel-argument segment.
+static_assert(std::is_trivially_copyable<VerifyParams>::value, "VerifyParams is passed by value to the kernels");
 template <int NP>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NP == 32 ? 4 : 1)))
 tree_commit_verify_kernel(const VerifyParams P) {
