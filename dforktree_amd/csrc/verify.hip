@@ -79,6 +79,31 @@ __device__ __forceinline__ void lds_dma16(const void* g, void* lds) {
 __device__ __forceinline__ void lds_dma16_nt(const void* g, void* lds) {
   __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)lds, 16, 0, 2);
 }
+// lds_dma16_nt issued from inline assembly, which the backend's wait
+// analysis does not see.  For the late v rows it cannot tell the copy's LDS
+// destination (the q rows' region) from the k rows read next and would wait
+// for the copy at once; the caller waits (vmcnt) before the destination is
+// read.  An untracked load issued before a tracked one leaves the backend's
+// own counted waits exact (vector memory returns in issue order); issued
+// after, it only makes them wait longer.  Measured at 64 nodes: 2.1% faster.
+__device__ __forceinline__ void lds_dma16_nt_untracked(const void* g, void* lds) {
+  const uint32_t base =
+      __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)lds);
+  // m0 is reserved to the backend: its value is kept across the statement.
+  // A DMA needs one wait state after m0 is written (s_nop 0), and so does a
+  // DMA of the backend's own right after the restore.
+  uint32_t keep;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %2\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %1, off nt\n\t"
+      "s_mov_b32 m0, %0\n\t"
+      "s_nop 0"
+      : "=&s"(keep)
+      : "v"(g), "s"(base)
+      : "memory");
+}
 __device__ __forceinline__ void lds_dma4(const void* g, void* lds) {
   __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)lds, 4, 0, 0);
 }
@@ -629,7 +654,9 @@ __device__ __forceinline__ void issue_rows(const dft_verify_args& p, const Item&
       // same L2); each v row is read once.  Non-temporal v copies measured
       // 1.2% faster at batch 64; non-temporal q/k copies gained nothing.
       const void* src = it.n > 0 ? static_cast<const void*>(srcs[m] + goff) : alt;
-      if (m == 2)
+      if (m == 2 && M0 == 2)  // the late v rows, copied alone while Ck computes
+        lds_dma16_nt_untracked(src, dsts[m] + 4 * blk * kD);
+      else if (m == 2)
         lds_dma16_nt(src, dsts[m] + 4 * blk * kD);
       else
         lds_dma16(src, dsts[m] + 4 * blk * kD);
@@ -1176,7 +1203,7 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
     __syncthreads();  // X and M complete, the q rows consumed
     issue_rows<NP, 2, 3>(p, it, wave, lane, S0, sm);
     phase_cq_ck<NP, 2>(lane, sm, s0r, cq, ck);
-    __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 15));
+    __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 15));  // the v row copies (untracked by the backend)
     __syncthreads();
   } else {
     phase_cq_ck<NP>(lane, sm, s0r, cq, ck);
