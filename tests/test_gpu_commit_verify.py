@@ -140,7 +140,7 @@ def test_commit_verify_packed_ragged_per_khead(cuda, path_dtype):
 
 def test_commit_verify_bench_shape(cuda):
     """The measured shape: 64 requests of 32-node random trees at full width
-    (2048 items, two rounds of resident workgroups, so freed slots take
+    (2048 items, two generations of resident workgroups, so freed slots take
     further items), keys saved per k-head; one request without a path and
     one with a shortened path_len."""
     from dforktree_amd import synth

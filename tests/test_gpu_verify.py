@@ -216,7 +216,7 @@ def test_verify_uniform_many_items_dense_ancestry(cuda):
 
 def test_verify_bench_shape(cuda):
     """The measured shape: 64 requests of 32-node random trees at full width
-    (2048 items, two rounds of resident workgroups), against the oracle."""
+    (2048 items, two generations of resident workgroups), against the oracle."""
     from dforktree_amd import synth
     announce("verify bench shape 64 x 32")
     batch = synth.make_batch(14, 0, [32] * 64, hk=16, hv=32, kinds="random")
