@@ -87,6 +87,40 @@ def test_commit_inplace_negative_slot_writes_nothing(cuda):
             assert rel_l2(got[l, s].transpose(0, 2, 1), want) <= 1e-5, (l, b)
 
 
+def test_commit_full_size_pool(cuda):
+    """Accept-and-commit at full size: 24 layers x 128 requests x 32 v-heads
+    of 2 MiB fp32 state per request-layer (a 6 GiB pool, so byte offsets pass
+    4 GiB), 32-node random trees, random accepted walks of length 1-16, keys
+    per k-head (16 k-heads).  One launch commits everything in place; a spread
+    of (layer, request) tiles, the first and last ones included, is checked
+    against the fp32 closed form, and every committed value must be finite."""
+    from dforktree_amd import ops, synth
+    announce("commit in place, full-size pool (24 x 128 x 32 heads)")
+    L, B, HK, HV, N, D = 24, 128, 16, 32, 32, 128
+    rows = B * N
+    S = synth.device_randn_(torch.empty(L, B, HV, D, D, device=cuda), 21, std=0.02)  # [L, slot, H, V, K]
+    keys = synth.device_randn_(torch.empty(L, HK, rows, D, device=cuda), 22, std=D ** -0.5)
+    vals = synth.device_randn_(torch.empty(L, HV, rows, D, device=cuda), 23, std=0.3)
+    gains = synth.device_randn_(torch.empty(L, HV, rows, device=cuda), 24).abs_().neg_()
+    g = torch.Generator().manual_seed(25)
+    pars = [synth.tree_parents(N, "random", g) for _ in range(B)]
+    paths, idx, lens = _paths(pars, 16, 26)
+    picks = [(0, 0), (0, B - 1), (L - 1, 0), (L - 1, B - 1), (11, 64), (17, 63)]
+    pg = torch.Generator().manual_seed(27)
+    picks += [(int(torch.randint(0, L, (1,), generator=pg)), int(torch.randint(0, B, (1,), generator=pg)))
+              for _ in range(10)]
+    before = {lb: np32(S[lb[0], lb[1]]) for lb in picks}
+    ops.tree_commit(S, keys, vals, gains, idx.to(cuda), n_nodes=N, path_len=lens.to(cuda), k_head_div=HV // HK)
+    torch.cuda.synchronize()
+    assert bool(torch.isfinite(S).all())
+    for l, b in picks:
+        sl = slice(b * N, (b + 1) * N)
+        kh = np32(keys[l, :, sl])[np.arange(HV) // (HV // HK)]  # v-head h uses k-head h // 2
+        want = O.closed_commit(before[(l, b)].transpose(0, 2, 1), kh, np32(vals[l, :, sl]), np32(gains[l, :, sl]),
+                               paths[b].tolist())
+        assert rel_l2(np32(S[l, b]).transpose(0, 2, 1), want) <= 1e-5, (l, b, len(paths[b]))
+
+
 def test_verify_then_commit_matches_replay(cuda):
     """Config-4 shape in miniature: verify every layer on the GPU (saving k, vn,
     G), commit the accepted root-to-node walk in place, compare with an fp64
