@@ -153,6 +153,23 @@ def test_commit_verify_bench_shape(cuda):
     _check_chain(batch1, batch2, pool, o2, aux2, walks, empty, per_khead=True)
 
 
+def test_commit_verify_ragged_bench_shape(cuda):
+    """The ragged batch at full size in both steps: 128 packed requests with
+    trees of 8-64 nodes at full width (both kernel sizes), a different tree
+    size per request in the second step, keys saved per k-head; one request
+    without a path and one with a shortened path_len."""
+    from dforktree_amd import synth
+    announce("commit->verify ragged bench shape 128 x 8-64")
+    sizes1, kinds1 = synth.ragged_sizes(128, 8, 64, seed=3)
+    sizes2, kinds2 = synth.ragged_sizes(128, 8, 64, seed=4)
+    batch1 = synth.make_batch(42, 0, sizes1, hk=16, hv=32, kinds=kinds1)
+    batch2 = synth.make_batch(43, 0, sizes2, hk=16, hv=32, kinds=kinds2)
+    empty, shorten = (7,), (100,)
+    pool, o2, aux2, walks = _run_chain(cuda, batch1, batch2, per_khead=True, packed=True, empty=empty,
+                                       shorten=shorten)
+    _check_chain(batch1, batch2, pool, o2, aux2, walks, empty, per_khead=True)
+
+
 def test_commit_verify_equals_commit_then_verify(cuda):
     """Full layer width (16 q/k heads, 32 v heads) at 32 nodes: the fused entry
     against dft_tree_commit (in place) followed by dft_tree_verify."""

@@ -223,6 +223,17 @@ def test_verify_bench_shape(cuda):
     check_against_oracle(batch, *run_gpu(batch, cuda, packed=False, use_bits=True))
 
 
+def test_verify_ragged_bench_shape(cuda):
+    """The measured ragged batch at full size: 128 packed requests with trees
+    of 8-64 nodes (chains, bushy and random thirds), 4507 nodes at full
+    width, both kernel sizes in one launch, against the oracle."""
+    from dforktree_amd import synth
+    announce("verify ragged bench shape 128 x 8-64")
+    sizes, kinds = synth.ragged_sizes(128, 8, 64, seed=3)
+    batch = synth.make_batch(15, 0, sizes, hk=16, hv=32, kinds=kinds)
+    check_against_oracle(batch, *run_gpu(batch, cuda, packed=True, use_bits=True))
+
+
 def test_verify_kmajor_state_element_loads(cuda):
     """A k-major state ([hv, dk, dv] contiguous, v stride 1) takes the
     element-load path of the kernel; same results."""
