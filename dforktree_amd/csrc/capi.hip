@@ -100,9 +100,9 @@ int dft_tree_conv(const dft_conv_args* a, void* stream) {
   if (a->width < 1 || a->width > 8) return DFT_ERR_UNSUPPORTED;
   if (a->batch == 0 || a->n_nodes == 0 || a->channels == 0) return DFT_OK;
   if (a->n_nodes > 65535 || a->batch > 65535) return DFT_ERR_UNSUPPORTED;
-  // the width-4 bf16 path launches one workgroup per (request, node, 2048 channels), rounded to 8 requests
-  const int64_t pairs8 = ((int64_t)a->batch * ((a->channels + 2047) / 2048) + 7) / 8;
-  if (pairs8 * 8 * a->n_nodes > max_blocks(256)) return DFT_ERR_UNSUPPORTED;
+  // the width-4 bf16 path launches one 64-thread workgroup per (request, node, 512 channels), rounded to 8
+  const int64_t pairs8 = ((int64_t)a->batch * ((a->channels + 511) / 512) + 7) / 8;
+  if (pairs8 * 8 * a->n_nodes > max_blocks(64)) return DFT_ERR_UNSUPPORTED;
   if (!a->x || !a->conv_state || !a->weight || !a->cidx || !a->y) return DFT_ERR_INVALID;
   if (!float_tag(a->x_dtype) || !float_tag(a->cs_dtype) || !float_tag(a->w_dtype) || !float_tag(a->y_dtype))
     return DFT_ERR_INVALID;

@@ -52,8 +52,8 @@ __global__ void __launch_bounds__(256) tree_conv_kernel(const dft_conv_args p) {
 }
 
 // Fast path for the plugin's layout: width 4, bf16 tokens / weights / output
-// / window, channel-contiguous rows.  A block of 256 threads covers 2048
-// channels of one node; a thread owns 8 consecutive channels, so every
+// / window, channel-contiguous rows.  A block of one wave (64 threads)
+// covers 512 channels of one node; a thread owns 8 consecutive channels, so every
 // gathered token row, the weights (8 channels x 4 taps) and the output are
 // 16-byte accesses.  The gather columns are uniform over the block: the four
 // come in one batch of scalar loads (the index width is a template
@@ -63,7 +63,7 @@ __global__ void __launch_bounds__(256) tree_conv_kernel(const dft_conv_args p) {
 // dependent dtype-switched index loads this measured 41.0 -> 40.5 us.
 // The node's window over the block's channels is one contiguous run
 // (iw[n][c][0..2]): the threads' 48-byte pieces go through LDS so that each
-// store instruction writes 4 KiB of consecutive bytes (whole lines) instead
+// store instruction writes 1 KiB of consecutive bytes (whole lines) instead
 // of 16 bytes every 48.
 // The grid is 1-D and XCD-aware: workgroups are dealt to the 8 XCDs round
 // robin, so ids that agree mod 8 (one XCD, one L2) cover every node of one
@@ -74,18 +74,21 @@ __global__ void __launch_bounds__(256) tree_conv_kernel(const dft_conv_args p) {
 // unstaged 48-byte window stores (non-temporal unstaged stores were slower
 // still: partial lines reach memory unmerged).  With the staged stores,
 // non-temporal y / window stores time the same as ordinary ones (within 1%).
+// Block size, in interleaved runs: one wave over 512 channels 40.0 us,
+// 128 threads over 1024 channels 40.8 us, 256 threads over 2048 channels
+// 41.3 us; 16 channels per thread (256 threads over 4096) 44.2 us.
 template <bool CIDX64>
-__global__ void __launch_bounds__(256) tree_conv4_bf16_kernel(const dft_conv_args p, int cblocks) {
-  __shared__ u32x4 stage[256 * 3];
+__global__ void __launch_bounds__(64) tree_conv4_bf16_kernel(const dft_conv_args p, int cblocks) {
+  __shared__ u32x4 stage[64 * 3];
   const int id = blockIdx.x;
   const int k = id >> 3;
   const int n = k % p.n_nodes;
   const int pair = (k / p.n_nodes) * 8 + (id & 7);
   if (pair >= p.batch * cblocks) return;  // uniform over the block
   const int cb = pair % cblocks, b = pair / cblocks;
-  const int nact = min(256, (p.channels - cb * 2048) / 8);  // threads with channels
+  const int nact = min(64, (p.channels - cb * 512) / 8);  // threads with channels
   const bool active = (int)threadIdx.x < nact;
-  const int c0 = (cb * 256 + threadIdx.x) * 8;
+  const int c0 = (cb * 64 + threadIdx.x) * 8;
 
   // the node's four tap columns: independent loads, one wait
   const int64_t cbase = (int64_t)b * p.cidx_req_stride + (int64_t)n * p.cidx_node_stride;
@@ -162,10 +165,10 @@ __global__ void __launch_bounds__(256) tree_conv4_bf16_kernel(const dft_conv_arg
     if (p.iw_indices) dst = ld_i(p.iw_indices, b, p.iw_indices_dtype);
     __syncthreads();
     u32x4* iw = reinterpret_cast<u32x4*>(static_cast<uint16_t*>(p.iw) + dst * p.iw_slot_stride +
-                                         (int64_t)n * p.iw_node_stride + (int64_t)cb * 2048 * 3);
+                                         (int64_t)n * p.iw_node_stride + (int64_t)cb * 512 * 3);
 #pragma unroll
     for (int q = 0; q < 3; ++q) {
-      const int i = threadIdx.x + 256 * q;
+      const int i = threadIdx.x + 64 * q;
       if (i < nact * 3) iw[i] = stage[i];
     }
   }
@@ -189,13 +192,13 @@ static bool conv4_bf16_ok(const dft_conv_args* a) {
 
 int launch_tree_conv(const dft_conv_args* a, hipStream_t stream) {
   if (conv4_bf16_ok(a)) {
-    const int cblocks = (a->channels + 2047) / 2048;
+    const int cblocks = (a->channels + 511) / 512;
     const int64_t pairs8 = ((int64_t)a->batch * cblocks + 7) / 8;
     const dim3 grid((unsigned)(pairs8 * 8 * a->n_nodes));
     if (a->cidx_dtype == DFT_I64)
-      hipLaunchKernelGGL(tree_conv4_bf16_kernel<true>, grid, dim3(256), 0, stream, *a, cblocks);
+      hipLaunchKernelGGL(tree_conv4_bf16_kernel<true>, grid, dim3(64), 0, stream, *a, cblocks);
     else
-      hipLaunchKernelGGL(tree_conv4_bf16_kernel<false>, grid, dim3(256), 0, stream, *a, cblocks);
+      hipLaunchKernelGGL(tree_conv4_bf16_kernel<false>, grid, dim3(64), 0, stream, *a, cblocks);
   } else {
     const dim3 grid((unsigned)((a->channels + 255) / 256), (unsigned)a->n_nodes, (unsigned)a->batch);
     hipLaunchKernelGGL(tree_conv_kernel, grid, dim3(256), 0, stream, *a);

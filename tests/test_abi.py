@@ -153,7 +153,7 @@ def test_validation_refuses_grids_past_the_launch_limit():
     c.batch = limit // (24 * 32) + 1  # layers * batch * heads workgroups
     assert lib.dft_tree_commit(ctypes.byref(c), None) == _lib.DFT_ERR_UNSUPPORTED
     k = _lib.ConvArgs()
-    k.batch, k.n_nodes, k.channels, k.width = 65535, 65535, 8192, 4  # 4 workgroups per (request, node)
+    k.batch, k.n_nodes, k.channels, k.width = 65535, 65535, 8192, 4  # 16 workgroups per (request, node)
     k.x = k.conv_state = k.weight = k.cidx = k.y = 16
     k.cidx_dtype = _lib.DFT_I32
     assert lib.dft_tree_conv(ctypes.byref(k), None) == _lib.DFT_ERR_UNSUPPORTED
