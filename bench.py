@@ -320,8 +320,9 @@ def cpu_baseline(seconds):
 def main():
     args = parse()
     if args.gpus != 1:
-        print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported (every rank would run an "
-              f"independent copy of this single-GPU path; see the sharding notes in DESIGN.md)", file=sys.stderr)
+        print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported (the path shards by request and "
+              f"head group with no exchange step, so every rank would run an independent copy of this "
+              f"single-GPU workload)", file=sys.stderr)
         sys.exit(2)
     import torch
     dev = torch.device("cuda:0")
