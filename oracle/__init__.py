@@ -1,6 +1,7 @@
 """CPU oracle for the GDN tree-verify path.
 
-TEST INFRASTRUCTURE ONLY. This package is the checker, never the product:
+TEST INFRASTRUCTURE ONLY. This package is what the tests compare against,
+never the product:
 only ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of
 ``bench.py`` may import it.  The product path (``dforktree_amd``) runs the HIP
 kernels and raises when the HIP library is missing; it never calls in here.

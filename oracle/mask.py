@@ -1,7 +1,8 @@
 """CPU oracle for the bit-packed attention masks.
 
-TEST INFRASTRUCTURE ONLY (see the package docstring): the checker for
-``dft_packbits`` and ``dft_tree_mask_pack``, never called by the product.
+TEST INFRASTRUCTURE ONLY (see the package docstring): the reference that
+the tests hold ``dft_packbits`` and ``dft_tree_mask_pack`` against, never
+called by the product.
 
 * ``packbits`` / ``segment_packbits``   flashinfer.packbits / segment_packbits
   as fc1_plan.py:26 calls them: numpy.packbits (the library routine) per

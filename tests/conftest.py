@@ -36,7 +36,7 @@ def cuda():
     if not torch.cuda.is_available():
         pytest.skip("no HIP device")
     from dforktree_amd import _lib
-    _lib.load()  # fail loudly if the library is missing on a GPU box
+    _lib.load()  # fail loudly if the library is missing on a machine with a GPU
     return torch.device("cuda:0")
 
 
