@@ -1253,9 +1253,11 @@ static VerifyParams make_params(const dft_verify_args* a) {
 }
 
 // A packed batch whose largest tree exceeds 32 nodes is split by tree size:
-// the 64-wide kernel (one workgroup per CU: its LDS) takes the requests of
-// 33-64 nodes and the 32-wide kernel (four per CU) the rest, each exiting at
-// once on the other's requests.  The sizes stay on the device.
+// the 64-wide kernel (two workgroups per CU: its LDS and registers) takes the
+// requests of 33-64 nodes and the 32-wide kernel (four per CU) the rest, each
+// exiting at once on the other's requests.  The sizes stay on the device.
+// The 64-wide kernel goes first: the reverse order measured 0.4% slower on
+// 128 requests of 8-64 nodes.
 static void split_by_size(const dft_verify_args* a, const VerifyParams& P, VerifyParams& narrow, VerifyParams& wide,
                           bool& split) {
   narrow = wide = P;
