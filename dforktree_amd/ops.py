@@ -5,10 +5,11 @@ launches go on the current HIP stream of the tensors' device and nothing here
 synchronises with the host, so every operator can be captured in a HIP graph.
 Per-request slot and path indices stay on the device.
 
-These are the building blocks of the reference-named modules
-(``tree_kernels``, ``fc1_fused``, ``fc1_conv``, ``tree_ops``,
-``fc1_block_inverse``) and of the batched API the reference lacks (it is
-batch-1 only: fc1_fused.py:69, fc1_branch64.py:13).
+These are the building blocks of the reference-named modules in
+``dforktree_amd.plugin`` (``tree_kernels``, ``fc1_fused``, ``fc1_conv``,
+``fc1_block_inverse``, ``fc1_plan``), of ``dforktree_amd.builder`` and of
+the batched API the reference lacks (it is batch-1 only: fc1_fused.py:69,
+fc1_branch64.py:13).
 """
 from __future__ import annotations
 

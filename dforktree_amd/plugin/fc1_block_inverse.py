@@ -17,10 +17,10 @@ import torch
 try:
     from dforktree_amd import ops as _ops
     from dforktree_amd import _lib
-except ImportError:  # bare import from this directory
+except ImportError:  # bare import, with the package itself not on sys.path
     import pathlib
     import sys
-    sys.path.insert(0, str(pathlib.Path(__file__).resolve().parents[1]))
+    sys.path.append(str(pathlib.Path(__file__).resolve().parents[2]))
     from dforktree_amd import ops as _ops
     from dforktree_amd import _lib
 

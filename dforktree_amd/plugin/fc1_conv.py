@@ -6,7 +6,10 @@ tree conv (width 4, SiLU) over ``[conv_state || tokens]`` with the gather
 columns ``CTX.cidx``, writes each node's 3-column window into
 ``intermediate_conv_window``, stashes the [NN, C] output in
 ``fc1_fused.CTX.current_mixed`` for the verify hook, and returns the
-[1, C, NN] view.  Anything else goes to the original SGLang function.
+[1, C, NN] view.  Anything else goes to the original SGLang function, and
+so does a call the library refuses before launching (DFT_ERR_INVALID /
+DFT_ERR_UNSUPPORTED); ``current_mixed`` is then cleared, so the next
+verify falls back as well instead of reading another layer's output.
 """
 from __future__ import annotations
 
@@ -17,12 +20,12 @@ if __package__:
 else:  # bare import from this directory
     import fc1_fused as F
 try:
-    from dforktree_amd import ops as _ops
-except ImportError:
+    from dforktree_amd import _lib, ops as _ops
+except ImportError:  # bare import, with the package itself not on sys.path
     import pathlib
     import sys
-    sys.path.insert(0, str(pathlib.Path(__file__).resolve().parents[1]))
-    from dforktree_amd import ops as _ops
+    sys.path.append(str(pathlib.Path(__file__).resolve().parents[2]))
+    from dforktree_amd import _lib, ops as _ops
 
 
 def default_cidx(nn, device):
@@ -47,16 +50,23 @@ def install():
     original = backend.causal_conv1d_update
 
     def call(x, conv_state, weight, bias=None, activation=None, **kw):
+        if F.CTX is not None:
+            F.CTX.current_mixed = None
         if F.NATIVE_REFERENCE or x.ndim != 3 or x.shape[0] != 1 or x.shape[-1] != F.NN:
             return original(x, conv_state, weight, bias, activation, **kw)
         assert weight.shape[-1] == 4 and activation in ['silu', 'swish', True]
         if F.CTX is None:
             F.CTX = F.Context()
-        if not hasattr(F.CTX, 'cidx'):
+        if getattr(F.CTX, 'cidx', None) is None:
             F.CTX.cidx = default_cidx(F.NN, x.device)
         out = torch.empty((1, F.NN, x.shape[1]), device=x.device, dtype=x.dtype)
-        conv(x, conv_state, weight, bias, F.CTX.cidx, kw['conv_state_indices'], kw['intermediate_state_indices'],
-             kw['intermediate_conv_window'], out)
+        try:
+            conv(x, conv_state, weight, bias, F.CTX.cidx, kw['conv_state_indices'], kw['intermediate_state_indices'],
+                 kw['intermediate_conv_window'], out)
+        except _lib.DftError as err:
+            if not F.refused(err):
+                raise
+            return original(x, conv_state, weight, bias, activation, **kw)
         F.CTX.current_mixed = out[0]
         return out.transpose(1, 2)
 

@@ -13,12 +13,17 @@ and routes the three hooked SGLang entry points to the gfx950 library:
   verifies of NN tokens (fc1_fused.py:91-95).
 
 Shape guards fall back to the original SGLang functions exactly where the
-reference does (``cache_steps != NN``, ``draft_token_num != NN``).  Unlike
-the reference's snapshot kernel, an end of -1 (no tracked step) reads no
-state at all.
+reference does (``cache_steps != NN``, ``draft_token_num != NN``).  So does a
+call the library refuses before launching anything (status
+DFT_ERR_INVALID / DFT_ERR_UNSUPPORTED, e.g. a head dim other than 128), and
+a verify whose layer has no conv output from the conv hook (that conv ran in
+SGLang).  The commit then covers only the layers this module verified: the
+others hold SGLang's own snapshots.  Unlike the reference's snapshot
+kernel, an end of -1 (no tracked step) reads no state at all.
 """
 from __future__ import annotations
 
+import logging
 import os
 
 NN = int(os.environ.get('FC1_TREE_N', '64'))
@@ -31,12 +36,14 @@ if __package__:
 else:  # bare import from this directory (fc1_plugin's sys.path insert)
     import tree_kernels as TK
 try:
-    from dforktree_amd import ops as _ops
-except ImportError:
+    from dforktree_amd import _lib, ops as _ops
+except ImportError:  # bare import, with the package itself not on sys.path
     import pathlib
     import sys
-    sys.path.insert(0, str(pathlib.Path(__file__).resolve().parents[1]))
-    from dforktree_amd import ops as _ops
+    sys.path.append(str(pathlib.Path(__file__).resolve().parents[2]))
+    from dforktree_amd import _lib, ops as _ops
+
+_log = logging.getLogger(__name__)
 
 N_LAYERS = 24   # GDN layers of the target model (fc1_fused.py:15)
 N_HEADS = 32    # GDN v-heads (fc1_fused.py:15)
@@ -55,6 +62,8 @@ class Context:
         self.gains = torch.empty(N_LAYERS, N_HEADS, NN, device=device)
         self.layers = {}
         self.inter_indices = None
+        self.current_mixed = None  # the conv hook's [NN, C] output, consumed by the next verify
+        self.saved = set()         # layers whose last verify ran here and saved keys/values/gains
 
     def layer(self, A_log):
         """Layer index by first sight of A_log's storage, plus the cached
@@ -108,6 +117,28 @@ def _context():
     return CTX
 
 
+def refused(err) -> bool:
+    """True for a library status that launched nothing and names a request
+    this build does not take (DFT_ERR_INVALID, DFT_ERR_UNSUPPORTED): the hook
+    hands such a call to SGLang's own function, as the reference's guards do
+    (fc1_fused.py:61-62, :92-94; fc1_conv.py:34-35)."""
+    if isinstance(err, _lib.DftError) and err.status in (_lib.DFT_ERR_INVALID, _lib.DFT_ERR_UNSUPPORTED):
+        _log.warning("dforktree_amd: %s; running SGLang's own kernel instead", err)
+        return True
+    return False
+
+
+def layer_runs(layers):
+    """Sorted layer indices as [start, stop) runs of consecutive layers."""
+    runs = []
+    for li in sorted(layers):
+        if runs and runs[-1][1] == li:
+            runs[-1][1] = li + 1
+        else:
+            runs.append([li, li + 1])
+    return [tuple(r) for r in runs]
+
+
 def install():
     """Patch SGLang's GDN verify, mamba commit and routing (fc1_fused.py:51-97)."""
     from sglang.srt.layers.attention.linear.kernels.gdn_triton import TritonGDNKernel
@@ -124,16 +155,27 @@ def install():
         ctx = _context()
         li, neg = ctx.layer(A_log)
         assert li < N_LAYERS and q.shape[0] == 1 and q.shape[1] == NN
-        ctx.inter_indices = kw['intermediate_state_indices']
+        # the conv hook's output for this layer; None when this layer's conv ran in SGLang
+        y, ctx.current_mixed = ctx.current_mixed, None
+        ctx.saved.discard(li)
+        if y is None:
+            return original_verify(self, A_log, dt_bias, q, k, v, a, b, **kw)
         pool = kw['ssm_states']
-        out = TK.tree_gdn_split(ctx.current_mixed, a.reshape(NN, -1), b.reshape(NN, -1), A_log, dt_bias,
-                                pool[0].transpose(-1, -2), ctx.anc, q.shape[2], v.shape[2], q.shape[3], v.shape[3],
-                                aux=(ctx.keys[li], ctx.values[li], ctx.gains[li]), neg_exp_A=neg,
-                                state_indices=kw['cache_indices'], state_slot_stride=pool.stride(0))
+        try:
+            out = TK.tree_gdn_split(y, a.reshape(NN, -1), b.reshape(NN, -1), A_log, dt_bias,
+                                    pool[0].transpose(-1, -2), ctx.anc, q.shape[2], v.shape[2], q.shape[3],
+                                    v.shape[3], aux=(ctx.keys[li], ctx.values[li], ctx.gains[li]), neg_exp_A=neg,
+                                    state_indices=kw['cache_indices'], state_slot_stride=pool.stride(0))
+        except _lib.DftError as err:
+            if not refused(err):
+                raise
+            return original_verify(self, A_log, dt_bias, q, k, v, a, b, **kw)
+        ctx.inter_indices = kw['intermediate_state_indices']
+        ctx.saved.add(li)
         return out.unsqueeze(0)
 
     def fused_commit(target_worker, batch, accept_lens, accept_index, draft_token_num, prepared_step_indices=None):
-        if CTX is not None and draft_token_num == NN and accept_index.numel():
+        if CTX is not None and CTX.saved and draft_token_num == NN and accept_index.numel():
             last, track = _verify_commit_step_indices(batch=batch, accept_index=accept_index,
                                                       accept_lens=accept_lens, draft_token_num=draft_token_num)
             if track is None:
@@ -142,8 +184,12 @@ def install():
             pool = target_worker.model_runner.req_to_token_pool
             state = pool.get_speculative_mamba2_params_all_layers()
             slots = pool.get_mamba_indices(batch.req_pool_indices)
-            snapshot_commit(state.temporal, CTX.keys, CTX.values, CTX.gains, CTX.anc, accept_index, ends, slots,
-                            CTX.inter_indices, state.intermediate_ssm)
+            # Only the layers verified here have no snapshot from SGLang's own verify.  A refusal
+            # here cannot fall back: those layers' snapshots would be missing, so it is raised.
+            for l0, l1 in layer_runs(CTX.saved):
+                snapshot_commit(state.temporal[l0:l1], CTX.keys[l0:l1], CTX.values[l0:l1], CTX.gains[l0:l1],
+                                CTX.anc, accept_index, ends, slots, CTX.inter_indices,
+                                state.intermediate_ssm[l0:l1])
         return original_commit(target_worker, batch, accept_lens, accept_index, draft_token_num, prepared_step_indices)
 
     def direct_routing(self, **kwargs):

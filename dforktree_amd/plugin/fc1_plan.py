@@ -13,7 +13,8 @@ The fast path:
     host read-back;
   * sets the mask indptr to [0, bytes];
   * calls SGLang's ``fast_prefill_plan`` with the host-side lengths.
-Any other call goes to the original ``plan``.
+Any other call goes to the original ``plan``, and so does one whose packing
+the library refuses before launching (DFT_ERR_INVALID / DFT_ERR_UNSUPPORTED).
 
 ``pack_tree_mask()`` is the direct form for callers that hold the tree's
 ancestry bits. It builds the packed mask of fc1_branch64.py:39 (ones over
@@ -27,12 +28,12 @@ import inspect
 import torch
 
 try:
-    from dforktree_amd import ops as _ops
-except ImportError:  # bare import from this directory
+    from dforktree_amd import _lib, ops as _ops
+except ImportError:  # bare import, with the package itself not on sys.path
     import pathlib
     import sys
-    sys.path.insert(0, str(pathlib.Path(__file__).resolve().parents[1]))
-    from dforktree_amd import ops as _ops
+    sys.path.append(str(pathlib.Path(__file__).resolve().parents[2]))
+    from dforktree_amd import _lib, ops as _ops
 
 HOST_KV_LEN = None
 TREE_SIZES = (16, 32, 64)
@@ -89,7 +90,12 @@ def install():
         assert qo.numel() == 2 and values["page_size"] == 1
         n = mask.numel() // HOST_KV_LEN
         assert n in TREE_SIZES and n * HOST_KV_LEN == mask.numel()
-        pack_mask_into(self, mask, n, HOST_KV_LEN)
+        try:
+            pack_mask_into(self, mask, n, HOST_KV_LEN)
+        except _lib.DftError as err:
+            if err.status not in (_lib.DFT_ERR_INVALID, _lib.DFT_ERR_UNSUPPORTED):
+                raise
+            return original(self, *args, **kwargs)  # nothing was launched: the plan flashinfer would make
         kv_host = torch.tensor([0, HOST_KV_LEN], dtype=torch.int32)
         fast = {k: v for k, v in values.items() if k in fast_names}
         fast.update(qo_indptr_host=torch.tensor([0, n], dtype=torch.int32), kv_indptr_host=kv_host,

@@ -18,10 +18,10 @@ import torch
 try:
     from dforktree_amd import ops as _ops
     from dforktree_amd import _lib
-except ImportError:  # imported by bare name after the plugin put this directory on sys.path
+except ImportError:  # bare import, with the package itself not on sys.path
     import pathlib
     import sys
-    sys.path.insert(0, str(pathlib.Path(__file__).resolve().parents[1]))
+    sys.path.append(str(pathlib.Path(__file__).resolve().parents[2]))
     from dforktree_amd import ops as _ops
     from dforktree_amd import _lib
 
@@ -43,9 +43,9 @@ def tree_conv_fused(conv_state, mixed0, cidx, w2, bias, BC=1024):
     KC = cidx.shape[1]
     assert mixed0.stride(1) == 1 and w2.is_contiguous()
     y = torch.empty(N, C, device=mixed0.device, dtype=mixed0.dtype)
-    ci = cidx if cidx.dtype == torch.int32 and cidx.is_contiguous() else cidx.to(torch.int32).contiguous()
     assert w2.shape == (C, KC)
-    _ops.tree_conv(mixed0.unsqueeze(0), conv_state, w2, bias, ci, silu=True, y=y.unsqueeze(0))
+    # cidx goes to the kernel as it is: int32 and int64 are both read on the device
+    _ops.tree_conv(mixed0.unsqueeze(0), conv_state, w2, bias, cidx, silu=True, y=y.unsqueeze(0))
     return y
 
 

@@ -159,7 +159,8 @@ def test_snapshot_two_ends_with_ancestry(cuda):
     """fc1_fused snapshot form: two ends per request (last accepted and a
     tracked earlier step, or -1), ancestry-checked path, a separate
     destination cache indexed by node; untouched destinations stay intact."""
-    from dforktree_amd import fc1_fused, synth
+    from dforktree_amd import synth
+    from dforktree_amd.plugin import fc1_fused
     announce("snapshot two ends")
     L, B, H, N = 2, 3, 4, 32
     g = torch.Generator().manual_seed(5)
@@ -211,7 +212,8 @@ def test_snapshot_two_ends_with_ancestry(cuda):
 def test_closed_commit_dropin(cuda):
     """tree_kernels.closed_commit: states [L, H, DK, DV] (k-major), path src
     with the last index n on the device, in place."""
-    from dforktree_amd import synth, tree_kernels as TK
+    from dforktree_amd import synth
+    from dforktree_amd.plugin import tree_kernels as TK
     announce("closed_commit drop-in")
     L, H, N = 3, 4, 32
     g = torch.Generator().manual_seed(8)

@@ -25,7 +25,8 @@ pytestmark = pytest.mark.gpu
 
 
 def test_hooked_layers_then_commit(cuda, monkeypatch):
-    from dforktree_amd import fc1_conv, fc1_fused as F, synth
+    from dforktree_amd import synth
+    from dforktree_amd.plugin import fc1_conv, fc1_fused as F
     announce("hooked conv + verify x2 layers + snapshot commit")
 
     def step_indices(batch, accept_index, accept_lens, draft_token_num):

@@ -117,7 +117,7 @@ def test_plan_override_packs_on_the_device(cuda, monkeypatch):
     import fake_flashinfer
     mods, calls, saved = fake_flashinfer.install_fakes()
     try:
-        from dforktree_amd import fc1_plan as P
+        from dforktree_amd.plugin import fc1_plan as P
         P.install()
         n, plen = 64, 1237
         parents, ancs = _batch(8, [n], ["random"])

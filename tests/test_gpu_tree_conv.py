@@ -55,14 +55,15 @@ def test_tree_struct_status_flags(cuda):
     assert r["status"].cpu().tolist() == [1, 0, 2]
 
 
-def test_tree_ops_dropin_matches_reference_closure(cuda):
-    """tree_ops.tree_struct == the reference's squaring closure for N <= 32."""
-    from dforktree_amd import synth, tree_ops
-    announce("tree_ops drop-in")
+def test_builder_tree_struct_matches_reference_closure(cuda):
+    """builder.tree_struct (the opt-in for tree_ops.tree_struct) == the
+    reference's squaring closure for N <= 32."""
+    from dforktree_amd import builder, synth
+    announce("builder.tree_struct")
     g = torch.Generator().manual_seed(1)
     for kind in ("random", "chain", "bushy"):
         p = synth.tree_parents(32, kind, g)
-        anc, depth, cidx = tree_ops.tree_struct(p.to(cuda).long(), 4)
+        anc, depth, cidx = builder.tree_struct(p.to(cuda).long(), 4)
         ra, rd, rc = O.tree_struct_squaring(p.numpy(), 4)
         assert anc.dtype == torch.float32 and depth.dtype == torch.int64 and cidx.dtype == torch.int64
         assert np.array_equal(anc.cpu().numpy(), ra)
@@ -121,7 +122,7 @@ def test_conv_slots_bias_and_state(cuda):
 
 def test_tree_conv_fused_dropin(cuda):
     """tree_kernels.tree_conv_fused: 2-D conv_state [C, T], mixed0 [N, C]."""
-    from dforktree_amd import tree_kernels as TK
+    from dforktree_amd.plugin import tree_kernels as TK
     announce("tree_conv_fused drop-in")
     N, C = 32, 512
     x, w, cs, cidx = _conv_inputs(3, 1, N, C)

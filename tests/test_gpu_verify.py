@@ -121,7 +121,8 @@ def test_verify_state_indices(cuda):
 def test_tree_gdn_split_dropin(cuda):
     """tree_kernels.tree_gdn_split with the plugin's argument forms: pool view,
     slot on device, cached neg_exp_A, aux buffers [Hv, N, D]."""
-    from dforktree_amd import synth, tree_kernels as TK
+    from dforktree_amd import synth
+    from dforktree_amd.plugin import tree_kernels as TK
     announce("tree_gdn_split drop-in")
     batch = synth.make_batch(6, 0, [32], hk=2, hv=4)
     anc = torch.from_numpy(O.tree_struct(batch.parent.numpy())[0])
@@ -147,7 +148,8 @@ def test_tree_gdn_split_dropin(cuda):
 
 def test_tree_gdn_fused_dropin(cuda):
     """tree_gdn_fused returns fp32 and, for N > 32, delegates to the split path."""
-    from dforktree_amd import synth, tree_kernels as TK
+    from dforktree_amd import synth
+    from dforktree_amd.plugin import tree_kernels as TK
     announce("tree_gdn_fused drop-in")
     for n in (24, 64):
         batch = synth.make_batch(7, 0, [n], hk=2, hv=4)
@@ -165,7 +167,7 @@ def test_tree_gdn_fused_dropin(cuda):
 
 
 def test_block_inverse_dropin(cuda):
-    from dforktree_amd import fc1_block_inverse as FBI
+    from dforktree_amd.plugin import fc1_block_inverse as FBI
     import scipy.linalg
     announce("block inverse")
     rng = np.random.default_rng(0)

@@ -13,7 +13,7 @@ from fake_sglang import install_fakes, remove_fakes
 
 @pytest.fixture
 def hooked(monkeypatch):
-    from dforktree_amd import fc1_conv, fc1_fused as F
+    from dforktree_amd.plugin import fc1_conv, fc1_fused as F
 
     def step_indices(batch, accept_index, accept_lens, draft_token_num):
         last = accept_index.gather(1, (accept_lens.long() - 1)[:, None])
@@ -47,7 +47,8 @@ def test_verify_hook_routes_tree_verifies_to_split(hooked, monkeypatch):
 
     monkeypatch.setattr(F.TK, "tree_gdn_split", fake_split)
     K = mods["sglang.srt.layers.attention.linear.kernels.gdn_triton"].TritonGDNKernel
-    F.CTX.current_mixed = torch.zeros(F.NN, 8192, dtype=torch.bfloat16)
+    mixed = torch.zeros(F.NN, 8192, dtype=torch.bfloat16)
+    F.CTX.current_mixed = mixed
     pool = torch.zeros(3, 32, 128, 128)
     A_log, dt_bias, q, k, v, a, b = _verify_args(F.NN)
     slots, islots = torch.tensor([2]), torch.tensor([1])
@@ -56,7 +57,9 @@ def test_verify_hook_routes_tree_verifies_to_split(hooked, monkeypatch):
     assert out.shape == (1, F.NN, 32, 128)
     (args, kw), = seen
     y, aa, bb, A, dtb, S0, anc, Hk, Hv, Dk, Dv = args
-    assert y is F.CTX.current_mixed and anc is F.CTX.anc
+    assert y is mixed and anc is F.CTX.anc
+    # the conv output is consumed: a verify never reads another layer's
+    assert F.CTX.current_mixed is None and F.CTX.saved == {0}
     assert aa.shape == (F.NN, 32) and (Hk, Hv, Dk, Dv) == (16, 32, 128, 128)
     assert S0.shape == (32, 128, 128) and S0.stride() == pool[0].transpose(-1, -2).stride()
     assert kw["state_indices"] is slots and kw["state_slot_stride"] == pool.stride(0)
@@ -66,12 +69,12 @@ def test_verify_hook_routes_tree_verifies_to_split(hooked, monkeypatch):
     assert F.CTX.inter_indices is islots
     # a second layer (another A_log) gets the next aux slice; the first keeps its index
     A2 = A_log.clone()
-    K().target_verify(A2, dt_bias, q, k, v, a, b, cache_steps=F.NN, ssm_states=pool, cache_indices=slots,
-                      intermediate_state_indices=islots)
-    K().target_verify(A_log, dt_bias, q, k, v, a, b, cache_steps=F.NN, ssm_states=pool, cache_indices=slots,
-                      intermediate_state_indices=islots)
+    for A in (A2, A_log):
+        F.CTX.current_mixed = mixed
+        K().target_verify(A, dt_bias, q, k, v, a, b, cache_steps=F.NN, ssm_states=pool, cache_indices=slots,
+                          intermediate_state_indices=islots)
     assert [s[1]["aux"][0].data_ptr() for s in seen] == [F.CTX.keys[i].data_ptr() for i in (0, 1, 0)]
-    assert calls.names() == []
+    assert calls.names() == [] and F.CTX.saved == {0, 1}
 
 
 def test_verify_hook_falls_back_for_other_step_counts(hooked):
@@ -108,6 +111,7 @@ def test_commit_hook_snapshots_both_ends_then_calls_original(hooked, monkeypatch
     commit = mods["sglang.srt.speculative.eagle_worker_common"].commit_mamba_states_after_verify
     temporal, inter, slots = torch.zeros(2, 3, 4, 1, 1), torch.zeros(2, 2, F.NN, 4, 1, 1), torch.tensor([2])
     F.CTX.inter_indices = torch.tensor([1])
+    F.CTX.saved = {0, 1}   # both layers verified here
     accept_index = torch.tensor([[0, 5, 9, -1]], dtype=torch.int32)
     batch = types.SimpleNamespace(req_pool_indices=torch.tensor([0]),
                                   track=None if track is None else torch.tensor([[track]]))
@@ -116,8 +120,11 @@ def test_commit_hook_snapshots_both_ends_then_calls_original(hooked, monkeypatch
     assert calls.names() == ["step_indices", "original_commit"]
     (args,), = [seen]
     S, keys, vals, gains, anc, acc, ends, sl, isl, dst = args
-    assert S is temporal and dst is inter and sl is slots and isl is F.CTX.inter_indices
-    assert keys is F.CTX.keys and anc is F.CTX.anc and acc is accept_index
+    assert S.data_ptr() == temporal.data_ptr() and S.shape == temporal.shape
+    assert dst.data_ptr() == inter.data_ptr() and dst.shape == inter.shape
+    assert sl is slots and isl is F.CTX.inter_indices
+    assert keys.data_ptr() == F.CTX.keys.data_ptr() and keys.shape[0] == 2
+    assert anc is F.CTX.anc and acc is accept_index
     assert ends.tolist() == [[9, -1 if track is None else track]]
 
 
@@ -160,3 +167,100 @@ def test_conv_hook_routes_batch1_tree_verifies(hooked, monkeypatch):
     monkeypatch.setattr(F, "NATIVE_REFERENCE", True)
     assert backend.causal_conv1d_update(x, cs, w) == "original_conv"
     assert calls.names() == ["original_conv"] * 3
+
+
+def _refusal(status):
+    from dforktree_amd import _lib
+
+    def raise_status(*args, **kw):
+        raise _lib.DftError("dft_stub", status, "forced by the test")
+    return raise_status
+
+
+def test_refused_verify_falls_back_and_is_not_committed(hooked, monkeypatch):
+    """A verify the library refuses (nothing launched) runs SGLang's own
+    kernel (fc1_fused.py:61-62), and the commit then leaves that layer to
+    SGLang's snapshot."""
+    from dforktree_amd import _lib
+    F, _, mods, calls = hooked
+    K = mods["sglang.srt.layers.attention.linear.kernels.gdn_triton"].TritonGDNKernel
+    A_log, dt_bias, q, k, v, a, b = _verify_args(F.NN)
+    kw = dict(cache_steps=F.NN, ssm_states=torch.zeros(3, 32, 128, 128), cache_indices=torch.tensor([0]),
+              intermediate_state_indices=torch.tensor([0]))
+    F.CTX.saved = {0}
+    for status in (_lib.DFT_ERR_UNSUPPORTED, _lib.DFT_ERR_INVALID):
+        monkeypatch.setattr(F.TK, "tree_gdn_split", _refusal(status))
+        F.CTX.current_mixed = torch.zeros(F.NN, 8192, dtype=torch.bfloat16)
+        assert K().target_verify(A_log, dt_bias, q, k, v, a, b, **kw) == "original_verify"
+        assert F.CTX.saved == set() and F.CTX.current_mixed is None
+    assert calls.names() == ["original_verify"] * 2
+    # a launch failure is not a refusal: it propagates
+    monkeypatch.setattr(F.TK, "tree_gdn_split", _refusal(_lib.DFT_ERR_LAUNCH))
+    F.CTX.current_mixed = torch.zeros(F.NN, 8192, dtype=torch.bfloat16)
+    with pytest.raises(_lib.DftError):
+        K().target_verify(A_log, dt_bias, q, k, v, a, b, **kw)
+    # no layer was verified here: the commit launches nothing and calls SGLang's commit
+    monkeypatch.setattr(F, "snapshot_commit", lambda *args: pytest.fail("must not commit"))
+    commit = mods["sglang.srt.speculative.eagle_worker_common"].commit_mamba_states_after_verify
+    batch = types.SimpleNamespace(req_pool_indices=torch.tensor([0]))
+    assert commit(None, batch, torch.tensor([1]), torch.tensor([[0]]), F.NN) == "original_commit"
+
+
+def test_refused_conv_falls_back_and_so_does_the_next_verify(hooked, monkeypatch):
+    """fc1_conv.py:34-35: a refused conv runs SGLang's conv; the verify of
+    that layer then has no tree input and falls back too."""
+    from dforktree_amd import _lib
+    F, conv_mod, mods, calls = hooked
+    backend = mods["sglang.srt.layers.attention.linear.gdn_backend"]
+    K = mods["sglang.srt.layers.attention.linear.kernels.gdn_triton"].TritonGDNKernel
+    monkeypatch.setattr(F.TK, "tree_gdn_split", lambda *a, **k: pytest.fail("must not verify"))
+    C = 96
+    x = torch.zeros(1, C, F.NN, dtype=torch.bfloat16)
+    cs, w, iw = torch.zeros(3, C, 3), torch.zeros(C, 4), torch.zeros(2, F.NN, C, 3)
+    conv_kw = dict(conv_state_indices=torch.tensor([0]), intermediate_state_indices=torch.tensor([0]),
+                   intermediate_conv_window=iw)
+    monkeypatch.setattr(conv_mod._ops, "tree_conv", _refusal(_lib.DFT_ERR_UNSUPPORTED))
+    F.CTX.current_mixed = torch.zeros(F.NN, C, dtype=torch.bfloat16)   # a previous layer's output
+    assert backend.causal_conv1d_update(x, cs, w, None, "silu", **conv_kw) == "original_conv"
+    assert F.CTX.current_mixed is None
+    A_log, dt_bias, q, k, v, a, b = _verify_args(F.NN)
+    out = K().target_verify(A_log, dt_bias, q, k, v, a, b, cache_steps=F.NN, ssm_states=torch.zeros(1, 32, 128, 128),
+                            cache_indices=torch.tensor([0]), intermediate_state_indices=torch.tensor([0]))
+    assert out == "original_verify"
+    assert calls.names() == ["original_conv", "original_verify"]
+    # a conv that falls back on its guard clears the stale output as well
+    F.CTX.current_mixed = torch.zeros(F.NN, C, dtype=torch.bfloat16)
+    assert backend.causal_conv1d_update(torch.zeros(2, C, F.NN), cs, w) == "original_conv"
+    assert F.CTX.current_mixed is None
+    monkeypatch.setattr(conv_mod._ops, "tree_conv", _refusal(_lib.DFT_ERR_LAUNCH))
+    with pytest.raises(_lib.DftError):
+        backend.causal_conv1d_update(x, cs, w, None, "silu", **conv_kw)
+
+
+def test_commit_covers_only_layers_verified_here(hooked, monkeypatch):
+    """Layers whose verify fell back keep SGLang's snapshots: the commit
+    launches over the runs of layers verified here, and a refusal there is
+    raised (falling back would leave those layers without a snapshot)."""
+    from dforktree_amd import _lib
+    F, _, mods, calls = hooked
+    seen = []
+    monkeypatch.setattr(F, "snapshot_commit", lambda *args: seen.append(args))
+    commit = mods["sglang.srt.speculative.eagle_worker_common"].commit_mamba_states_after_verify
+    L = 6
+    temporal, inter = torch.zeros(L, 3, 4, 1, 1), torch.zeros(L, 2, F.NN, 4, 1, 1)
+    F.CTX.inter_indices = torch.tensor([1])
+    F.CTX.saved = {0, 1, 3, 5}
+    batch = types.SimpleNamespace(req_pool_indices=torch.tensor([0]), track=None)
+    accept_index = torch.tensor([[0, 2, -1]], dtype=torch.int32)
+    assert commit(_worker(temporal, inter, torch.tensor([2])), batch, torch.tensor([2]), accept_index,
+                  F.NN) == "original_commit"
+    got = [(args[0].data_ptr() - temporal.data_ptr()) // temporal.stride(0) // 4 for args in seen]
+    assert got == [0, 3, 5] and [args[0].shape[0] for args in seen] == [2, 1, 1]
+    for args in seen:
+        l0 = (args[0].data_ptr() - temporal.data_ptr()) // temporal.stride(0) // 4
+        assert args[1].data_ptr() == F.CTX.keys[l0].data_ptr() and args[1].shape[0] == args[0].shape[0]
+        assert args[9].data_ptr() == inter[l0].data_ptr() and args[9].shape[0] == args[0].shape[0]
+    assert F.layer_runs({0, 1, 3, 5}) == [(0, 2), (3, 4), (5, 6)] and F.layer_runs(set()) == []
+    monkeypatch.setattr(F, "snapshot_commit", _refusal(_lib.DFT_ERR_UNSUPPORTED))
+    with pytest.raises(_lib.DftError):
+        commit(_worker(temporal, inter, torch.tensor([2])), batch, torch.tensor([2]), accept_index, F.NN)

@@ -15,7 +15,7 @@ N, PLEN = 32, 77
 @pytest.fixture
 def plan_mod(monkeypatch):
     mods, calls, saved = fake_flashinfer.install_fakes()
-    from dforktree_amd import fc1_plan as P
+    from dforktree_amd.plugin import fc1_plan as P
 
     def np_packbits(x, bitorder="little", *, out=None, status=None):
         p = torch.from_numpy(np.packbits(x.cpu().numpy().reshape(-1) != 0, bitorder=bitorder))
@@ -79,3 +79,22 @@ def test_tree_sizes_are_checked(plan_mod, monkeypatch):
     monkeypatch.setattr(P, "HOST_KV_LEN", 10)
     with pytest.raises(AssertionError):
         W().plan(**dict(_args(torch.ones(12 * 10, dtype=torch.bool)), qo_indptr=torch.tensor([0, 12])))
+
+
+def test_refused_packing_falls_back_to_the_original_plan(plan_mod, monkeypatch):
+    """A packing the library refuses before launching goes to flashinfer's
+    own plan; a launch failure propagates."""
+    from dforktree_amd import _lib
+    P, W, calls = plan_mod
+    monkeypatch.setattr(P, "HOST_KV_LEN", PLEN + N)
+    for status, falls_back in ((_lib.DFT_ERR_UNSUPPORTED, True), (_lib.DFT_ERR_INVALID, True),
+                               (_lib.DFT_ERR_LAUNCH, False)):
+        def refuse(*args, _status=status, **kw):
+            raise _lib.DftError("dft_packbits", _status, "forced by the test")
+        monkeypatch.setattr(P._ops, "packbits", refuse)
+        if falls_back:
+            assert W().plan(**_args(_mask())) == "original_plan"
+            assert calls[-1][0] == "original_plan"
+        else:
+            with pytest.raises(_lib.DftError):
+                W().plan(**_args(_mask()))
