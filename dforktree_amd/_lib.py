@@ -15,6 +15,8 @@ DFT_OK, DFT_ERR_INVALID, DFT_ERR_UNSUPPORTED, DFT_ERR_LAUNCH = 0, 1, 2, 3
 DFT_F32, DFT_BF16, DFT_F16, DFT_I32, DFT_I64 = 0, 1, 2, 3, 4
 DFT_VERIFY_AUX_K_PER_KHEAD = 1
 DFT_COMMIT_KV, DFT_COMMIT_CHECK_ANC, DFT_COMMIT_LEN_IS_LAST = 1, 2, 4
+DFT_STATUS_SPAN, DFT_STATUS_PATH = 1, 2
+ABI_VERSION = 2
 
 i32, i64, f32, vp = C.c_int32, C.c_int64, C.c_float, C.c_void_p
 
@@ -38,6 +40,7 @@ class VerifyArgs(C.Structure):
         ("aux_k", vp), ("aux_k_h_stride", i64), ("aux_k_row_stride", i64),
         ("aux_v", vp), ("aux_v_h_stride", i64), ("aux_v_row_stride", i64),
         ("aux_g", vp), ("aux_g_h_stride", i64), ("aux_g_row_stride", i64),
+        ("status", vp),
     ]
 
 
@@ -88,6 +91,7 @@ class CommitArgs(C.Structure):
         ("dst", vp), ("dst_layer_stride", i64), ("dst_slot_stride", i64), ("dst_node_stride", i64),
         ("dst_h_stride", i64), ("dst_row_stride", i64), ("dst_col_stride", i64),
         ("dst_slots", vp), ("dst_slots_dtype", i32),
+        ("status", vp),
     ]
 
 
@@ -171,6 +175,9 @@ def load() -> C.CDLL:
     lib.dft_error_string.restype = C.c_char_p
     lib.dft_abi_version.argtypes = []
     lib.dft_abi_version.restype = C.c_int
+    if lib.dft_abi_version() != ABI_VERSION:
+        raise LibraryMissing(f"{LIB_PATH} has ABI version {lib.dft_abi_version()}, this binding needs {ABI_VERSION}; "
+                             "rebuild it (python -m dforktree_amd.build)")
     _lib = lib
     return lib
 

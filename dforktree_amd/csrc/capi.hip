@@ -74,7 +74,8 @@ int dft_tree_commit_verify(const dft_verify_args* a, const dft_pending_commit* c
   const int st = verify_status(a);
   if (st != DFT_OK) return st < 0 ? DFT_OK : st;
   if (!c) return DFT_ERR_INVALID;
-  if (c->path_cols < 0 || c->path_cols > 16) return DFT_ERR_UNSUPPORTED;
+  if (c->path_cols < 1) return DFT_ERR_INVALID;  // the kernels read entry path_cols - 1 for padding lanes
+  if (c->path_cols > 16) return DFT_ERR_UNSUPPORTED;
   if (c->k_head_div <= 0 || a->hv % c->k_head_div != 0) return DFT_ERR_INVALID;
   if (!c->prev_cu_seqlens && (c->prev_n_nodes < 0 || c->prev_n_nodes > 64)) return DFT_ERR_INVALID;
   if (!c->path || !c->keys || !c->values || !c->gains) return DFT_ERR_INVALID;
@@ -118,7 +119,8 @@ int dft_tree_commit(const dft_commit_args* a, void* stream) {
   if (!a) return DFT_ERR_INVALID;
   if (a->n_layers < 0 || a->batch < 0 || a->hv <= 0 || a->n_nodes < 0) return DFT_ERR_INVALID;
   if (a->dk != 128 || a->dv != 128) return DFT_ERR_UNSUPPORTED;
-  if (a->n_nodes > 64 || a->path_cols < 0 || a->path_cols > 64) return DFT_ERR_UNSUPPORTED;
+  if (a->path_cols < 1) return DFT_ERR_INVALID;
+  if (a->n_nodes > 64 || a->path_cols > 64) return DFT_ERR_UNSUPPORTED;
   if (a->n_ends != 1 && a->n_ends != 2) return DFT_ERR_INVALID;
   if (a->k_head_div <= 0 || a->hv % a->k_head_div != 0) return DFT_ERR_INVALID;
   if (a->n_layers == 0 || a->batch == 0) return DFT_OK;

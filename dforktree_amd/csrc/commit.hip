@@ -22,6 +22,28 @@ struct CommitParams {
   int src_vec, dst_vec;  // 16-byte vector path usable
 };
 
+// path entries of request b that count (path_len, or all path_cols)
+__device__ __forceinline__ int path_entries(const dft_commit_args& p, int b) {
+  int len = p.path_cols;
+  if (p.path_len) {
+    len = (int)ld_i(p.path_len, b, p.path_len_dtype);
+    if (p.flags & DFT_COMMIT_LEN_IS_LAST) len += 1;
+    len = len < 0 ? 0 : (len > p.path_cols ? p.path_cols : len);
+  }
+  return len;
+}
+
+// The status word of request b (wave 0 of its first workgroup): a row span
+// past n_nodes, and path entries or ends at or past its n nodes.
+__device__ __forceinline__ void commit_status(const dft_commit_args& p, int b, int n, bool span_bad, int lane) {
+  const int len = path_entries(p, b);
+  bool bad = false;
+  for (int c = lane; c < len; c += 64) bad |= ld_i(p.path, (int64_t)b * p.path_req_stride + c, p.path_dtype) >= n;
+  if (p.ends && lane < p.n_ends) bad |= ld_i(p.ends, (int64_t)b * p.ends_req_stride + lane, p.ends_dtype) >= n;
+  const bool any = __ballot(bad) != 0;
+  if (lane == 0) p.status[b] = (span_bad ? DFT_STATUS_SPAN : 0) | (any ? DFT_STATUS_PATH : 0);
+}
+
 // Five waves per SIMD (five workgroups per CU instead of four, 64 KiB more
 // state in flight per CU): 48.3 -> 46.4 us per layer at batch 64 in
 // interleaved runs.  At the 96-register budget this takes, 14 registers are
@@ -47,16 +69,18 @@ tree_commit_kernel(const CommitParams P) {
   const int b = id % p.batch;
   const int l = id / p.batch;
 
+  // nodes of the request: its row span cut to [0, n_nodes]
   int64_t row0;
-  int n;
+  int span;
   if (p.cu_seqlens) {
     row0 = p.cu_seqlens[b];
-    n = p.cu_seqlens[b + 1] - p.cu_seqlens[b];
+    span = p.cu_seqlens[b + 1] - p.cu_seqlens[b];
   } else {
     row0 = (int64_t)b * p.n_nodes;
-    n = p.n_nodes;
+    span = p.n_nodes;
   }
-  n = n < 0 ? 0 : (n > 64 ? 64 : n);
+  const int n = span < 0 ? 0 : (span > p.n_nodes ? p.n_nodes : span);
+  if (p.status && l == 0 && h == 0 && e == 0 && tid < 64) commit_status(p, b, n, span < 0 || span > p.n_nodes, lane);
 
   int u_end = -1;
   if (p.ends) {
@@ -93,12 +117,7 @@ tree_commit_kernel(const CommitParams P) {
 
   // ---- path bookkeeping on wave 0: the nodes that contribute, in path order
   if (tid < 64) {
-    int len = p.path_cols;
-    if (p.path_len) {
-      len = (int)ld_i(p.path_len, b, p.path_len_dtype);
-      if (p.flags & DFT_COMMIT_LEN_IS_LAST) len += 1;
-      len = len < 0 ? 0 : (len > p.path_cols ? p.path_cols : len);
-    }
+    const int len = path_entries(p, b);
     int node = -1;
     if (lane < len) node = (int)ld_i(p.path, (int64_t)b * p.path_req_stride + lane, p.path_dtype);
     if (node >= n) node = -1;

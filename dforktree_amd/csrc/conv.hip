@@ -19,9 +19,12 @@ __global__ void __launch_bounds__(256) tree_conv_kernel(const dft_conv_args p) {
   if (c >= p.channels) return;
   const int W = p.width;
 
+  // A negative state slot (a padded request) reads slot 0; a negative window
+  // slot writes no window.
   int64_t slot = b, dst = b;
   if (p.cs_indices) slot = ld_i(p.cs_indices, b, p.cs_indices_dtype);
   if (p.iw_indices) dst = ld_i(p.iw_indices, b, p.iw_indices_dtype);
+  if (slot < 0) slot = 0;
 
   const int64_t cbase = (int64_t)b * p.cidx_req_stride + (int64_t)n * p.cidx_node_stride;
   float acc = 0.f;
@@ -40,7 +43,7 @@ __global__ void __launch_bounds__(256) tree_conv_kernel(const dft_conv_args p) {
                  p.x_dtype);
     const float w = ld_f(p.weight, (int64_t)c * p.w_chan_stride + (int64_t)j * p.w_tap_stride, p.w_dtype);
     acc += val * w;
-    if (j > 0 && p.iw)
+    if (j > 0 && p.iw && dst >= 0)
       st_f(p.iw,
            dst * p.iw_slot_stride + (int64_t)n * p.iw_node_stride + (int64_t)c * p.iw_chan_stride +
                (int64_t)(j - 1) * p.iw_col_stride,
@@ -124,8 +127,9 @@ __global__ void __launch_bounds__(64) tree_conv4_bf16_kernel(const dft_conv_args
 #pragma unroll
     for (int j = 0; j < 4; ++j)
       if (!tok[j]) raw[j] = u32x4{0u, 0u, 0u, 0u};
-    // the state slot (needed by conv-state taps only)
+    // the state slot (needed by conv-state taps only); a negative one reads slot 0
     if (p.cs_indices) slot = ld_i(p.cs_indices, b, p.cs_indices_dtype);
+    if (slot < 0) slot = 0;
 
     float acc[8];
 #pragma unroll
@@ -164,12 +168,14 @@ __global__ void __launch_bounds__(64) tree_conv4_bf16_kernel(const dft_conv_args
   if (p.iw) {
     if (p.iw_indices) dst = ld_i(p.iw_indices, b, p.iw_indices_dtype);
     __syncthreads();
-    u32x4* iw = reinterpret_cast<u32x4*>(static_cast<uint16_t*>(p.iw) + dst * p.iw_slot_stride +
-                                         (int64_t)n * p.iw_node_stride + (int64_t)cb * 512 * 3);
+    if (dst >= 0) {  // uniform over the block (one request); a negative slot writes no window
+      u32x4* iw = reinterpret_cast<u32x4*>(static_cast<uint16_t*>(p.iw) + dst * p.iw_slot_stride +
+                                           (int64_t)n * p.iw_node_stride + (int64_t)cb * 512 * 3);
 #pragma unroll
-    for (int q = 0; q < 3; ++q) {
-      const int i = threadIdx.x + 64 * q;
-      if (i < nact * 3) iw[i] = stage[i];
+      for (int q = 0; q < 3; ++q) {
+        const int i = threadIdx.x + 64 * q;
+        if (i < nact * 3) iw[i] = stage[i];
+      }
     }
   }
 }

@@ -350,6 +350,7 @@ struct Pending {
   int ent;         // this lane's entry (an invalid one replaced by u)
   uint32_t vmask;  // bit c: entry c valid
   int last;        // slot of u, -1 when nothing is pending
+  bool bad;        // an entry within the length names a node past the previous tree
   int64_t prow0;   // row of the request's node 0 in the previous step's buffers
 };
 
@@ -368,18 +369,21 @@ struct PendingHead {
   int bound, len;
 };
 
-__device__ __forceinline__ PendingHead pending_head(const dft_pending_commit& c, int b) {
+// (CP: a pointer to the descriptor, generic or in the kernel-argument segment)
+template <class CP>
+__device__ __forceinline__ PendingHead pending_head(CP c, int b) {
   PendingHead ph;
-  if (c.prev_cu_seqlens) {
-    ph.prow0 = c.prev_cu_seqlens[b];
-    ph.bound = c.prev_cu_seqlens[b + 1] - c.prev_cu_seqlens[b];
+  const int32_t* pcu = c->prev_cu_seqlens;
+  if (pcu) {
+    ph.prow0 = pcu[b];
+    ph.bound = pcu[b + 1] - pcu[b];
   } else {
-    ph.prow0 = (int64_t)b * c.prev_n_nodes;
-    ph.bound = c.prev_n_nodes;
+    ph.prow0 = (int64_t)b * c->prev_n_nodes;
+    ph.bound = c->prev_n_nodes;
   }
-  ph.len = c.path_cols;
-  if (c.path_len) {
-    const int64_t l = ld_i(c.path_len, b, c.path_len_dtype);
+  ph.len = c->path_cols;
+  if (c->path_len) {
+    const int64_t l = ld_i(c->path_len, b, c->path_len_dtype);
     ph.len = l < 0 ? 0 : (l < ph.len ? (int)l : ph.len);
   }
   return ph;
@@ -391,6 +395,7 @@ __device__ __forceinline__ Pending decode_pending(const PendingHead& ph, int lan
   const int bound = ph.bound, len = ph.len;
   const int e = (int)word;
   const bool ok = (lane & 15) < len && e >= 0 && e < bound;
+  pd.bad = (__ballot((lane & 15) < len && e >= bound) & 0xffffull) != 0;
   pd.vmask = (uint32_t)__ballot(ok) & 0xffffu;
   pd.last = pd.vmask ? 31 - __clz(pd.vmask) : -1;
   const int u = __shfl(e, pd.last < 0 ? 0 : pd.last);
@@ -512,6 +517,7 @@ __device__ __forceinline__ void store_state(float* S, int64_t v_stride, int wave
 struct Item {
   int b, hk, rr, h;  // request, k-head, v-head within the k-head, v-head
   int n;             // nodes (0: nothing to verify)
+  bool span_bad;     // row span negative or past n_nodes (cut to n_nodes): DFT_STATUS_SPAN
   bool no_slot = false;  // negative state index: S0 is read from slot 0, nothing is committed
   int64_t row0;      // row of node 0
   const float* S0;   // the head's state tile (k stride 1 on the vector paths)
@@ -539,20 +545,24 @@ __device__ __forceinline__ void item_heads(const dft_verify_args& p, int id, Ite
   it.h = it.hk * R + rr;
 }
 
-// rows, node count and state tile of a request (loads the index arrays)
-// Returns false when the request belongs to the other kernel of a launch
-// split by tree size (its node count outside [n_lo, n_hi]).
+// rows, node count and state tile of a request (loads the index arrays).
+// A row span that is negative or exceeds n_nodes is cut to [0, n_nodes] and
+// flagged.  Returns false when the request belongs to the other kernel of a
+// launch split by tree size (its node count outside [n_lo, n_hi]).
 template <int NP>
 __device__ __forceinline__ bool item_rows(const dft_verify_args& p, Item& it, int n_lo, int n_hi) {
+  int span;
   if (p.cu_seqlens) {
     it.row0 = p.cu_seqlens[it.b];
-    it.n = p.cu_seqlens[it.b + 1] - p.cu_seqlens[it.b];
+    span = p.cu_seqlens[it.b + 1] - p.cu_seqlens[it.b];
   } else {
     it.row0 = (int64_t)it.b * p.n_nodes;
-    it.n = p.n_nodes;
+    span = p.n_nodes;
   }
+  it.span_bad = span < 0 || span > p.n_nodes;
+  it.n = span < 0 ? 0 : (span > p.n_nodes ? p.n_nodes : span);
   if (it.n < n_lo || it.n > n_hi) return false;
-  it.n = it.n < 0 ? 0 : (it.n > NP ? NP : it.n);
+  it.n = it.n > NP ? NP : it.n;  // the launch width covers n_nodes: never cuts
   int64_t slot = it.b;
   if (p.state_indices) {
     slot = ld_i(p.state_indices, it.b, p.state_indices_dtype);
@@ -1077,6 +1087,28 @@ __device__ __forceinline__ void phase_stores(const VerifyParams& P, const Item& 
   }
 }
 
+// The fused kernel's status word (wave 0 of the request's head-0
+// workgroup), written at the end of the workgroup from this lane's pending
+// path entry word (still in gate row 4 of LDS there) and the arguments
+// re-read from the kernel-argument segment.  Evaluated early and held
+// through the state stream, the flags cost the kernel a spilled register.
+__device__ __forceinline__ void fused_status(const Item& it, int lane, uint32_t path_word) {
+  typedef const __attribute__((address_space(4))) VerifyParams* KParams;
+  KParams kp = (KParams)__builtin_amdgcn_kernarg_segment_ptr();
+  asm volatile("" : "+s"(kp));
+  int32_t* status = kp->a.status;
+  if (!status) return;
+  const int b = it.b;
+  const int32_t* cu = kp->a.cu_seqlens;
+  const int nn = kp->a.n_nodes;
+  const int span = cu ? cu[b + 1] - cu[b] : nn;
+  PendingHead ph = pending_head(&kp->c, b);
+  // no slot of its own: nothing is committed, as in the commit itself
+  if (kp->a.state_indices && ld_i(kp->a.state_indices, b, kp->a.state_indices_dtype) < 0) ph.len = 0;
+  const Pending pd = decode_pending(ph, lane, path_word);
+  if (lane == 0) status[b] = (span < 0 || span > nn ? DFT_STATUS_SPAN : 0) | (pd.bad ? DFT_STATUS_PATH : 0);
+}
+
 // The body of the one-head-per-workgroup kernels (COMMIT: the fused commit ->
 // verify form).
 template <int NP, bool S0VEC, bool COMMIT>
@@ -1093,13 +1125,20 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
   Item it;
   item_heads(p, blockIdx.x, it);
   if (!item_rows<NP>(p, it, P.n_lo, P.n_hi)) return;
+  // Thread 0 of the request's head-0 workgroup writes its status word (the
+  // condition is evaluated where it is written: held from here, it would
+  // cost the fused kernel a register through the state stream).
+  if constexpr (!COMMIT)
+    if (p.status && it.h == 0 && tid == 0) p.status[it.b] = it.span_bad ? DFT_STATUS_SPAN : 0;
   const float* S0 = it.S0;
   PendingHead ph{};
   if constexpr (COMMIT) {
-    ph = pending_head(P.c, it.b);
+    ph = pending_head(&P.c, it.b);
     if (it.no_slot) ph.len = 0;  // no slot of its own: nothing is committed
     if (it.n == 0) {  // nothing to verify this step: the commit alone
-      const Pending pd = decode_pending(ph, lane, *path_word(P.c, it.b, lane));
+      const uint32_t word = *path_word(P.c, it.b, lane);
+      const Pending pd = decode_pending(ph, lane, word);
+      if (it.h == 0 && wave == 0) fused_status(it, lane, word);
       if (pd.last < 0) return;
       f32x4 s0r[2][8], kr[2];
       float vnr[4][2], gp[4];
@@ -1217,6 +1256,8 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
     __syncthreads();
     phase_stores<NP, COMMIT>(P, it, tid, sm);
   }
+  if constexpr (COMMIT)
+    if (it.h == 0 && wave == 0) fused_status(it, lane, sm.graw[4][lane & 15]);
 }
 
 template <int NP, bool S0VEC>

@@ -86,7 +86,7 @@ def tree_verify(y: torch.Tensor, a: torch.Tensor, b: torch.Tensor, A_log: Option
                 state_slot_stride: Optional[int] = None, o: Optional[torch.Tensor] = None,
                 o_dtype: Optional[torch.dtype] = None, aux_k: Optional[torch.Tensor] = None,
                 aux_v: Optional[torch.Tensor] = None, aux_g: Optional[torch.Tensor] = None,
-                aux_k_per_khead: bool = False) -> torch.Tensor:
+                aux_k_per_khead: bool = False, status: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Fused tree verify of every (request, v-head).
 
     y [rows, 2*hk*128 + hv*128] bf16 with channel stride 1; a, b [rows, hv];
@@ -95,19 +95,32 @@ def tree_verify(y: torch.Tensor, a: torch.Tensor, b: torch.Tensor, A_log: Option
     the tree as ``anc`` [batch, N, N] / [N, N] 0/1 or ``anc_bits`` [rows]
     int64 bit masks.  Rows of request b start at cu_seqlens[b] (packed) or
     b*n_nodes.  Returns o [rows, hv, dv]; aux_k [hv|hk, rows, dk],
-    aux_v [hv, rows, dv], aux_g [hv, rows] are filled when given.
+    aux_v [hv, rows, dv], aux_g [hv, rows] are filled when given.  ``status``
+    (int32 [batch]) receives every request's DFT_STATUS_* bits: a packed
+    request longer than n_nodes is cut to n_nodes rows (DFT_STATUS_SPAN).
     """
     args, o, dev, _keep = _verify_args(
         y, a, b, A_log, dt_bias, state, hk=hk, hv=hv, anc=anc, anc_bits=anc_bits, batch=batch, n_nodes=n_nodes,
         cu_seqlens=cu_seqlens, scale=scale, neg_exp_A=neg_exp_A, state_indices=state_indices,
         state_slot_stride=state_slot_stride, o=o, o_dtype=o_dtype, aux_k=aux_k, aux_v=aux_v, aux_g=aux_g,
-        aux_k_per_khead=aux_k_per_khead)
+        aux_k_per_khead=aux_k_per_khead, status=status)
     check("dft_tree_verify", load().dft_tree_verify(C.byref(args), _stream(dev)))
     return o
 
 
+def _status_ptr(status, batch, dev):
+    if status is None:
+        return None
+    if status.dtype != torch.int32 or not status.is_contiguous() or status.numel() < batch:
+        raise ValueError(f"status must be a contiguous int32 tensor of at least {batch} entries")
+    if status.device != dev:
+        raise ValueError(f"status is on {status.device}, the inputs on {dev}")
+    return status.data_ptr()
+
+
 def _verify_args(y, a, b, A_log, dt_bias, state, *, hk, hv, anc, anc_bits, batch, n_nodes, cu_seqlens, scale,
-                 neg_exp_A, state_indices, state_slot_stride, o, o_dtype, aux_k, aux_v, aux_g, aux_k_per_khead):
+                 neg_exp_A, state_indices, state_slot_stride, o, o_dtype, aux_k, aux_v, aux_g, aux_k_per_khead,
+                 status=None):
     """Validate the verify operands and fill the C descriptor; returns
     (args, o, device, tensors that must outlive the launch call)."""
     dev = _device_of(y, a, b, A_log, dt_bias, state, anc, anc_bits, cu_seqlens, neg_exp_A,
@@ -120,7 +133,11 @@ def _verify_args(y, a, b, A_log, dt_bias, state, *, hk, hv, anc, anc_bits, batch
     if y.shape[1] < 2 * hk * D_HEAD + hv * D_HEAD:
         raise ValueError(f"y has {y.shape[1]} channels, need {2 * hk * D_HEAD + hv * D_HEAD}")
     if y.data_ptr() % 16 or y.stride(0) % 8:
-        y = y.contiguous()
+        # the kernels copy q/k/v rows as 16-byte pieces: a fresh buffer with
+        # the row pitch rounded up to 8 elements (a contiguous but misaligned
+        # view would stay misaligned under .contiguous())
+        pitch = -(-y.shape[1] // 8) * 8
+        y = torch.empty(rows, pitch, device=y.device, dtype=y.dtype)[:, :y.shape[1]].copy_(y)
     if cu_seqlens is not None:
         if batch is None:
             batch = cu_seqlens.numel() - 1
@@ -210,6 +227,7 @@ def _verify_args(y, a, b, A_log, dt_bias, state, *, hk, hv, anc, anc_bits, batch
     if aux_g is not None:
         _check_aux(aux_g, "aux_g", torch.float32, dims=2)
         args.aux_g, args.aux_g_h_stride, args.aux_g_row_stride = aux_g.data_ptr(), aux_g.stride(0), aux_g.stride(1)
+    args.status = _status_ptr(status, batch, dev)
     return args, o, dev, (y, cu_seqlens, anc, anc_bits, si)
 
 
@@ -225,19 +243,22 @@ def tree_commit_verify(y: torch.Tensor, a: torch.Tensor, b: torch.Tensor, A_log:
                        state_indices: Optional[torch.Tensor] = None, state_slot_stride: Optional[int] = None,
                        o: Optional[torch.Tensor] = None, o_dtype: Optional[torch.dtype] = None,
                        aux_k: Optional[torch.Tensor] = None, aux_v: Optional[torch.Tensor] = None,
-                       aux_g: Optional[torch.Tensor] = None, aux_k_per_khead: bool = False) -> torch.Tensor:
+                       aux_g: Optional[torch.Tensor] = None, aux_k_per_khead: bool = False,
+                       status: Optional[torch.Tensor] = None) -> torch.Tensor:
     """``tree_verify`` with the previous step's accepted path committed into
     each request's state slot on the way in (one read of the state, one
     write back).  The pending_* tensors are the previous step's saves
     (keys [hv or hk, rows, 128], values [hv, rows, 128], gains [hv, rows])
     and its accepted path [batch, P <= 16] (-1 padded); they must not alias
     this step's aux outputs.  Previous rows of request b start at
-    prev_cu_seqlens[b] or b * prev_n_nodes.  Returns o."""
+    prev_cu_seqlens[b] or b * prev_n_nodes.  Returns o.  ``status`` as in
+    ``tree_verify``, plus DFT_STATUS_PATH for a pending entry past the
+    previous tree (the entry is ignored)."""
     args, o, dev, _keep = _verify_args(
         y, a, b, A_log, dt_bias, state, hk=hk, hv=hv, anc=anc, anc_bits=anc_bits, batch=batch, n_nodes=n_nodes,
         cu_seqlens=cu_seqlens, scale=scale, neg_exp_A=neg_exp_A, state_indices=state_indices,
         state_slot_stride=state_slot_stride, o=o, o_dtype=o_dtype, aux_k=aux_k, aux_v=aux_v, aux_g=aux_g,
-        aux_k_per_khead=aux_k_per_khead)
+        aux_k_per_khead=aux_k_per_khead, status=status)
     _device_of(pending_path, pending_keys, pending_values, pending_gains, pending_path_len, prev_cu_seqlens, y)
     for t, nm, dims in ((pending_keys, "pending_keys", 3), (pending_values, "pending_values", 3),
                         (pending_gains, "pending_gains", 2)):
@@ -351,7 +372,7 @@ def tree_commit(src: torch.Tensor, keys: torch.Tensor, values: torch.Tensor, gai
                 anc: Optional[torch.Tensor] = None, anc_bits: Optional[torch.Tensor] = None,
                 cu_seqlens: Optional[torch.Tensor] = None, src_slots: Optional[torch.Tensor] = None,
                 dst: Optional[torch.Tensor] = None, dst_slots: Optional[torch.Tensor] = None,
-                kv_layout: bool = False, k_head_div: int = 1) -> torch.Tensor:
+                kv_layout: bool = False, k_head_div: int = 1, status: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Closed-form commit of the accepted path for every (layer, request, head).
 
     src: states [L, slots, H, rows=V, cols=K] (pool layout; ``kv_layout=True``
@@ -361,6 +382,7 @@ def tree_commit(src: torch.Tensor, keys: torch.Tensor, values: torch.Tensor, gai
     None; otherwise dst is [L, dslots, N, H, rows, cols] and receives S_u at
     node u for every end in ``ends`` [batch, E] (-1 = skip).  ``anc`` /
     ``anc_bits`` restrict the sum to ancestors of u (fc1_fused.py:41).
+    ``status`` (int32 [batch]) receives every request's DFT_STATUS_* bits.
     """
     dev = _device_of(src, keys, values, gains, path, path_len, ends, anc, anc_bits, cu_seqlens,
                      src_slots, dst, dst_slots)
@@ -381,6 +403,8 @@ def tree_commit(src: torch.Tensor, keys: torch.Tensor, values: torch.Tensor, gai
     B, P = path.shape
     if P > MAX_NODES or n_nodes > MAX_NODES:
         raise ValueError(f"paths and trees are limited to {MAX_NODES} nodes")
+    if P < 1:
+        raise ValueError("a path holds at least one entry (-1 for none)")
     a = CommitArgs()
     a.n_layers, a.batch, a.hv, a.dk, a.dv = L, B, H, D_HEAD, D_HEAD
     a.n_nodes, a.path_cols = n_nodes, P
@@ -437,6 +461,7 @@ def tree_commit(src: torch.Tensor, keys: torch.Tensor, values: torch.Tensor, gai
          a.dst_col_stride) = dst.stride()
     ds, a.dst_slots_dtype = _idx_vec(dst_slots, "dst_slots")
     a.dst_slots = _ptr(ds)
+    a.status = _status_ptr(status, B, dev)
     check("dft_tree_commit", load().dft_tree_commit(C.byref(a), _stream(dev)))
     return src if dst is None else dst
 

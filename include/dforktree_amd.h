@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define DFT_ABI_VERSION 1
+#define DFT_ABI_VERSION 2
 
 #if defined(__GNUC__)
 #define DFT_API __attribute__((visibility("default")))
@@ -58,6 +58,20 @@ enum dft_status {
 
 enum dft_dtype { DFT_F32 = 0, DFT_BF16 = 1, DFT_F16 = 2, DFT_I32 = 3, DFT_I64 = 4 };
 
+/* Per-request status words (the optional `status` arrays of dft_verify_args
+ * and dft_commit_args): every launch writes status[b] for every request b
+ * (no clearing needed), as a set of these bits; 0 = the request was taken
+ * as given. */
+enum dft_request_status {
+  /* the request's row span (cu_seqlens[b+1] - cu_seqlens[b]) is negative or
+   * exceeds n_nodes: only its first min(span, n_nodes) rows were processed,
+   * and no output row past them was written */
+  DFT_STATUS_SPAN = 1,
+  /* a path entry (within its length) or a commit end names a node at or past
+   * the size of its tree: that entry (or end) was ignored */
+  DFT_STATUS_PATH = 2
+};
+
 /* ---------------------------------------------------------------------------
  * Tree verify: one fused launch of prepare + (I+A)^-1 + finish for every
  * (request, v-head).  Node i of request b lives at row row0(b)+i of y/a/b/o,
@@ -69,7 +83,8 @@ enum dft_verify_flags {
 
 typedef struct dft_verify_args {
   int32_t batch;   /* requests */
-  int32_t n_nodes; /* nodes per request; with cu_seqlens the maximum, <= 64 */
+  int32_t n_nodes; /* nodes per request; with cu_seqlens the maximum (longer
+                      requests are cut to it: DFT_STATUS_SPAN), <= 64 */
   int32_t hk, hv;  /* q/k heads and v heads, hv % hk == 0 */
   int32_t dk, dv;  /* head dims, both 128 */
   float scale;     /* q scale (reference default dk^-0.5) */
@@ -125,6 +140,10 @@ typedef struct dft_verify_args {
   int64_t aux_v_h_stride, aux_v_row_stride;
   float* aux_g;
   int64_t aux_g_h_stride, aux_g_row_stride;
+
+  /* optional [batch] dft_request_status bits (DFT_STATUS_SPAN; with
+   * dft_tree_commit_verify also DFT_STATUS_PATH for the pending path) */
+  int32_t* status;
 } dft_verify_args;
 
 DFT_API int dft_tree_verify(const dft_verify_args* args, void* stream);
@@ -145,7 +164,7 @@ typedef struct dft_conv_args {
   const void* conv_state; /* [slot][c][col] */
   int64_t cs_slot_stride, cs_chan_stride, cs_col_stride;
   int32_t cs_dtype;
-  const void* cs_indices; /* slot per request, or NULL: slot = b */
+  const void* cs_indices; /* slot per request, or NULL: slot = b.  Negative: taps read slot 0 */
   int32_t cs_indices_dtype;
 
   const void* weight; /* [c][tap] */
@@ -165,7 +184,7 @@ typedef struct dft_conv_args {
   void* iw; /* optional [dst][n][c][col] */
   int64_t iw_slot_stride, iw_node_stride, iw_chan_stride, iw_col_stride;
   int32_t iw_dtype;
-  const void* iw_indices; /* dst per request, or NULL: dst = b */
+  const void* iw_indices; /* dst per request, or NULL: dst = b.  Negative: no window is written */
   int32_t iw_indices_dtype;
 } dft_conv_args;
 
@@ -189,8 +208,8 @@ enum dft_commit_flags {
 typedef struct dft_commit_args {
   int32_t n_layers, batch, hv;
   int32_t dk, dv;      /* both 128 */
-  int32_t n_nodes;     /* nodes per request (index bound), <= 64 */
-  int32_t path_cols;   /* entries per request in path, <= 64 */
+  int32_t n_nodes;     /* nodes per request; with cu_seqlens the maximum (index bound), <= 64 */
+  int32_t path_cols;   /* entries per request in path, 1..64 */
   int32_t n_ends;      /* 1 or 2 */
   int32_t flags;       /* dft_commit_flags */
   int32_t k_head_div;  /* aux_k head = h / k_head_div */
@@ -226,6 +245,11 @@ typedef struct dft_commit_args {
       dst_col_stride;
   const void* dst_slots; /* dst slot per request, or NULL: same as src slot.  Negative: nothing is written */
   int32_t dst_slots_dtype;
+
+  /* optional [batch] dft_request_status bits: DFT_STATUS_SPAN for a row span
+   * past n_nodes (nodes past n_nodes do not count), DFT_STATUS_PATH for a
+   * path entry or an end at or past the request's node count */
+  int32_t* status;
 } dft_commit_args;
 
 DFT_API int dft_tree_commit(const dft_commit_args* args, void* stream);

@@ -29,7 +29,7 @@ def test_library_exports_every_declared_symbol():
     out = subprocess.run(["nm", "-D", "--defined-only", str(_lib.LIB_PATH)], capture_output=True, text=True).stdout
     exported = {l.split()[-1] for l in out.splitlines() if " T " in l}
     assert exported == set(names), "only the C ABI is exported"
-    assert lib.dft_abi_version() == 1
+    assert lib.dft_abi_version() == _lib.ABI_VERSION == 2
 
 
 @pytest.fixture(scope="module")
@@ -56,7 +56,10 @@ def c_layouts(tmp_path_factory):
 
 
 def test_ctypes_structs_match_c_layout(c_layouts):
+    from dforktree_amd import _lib
     layout, structs = c_layouts
+    # the status words were appended: every earlier field kept its offset
+    assert _lib.VerifyArgs._fields_[-1][0] == "status" and _lib.CommitArgs._fields_[-1][0] == "status"
     for cname, py in structs.items():
         assert ctypes.sizeof(py) == layout[f"{cname}.__size__"], cname
         for f, _ in py._fields_:
@@ -90,6 +93,8 @@ def test_validation_rejects_bad_descriptors_without_launching():
     pc.path = pc.keys = pc.values = pc.gains = 16
     pc.path_cols = 17
     assert lib.dft_tree_commit_verify(ctypes.byref(v), ctypes.byref(pc), None) == _lib.DFT_ERR_UNSUPPORTED
+    pc.path_cols = 0  # the kernel pads from entry path_cols - 1: at least one column
+    assert lib.dft_tree_commit_verify(ctypes.byref(v), ctypes.byref(pc), None) == _lib.DFT_ERR_INVALID
     pc.path_cols, v.state_k_stride, v.state_v_stride = 16, 128, 1  # k-major state: no 16-byte rows
     assert lib.dft_tree_commit_verify(ctypes.byref(v), ctypes.byref(pc), None) == _lib.DFT_ERR_UNSUPPORTED
     v.batch = 0
@@ -100,6 +105,9 @@ def test_validation_rejects_bad_descriptors_without_launching():
     c.n_ends = 2
     c.path = c.keys = c.values = c.gains = c.src = c.dst = 16
     assert lib.dft_tree_commit(ctypes.byref(c), None) == _lib.DFT_ERR_INVALID       # 2 ends in place
+    c.n_ends, c.path_cols = 1, 0
+    assert lib.dft_tree_commit(ctypes.byref(c), None) == _lib.DFT_ERR_INVALID       # no path column
+    c.path_cols = 16
     t = _lib.TreeArgs()
     t.batch, t.n_nodes, t.kc = 1, 65, 4
     assert lib.dft_tree_struct(ctypes.byref(t), None) == _lib.DFT_ERR_INVALID

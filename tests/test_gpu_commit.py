@@ -230,3 +230,59 @@ def test_closed_commit_dropin(cuda):
     for l in range(L):
         want = O.closed_commit(np32(S[l]), np32(keys[l]), np32(vals[l]), np32(gains[l]), path.tolist())
         assert rel_l2(np32(Sg[l]), want) <= 1e-5
+
+
+def test_config4_full_size_verify_then_commit_matches_replay(cuda):
+    """The accept-and-commit workload at full size, after a real verify:
+    24 layers x 128 requests of 32-node trees at full width (16 q/k heads,
+    32 v heads, 2 MiB of fp32 state per request-layer: a 6 GiB pool).  Every
+    layer is verified on the GPU (keys saved per k-head, vn, G), then each
+    request's seeded accepted walk (length 1-16) is committed in place in
+    one launch.  At least 16 (layer, request) tiles, the first and last
+    included, must agree with an fp64 decoder that consumes only the
+    accepted tokens (rel-L2 <= 2e-3).  Every 4th request is a chain, whose
+    accepted walk is a prefix: there the replay is plain gated delta-rule
+    decoding of the first tokens.  Every committed value must be finite."""
+    import math
+    from dforktree_amd import ops, synth
+    announce("config4 full size: verify 24 x 128 x 32 heads, commit, replay")
+    L, B, HK, HV, N, D = 24, 128, 16, 32, 32, 128
+    C = 2 * HK * D + HV * D
+    rows = B * N
+    g = torch.Generator().manual_seed(80)
+    kinds = ["chain" if b % 4 == 0 else "random" for b in range(B)]
+    pars = [synth.tree_parents(N, k, g) for k in kinds]
+    parent = torch.cat(pars).to(cuda)
+    ts = ops.tree_struct(parent, 4, batch=B, n_nodes=N, want=("anc_bits",))
+    S = synth.device_randn_(torch.empty(L, B, HV, D, D, device=cuda), 81, std=0.02)  # [L, slot, H, V, K]
+    y = synth.device_randn_(torch.empty(L, rows, C, device=cuda, dtype=torch.bfloat16), 82)
+    a = synth.device_randn_(torch.empty(L, rows, HV, device=cuda), 83)
+    bb = synth.device_randn_(torch.empty(L, rows, HV, device=cuda), 84)
+    A_log = torch.full((HV,), math.log(0.5), device=cuda)
+    dt_bias = torch.zeros(HV, device=cuda)
+    keys = torch.empty(L, HK, rows, D, device=cuda)
+    vals = torch.empty(L, HV, rows, D, device=cuda)
+    gains = torch.empty(L, HV, rows, device=cuda)
+    picks = [(0, 0), (0, B - 1), (L - 1, 0), (L - 1, B - 1), (12, 4), (5, 64)]
+    pg = torch.Generator().manual_seed(85)
+    picks += [(int(torch.randint(0, L, (1,), generator=pg)), int(torch.randint(0, B, (1,), generator=pg)))
+              for _ in range(12)]
+    before = {(l, b): np32(S[l, b]) for l, b in picks}
+    for l in range(L):
+        ops.tree_verify(y[l], a[l], bb[l], A_log, dt_bias, S[l].transpose(-1, -2), hk=HK, hv=HV,
+                        anc_bits=ts["anc_bits"], batch=B, n_nodes=N, aux_k=keys[l], aux_v=vals[l], aux_g=gains[l],
+                        aux_k_per_khead=True)
+    paths, idx, lens = _paths(pars, 16, 86)
+    ops.tree_commit(S, keys, vals, gains, idx.to(cuda), n_nodes=N, path_len=lens.to(cuda), k_head_div=HV // HK)
+    torch.cuda.synchronize()
+    assert bool(torch.isfinite(S).all())
+    Al, dtb = np32(A_log), np32(dt_bias)
+    for l, b in picks:
+        sl = slice(b * N, (b + 1) * N)
+        path = paths[b].tolist()
+        if kinds[b] == "chain":
+            assert path == list(range(len(path))), "a chain's accepted walk is a prefix"
+        want = O.replay_path_f64(np32(y[l, sl]), np32(a[l, sl]), np32(bb[l, sl]), Al, dtb,
+                                 before[(l, b)].transpose(0, 2, 1), path, HK, HV, D, D)
+        err = rel_l2(np32(S[l, b]).transpose(0, 2, 1), want)
+        assert err <= REL_L2, (l, b, len(path), err)

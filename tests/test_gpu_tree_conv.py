@@ -160,3 +160,60 @@ def test_conv_general_layouts(cuda, case):
         want = O.bf16_round(ry)
         assert max_abs(np32(y[b]), want) <= MAX_ABS_BF16 and rel_l2(np32(y[b]), want) <= REL_L2
         assert np.array_equal(np32(iw[b]), O.bf16_round(rwin))
+
+
+@pytest.mark.parametrize("width", [2, 3, 5, 8])
+def test_conv_other_widths(cuda, width):
+    """The general-width conv (tree_kernels.py:17-33 takes any KC): the
+    tree's gather columns for `width` taps (tree_ops.py:81-88), through
+    ops.tree_conv over a batch (window included) and through the drop-in
+    tree_conv_fused, against the oracle."""
+    from dforktree_amd import ops, synth
+    from dforktree_amd.plugin import tree_kernels as TK
+    announce(f"conv width {width}")
+    B, N, C = 3, 32, 1024
+    g = torch.Generator().manual_seed(60 + width)
+    pars = [synth.tree_parents(N, k, g) for k in ("random", "chain", "bushy")]
+    x = torch.randn(B, N, C, generator=g).to(torch.bfloat16)
+    w = (torch.randn(C, width, generator=g) * 0.1).to(torch.bfloat16)
+    cs = torch.randn(B, C, max(width - 1, 1), generator=g).to(torch.bfloat16)
+    bias = torch.randn(C, generator=g).to(torch.bfloat16)
+    cidx = torch.stack([torch.from_numpy(O.tree_struct(p.numpy(), width)[2]) for p in pars])  # int64
+    iw = torch.zeros(B, N, C, width - 1, dtype=torch.bfloat16, device=cuda)
+    y = ops.tree_conv(x.to(cuda), cs.to(cuda), w.to(cuda), bias.to(cuda), cidx.to(cuda), iw=iw)
+    y1 = TK.tree_conv_fused(cs[0].to(cuda), x[0].to(cuda), cidx[0].to(cuda), w.to(cuda), bias.to(cuda))
+    torch.cuda.synchronize()
+    for b in range(B):
+        ry, rwin = O.tree_conv(np32(x[b]), np32(cs[b]), np32(w), np32(bias), cidx[b].numpy())
+        want = O.bf16_round(ry)
+        assert max_abs(np32(y[b]), want) <= MAX_ABS_BF16 and rel_l2(np32(y[b]), want) <= REL_L2, b
+        assert np.array_equal(np32(iw[b]), rwin), "window gathers must be bit-exact"
+        if b == 0:
+            assert max_abs(np32(y1), want) <= MAX_ABS_BF16 and rel_l2(np32(y1), want) <= REL_L2
+
+
+@pytest.mark.parametrize("layout", ["fast", "general"])
+def test_conv_negative_slots(cuda, layout):
+    """A negative conv-state slot (a padded request) reads slot 0, and a
+    negative window slot writes no window: every window slot keeps what it
+    held except the ones the valid requests own."""
+    from dforktree_amd import ops
+    announce(f"conv negative slots ({layout})")
+    B, N, C = 3, 32, 1024
+    x, w, cs, cidx = _conv_inputs(7, B, N, C, slots=3)
+    if layout == "general":
+        w = w.float()
+    slots = torch.tensor([2, -1, 0], dtype=torch.int32)
+    dsts = torch.tensor([1, -1, 2], dtype=torch.int32)
+    iw = torch.full((4, N, C, 3), 5.0, dtype=torch.bfloat16, device=cuda)
+    y = ops.tree_conv(x.to(cuda), cs.to(cuda), w.to(cuda), None, cidx.to(cuda), cs_indices=slots.to(cuda), iw=iw,
+                      iw_indices=dsts.to(cuda))
+    torch.cuda.synchronize()
+    got = np32(iw)
+    for b in range(B):
+        ry, rwin = O.tree_conv(np32(x[b]), np32(cs[max(int(slots[b]), 0)]), np32(w), None, cidx[b].numpy())
+        assert max_abs(np32(y[b]), O.bf16_round(ry)) <= MAX_ABS_BF16, b
+        if int(dsts[b]) >= 0:
+            assert np.array_equal(got[int(dsts[b])], rwin), b
+    for untouched in (0, 3):
+        assert np.all(got[untouched] == 5.0), f"window slot {untouched} was written"

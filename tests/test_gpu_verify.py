@@ -268,3 +268,81 @@ def test_verify_64_wide_output_forms(cuda, o_dtype):
     batch = synth.make_batch(19, 0, [64, 48, 33, 57], hk=2, hv=4, kinds=["random", "chain", "bushy", "random"])
     o, k, v, g = run_gpu(batch, cuda, o_dtype=o_dtype, packed=True)
     check_against_oracle(batch, o, k, v, g, o_bf16=(o_dtype == torch.bfloat16))
+
+
+def test_verify_fp16_gates_and_output(cuda):
+    """fp16 gate inputs a, b and an fp16 output o (DFT_F16 operands): the
+    oracle takes the same fp16-rounded a, b; o is compared after fp16
+    rounding of the oracle's output."""
+    from dforktree_amd import ops, synth
+    announce("verify fp16 a/b/o")
+    batch = synth.make_batch(12, 0, [32, 32], hk=2, hv=4, kinds=["random", "bushy"])
+    batch.a, batch.b = batch.a.half(), batch.b.half()
+    g = batch.to(cuda)
+    ts = ops.tree_struct(g.parent, 4, batch=2, n_nodes=32, want=("anc_bits",))
+    vn = torch.zeros(4, 64, 128, device=cuda)
+    o = ops.tree_verify(g.y, g.a, g.b, g.A_log, g.dt_bias, g.state.transpose(-1, -2), hk=2, hv=4,
+                        anc_bits=ts["anc_bits"], batch=2, n_nodes=32, o_dtype=torch.float16, aux_v=vn)
+    torch.cuda.synchronize()
+    assert o.dtype == torch.float16
+    ref = oracle_verify(batch)  # np32 of the fp16 a, b: the values the kernel reads
+    for r, sl in enumerate(request_slices(batch)):
+        want = ref[r]["o"].astype(np.float16).astype(np.float32)
+        assert rel_l2(np32(o[sl]), want) <= REL_L2 and max_abs(np32(o[sl]), want) <= MAX_ABS_BF16, r
+        assert rel_l2(np32(vn[:, sl]), ref[r]["vn"]) <= REL_L2, r
+
+
+def test_conv_then_verify_config1_chain(cuda):
+    """The full verify front end at batch 32 (32-node random trees, 16 q/k
+    heads, 32 v heads, C = 8192): the tree conv (width 4, SiLU, zero state at
+    the root, bf16 weights N(0, 0.1)) writes the y that the verify reads,
+    checked against the oracle chain O.tree_conv -> bf16 -> tree_gdn_split."""
+    from dforktree_amd import ops, synth
+    announce("conv -> verify chain, config1 (batch 32, full width)")
+    B, N, HK, HV, C = 32, 32, 16, 32, 8192
+    batch = synth.make_batch(1, 0, [N] * B, hk=HK, hv=HV)  # a, b, S0, trees; y is replaced by the conv output
+    g = torch.Generator().manual_seed(101)
+    x = torch.randn(B * N, C, generator=g).to(torch.bfloat16)
+    w = (torch.randn(C, 4, generator=g) * 0.1).to(torch.bfloat16)
+    cs = torch.zeros(B, C, 3, dtype=torch.bfloat16)
+    gb = batch.to(cuda)
+    ts = ops.tree_struct(gb.parent, 4, batch=B, n_nodes=N, want=("anc_bits", "cidx"))
+    y = ops.tree_conv(x.view(B, N, C).to(cuda), cs.to(cuda), w.to(cuda), None, ts["cidx"].view(B, N, 4))
+    o = ops.tree_verify(y.view(B * N, C), gb.a, gb.b, gb.A_log, gb.dt_bias, gb.state.transpose(-1, -2), hk=HK, hv=HV,
+                        anc_bits=ts["anc_bits"], batch=B, n_nodes=N)
+    torch.cuda.synchronize()
+    # the oracle chain
+    ys = []
+    for r, sl in enumerate(request_slices(batch)):
+        cidx = O.tree_struct(batch.parent[sl].numpy(), 4)[2]
+        ry, _ = O.tree_conv(np32(x[sl]), np32(cs[r]), np32(w), None, cidx)
+        ys.append(torch.from_numpy(O.bf16_round(ry)).to(torch.bfloat16))
+    batch.y = torch.cat(ys)
+    yd = np32(y.view(B * N, C))
+    assert max_abs(yd, np32(batch.y)) <= MAX_ABS_BF16, "conv output"
+    ref = oracle_verify(batch)
+    oh = np32(o)
+    for r, sl in enumerate(request_slices(batch)):
+        want = O.bf16_round(ref[r]["o"])
+        assert rel_l2(oh[sl], want) <= REL_L2 and max_abs(oh[sl], want) <= MAX_ABS_BF16, f"request {r}"
+
+
+def test_verify_misaligned_y_is_copied(cuda):
+    """A y view that is contiguous but not 16-byte aligned (an odd element
+    offset) is copied into an aligned buffer first: same outputs as the
+    aligned y."""
+    from dforktree_amd import ops, synth
+    announce("verify misaligned y")
+    batch = synth.make_batch(13, 0, [32, 32], hk=2, hv=4)
+    g = batch.to(cuda)
+    rows, C = g.y.shape
+    big = torch.zeros(rows * C + 1, device=cuda, dtype=torch.bfloat16)
+    ym = big[1:].view(rows, C)
+    ym.copy_(g.y)
+    assert ym.data_ptr() % 16 != 0 and ym.is_contiguous()
+    ts = ops.tree_struct(g.parent, 4, batch=2, n_nodes=32, want=("anc_bits",))
+    kw = dict(hk=2, hv=4, anc_bits=ts["anc_bits"], batch=2, n_nodes=32)
+    o1 = ops.tree_verify(ym, g.a, g.b, g.A_log, g.dt_bias, g.state.transpose(-1, -2), **kw)
+    o2 = ops.tree_verify(g.y, g.a, g.b, g.A_log, g.dt_bias, g.state.transpose(-1, -2), **kw)
+    torch.cuda.synchronize()
+    assert torch.equal(o1, o2)
