@@ -46,6 +46,9 @@ def parse():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-ragged", action="store_true", help="skip the packed ragged workload's line")
+    ap.add_argument("--no-plugin", action="store_true", help="skip the batch-1 plugin path's line")
+    ap.add_argument("--only-plugin", action="store_true", help="time the batch-1 plugin path alone")
+    ap.add_argument("--only-ragged", action="store_true", help="time the packed ragged workload alone")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--eager", action="store_true", help="time eager launches instead of a HIP graph")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -234,11 +237,128 @@ class RaggedWorkload:
                         neg_exp_A=self.neg, o=self.o[l], aux_k=self.keys[l], aux_v=self.vals[l],
                         aux_g=self.gains[l], aux_k_per_khead=True)
 
-    def bytes_per_launch(self):
-        # per request: the 2 MiB state, and per node its y row, o, vn, key (per k-head), G, a, b, ancestry word
+    def bytes_per_launch(self, lo=0, hi=64):
+        """Algorithmic bytes of the requests with lo <= nodes <= hi: per
+        request the 2 MiB state, and per node its y row, o, vn, key (per
+        k-head), G, a, b and ancestry word."""
         C = 2 * HK * D + HV * D
         node = C * 2 + HV * D * 2 + HV * D * 4 + HK * D * 4 + HV * 4 + 2 * HV * 2 + 8
-        return sum(D * D * 4 * HV + n * node for n in self.sizes)
+        return sum(D * D * 4 * HV + n * node for n in self.sizes if lo <= n <= hi)
+
+    def by_kernel(self):
+        """(requests, algorithmic bytes) of the launch's two kernels: the
+        64-wide one takes the trees of 33-64 nodes, the 32-wide one the rest."""
+        wide = [n for n in self.sizes if n > 32]
+        return {"tree_verify_kernel<64>": (len(wide), self.bytes_per_launch(33, 64)),
+                "tree_verify_kernel<32>": (self.RB - len(wide), self.bytes_per_launch(0, 32))}
+
+
+class PluginWorkload:
+    """The path the SGLang plugin drives today: batch 1 (fc1_branch64.py:13,
+    fc1_fused.py:69), one NN-node random tree per step, 24 GDN layers at full
+    width.  Per layer the hooked conv (fc1_conv.py:33-45: x [1, C, NN] as a
+    transposed view, the pool's conv state and intermediate window read
+    through device slot indices) writes the verify input, then
+    tree_gdn_split (fc1_fused.py:74) verifies on the dense fp32 CTX.anc,
+    saving keys per v-head as the reference's Context holds them.  Per step
+    the two-end snapshot commit (fc1_fused.py:77-87) writes the states at the
+    last accepted node and at a tracked earlier one into the intermediate
+    cache.  The same verify on ancestry bits (what tree_struct gives the
+    builder once per step) is timed beside it."""
+    SLOTS, ISLOTS = 4, 2
+
+    def __init__(self, dev, nn, seed=7):
+        import torch
+        from dforktree_amd import ops, synth
+        from dforktree_amd.plugin import fc1_conv, tree_kernels
+        self.nn = nn
+        C = 2 * HK * D + HV * D
+        self.x = synth.device_randn_(torch.empty(L, nn, C, device=dev, dtype=torch.bfloat16), seed)
+        self.cw = synth.device_randn_(torch.empty(C, 4, device=dev, dtype=torch.bfloat16), seed + 1, std=0.1)
+        self.conv_state = synth.device_randn_(torch.empty(L, self.SLOTS, C, 3, device=dev, dtype=torch.bfloat16),
+                                              seed + 2)
+        self.iwin = torch.zeros(L, self.ISLOTS, nn, C, 3, device=dev, dtype=torch.bfloat16)
+        self.a = synth.device_randn_(torch.empty(L, 1, nn, HV, device=dev, dtype=torch.bfloat16), seed + 3)
+        self.b = synth.device_randn_(torch.empty(L, 1, nn, HV, device=dev, dtype=torch.bfloat16), seed + 4)
+        self.A_log = torch.full((HV,), -0.6931471805599453, device=dev)
+        self.dt_bias = torch.zeros(HV, device=dev)
+        self.neg = -self.A_log.exp()
+        # SGLang's pools: temporal [L, slots, H, V, K], intermediate_ssm [L, islots, NN, H, V, K]
+        self.temporal = synth.device_randn_(torch.empty(L, self.SLOTS, HV, D, D, device=dev), seed + 5, std=0.02)
+        self.inter = torch.empty(L, self.ISLOTS, nn, HV, D, D, device=dev)
+        self.slot = torch.tensor([2], device=dev, dtype=torch.int32)
+        self.islot = torch.tensor([1], device=dev, dtype=torch.int32)
+        g = torch.Generator().manual_seed(seed)
+        parent = synth.tree_parents(nn, "random", g)
+        ts = ops.tree_struct(parent.to(dev), 4, batch=1, n_nodes=nn, want=("anc", "anc_bits", "cidx"),
+                             index_dtype=torch.int32)
+        self.anc, self.anc_bits, self.cidx = ts["anc"][0], ts["anc_bits"], ts["cidx"]
+        path = synth.accepted_path(parent, MAX_PATH, g)
+        self.accept = torch.full((1, MAX_PATH), -1, device=dev, dtype=torch.int32)
+        self.accept[0, :len(path)] = path.to(dev)
+        track = int(path[len(path) // 2])
+        self.ends = torch.tensor([[int(path[-1]), track]], device=dev, dtype=torch.int32)
+        # the reference's Context: keys per v-head (fc1_fused.py:16)
+        self.keys = torch.empty(L, HV, nn, D, device=dev)
+        self.values = torch.empty_like(self.keys)
+        self.gains = torch.empty(L, HV, nn, device=dev)
+        self.y = torch.empty(L, 1, nn, C, device=dev, dtype=torch.bfloat16)
+        self.o = torch.empty(L, nn, HV, D, device=dev, dtype=torch.bfloat16)
+        self._conv, self._tk = fc1_conv, tree_kernels
+
+    def conv(self, l):
+        x = self.x[l].t().unsqueeze(0)  # [1, C, NN], token stride C
+        self._conv.conv(x, self.conv_state[l], self.cw, None, self.cidx, self.slot, self.islot, self.iwin[l], self.y[l])
+
+    def verify_dense(self, l):
+        pool = self.temporal[l]
+        self._tk.tree_gdn_split(self.y[l, 0], self.a[l].reshape(self.nn, -1), self.b[l].reshape(self.nn, -1),
+                                self.A_log, self.dt_bias, pool[0].transpose(-1, -2), self.anc, HK, HV, D, D,
+                                aux=(self.keys[l], self.values[l], self.gains[l]), neg_exp_A=self.neg,
+                                state_indices=self.slot, state_slot_stride=pool.stride(0))
+
+    def verify_bits(self, l):
+        from dforktree_amd import ops
+        pool = self.temporal[l]
+        ops.tree_verify(self.y[l, 0], self.a[l].reshape(self.nn, -1), self.b[l].reshape(self.nn, -1), self.A_log,
+                        self.dt_bias, pool.transpose(-1, -2), hk=HK, hv=HV, anc_bits=self.anc_bits, batch=1,
+                        n_nodes=self.nn, neg_exp_A=self.neg, state_indices=self.slot, o=self.o[l],
+                        aux_k=self.keys[l], aux_v=self.values[l], aux_g=self.gains[l])
+
+    def layers(self):
+        for l in range(L):
+            self.conv(l)
+            self.verify_dense(l)
+
+    def commit(self):
+        from dforktree_amd.plugin import fc1_fused
+        fc1_fused.snapshot_commit(self.temporal, self.keys, self.values, self.gains, self.anc, self.accept, self.ends,
+                                  self.slot, self.islot, self.inter)
+
+
+def plugin_lines(dev, reps, warmup, eager):
+    """µs per layer and per step of the batch-1 plugin path at NN = 32 and 64."""
+    import torch
+    lines = {}
+    for nn in (32, 64):
+        pw = PluginWorkload(dev, nn)
+        torch.cuda.synchronize()
+        t_layers = time_graph(pw.layers, reps, warmup, eager) / L
+        t_conv = time_graph(lambda: [pw.conv(l) for l in range(L)], reps, warmup, eager) / L
+        t_dense = time_graph(lambda: [pw.verify_dense(l) for l in range(L)], reps, warmup, eager) / L
+        t_bits = time_graph(lambda: [pw.verify_bits(l) for l in range(L)], reps, warmup, eager) / L
+        t_commit = time_graph(pw.commit, reps, warmup, eager)
+        lines[f"nn{nn}"] = {"conv_plus_verify_us_per_layer": round(t_layers * 1e3, 2),
+                            "conv_us_per_layer": round(t_conv * 1e3, 2),
+                            "verify_dense_anc_us_per_layer": round(t_dense * 1e3, 2),
+                            "verify_anc_bits_us_per_layer": round(t_bits * 1e3, 2),
+                            "snapshot_commit_us_per_step": round(t_commit * 1e3, 2),
+                            "step_us": round((t_layers * L + t_commit) * 1e3, 1)}
+        del pw
+        torch.cuda.empty_cache()
+    lines["workload"] = ("batch 1, one random tree per step, 24 layers at full width: hooked conv + tree_gdn_split "
+                         "(dense CTX.anc) per layer, two-end snapshot commit per step")
+    return lines
 
 
 def time_graph(fn, reps, warmup, eager=False):
@@ -276,19 +396,36 @@ def time_graph(fn, reps, warmup, eager=False):
     return e0.elapsed_time(e1) / reps
 
 
+def _cpu_model():
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(seconds):
     """The CPU oracle on one layer of the workload (64 requests x 32 nodes,
-    verify + commit of each accepted path), repeated for ~`seconds`."""
+    verify + commit of each accepted path), repeated for ~`seconds`.  The
+    numpy BLAS gets one thread per core this process may run on (capped by
+    OMP_NUM_THREADS when the environment sets it, the CPU share of the box);
+    the trees' ancestry is built outside the timed region, as the GPU path
+    gets it from tree_struct once per step."""
     import numpy as np
     import torch
     from dforktree_amd import synth
     from oracle import gdn_tree as O
+    affinity = len(os.sched_getaffinity(0))
+    want = min(affinity, int(os.environ.get("OMP_NUM_THREADS", affinity) or affinity))
+    limiter, threads = None, None
     try:
-        from threadpoolctl import threadpool_info
-        threads = max([i.get("num_threads", 1) for i in threadpool_info() if i.get("internal_api") == "openblas"]
-                      or [1])
-    except Exception:  # threadpoolctl missing: report the env setting
-        threads = int(os.environ.get("OMP_NUM_THREADS", "1"))
+        from threadpoolctl import threadpool_info, threadpool_limits
+        limiter = threadpool_limits(limits=want, user_api="blas")
+        threads = max([i.get("num_threads", 1) for i in threadpool_info() if i.get("user_api") == "blas"] or [1])
+    except Exception:  # threadpoolctl missing: numpy's BLAS runs with what the environment gives it
+        threads = want
     bt = synth.make_batch(2, 0, [N] * B, hk=HK, hv=HV)
     y = bt.y.float().numpy().reshape(B, N, -1)
     a = bt.a.numpy().reshape(B, N, -1)
@@ -297,9 +434,9 @@ def cpu_baseline(seconds):
     par = bt.parent.numpy().reshape(B, N)
     g = torch.Generator().manual_seed(3)
     paths = [synth.accepted_path(torch.from_numpy(p), MAX_PATH, g).tolist() for p in par]
+    anc = np.stack([O.tree_struct(p)[0] for p in par])  # once per step, not per layer
 
     def layer():
-        anc = np.stack([O.tree_struct(p)[0] for p in par])
         r = O.tree_gdn_split(y, a, b, bt.A_log.numpy(), bt.dt_bias.numpy(), S0, anc, HK, HV, D, D)
         for i in range(B):
             O.closed_commit(S0[i], r["k"][i], r["vn"][i], r["G"][i], paths[i])
@@ -312,9 +449,13 @@ def cpu_baseline(seconds):
         layer()
         times.append(time.perf_counter() - t0)
     t = float(np.median(times))
+    if limiter is not None:
+        limiter.restore_original_limits()
     return {"value": B * N / t, "unit": "nodes/s/layer", "cores": threads, "kind": "port",
+            "affinity_cores": affinity, "cpu_model": _cpu_model(),
             "sample": f"{len(times)} x one layer of the workload ({B} requests x {N} nodes, verify + "
-                      f"commit of the accepted paths) through the numpy fp32 oracle, median {t * 1e3:.0f} ms"}
+                      f"commit of the accepted paths) through the numpy fp32 oracle (numpy {np.__version__}, "
+                      f"BLAS on {threads} threads), median {t * 1e3:.0f} ms"}
 
 
 def main():
@@ -326,6 +467,21 @@ def main():
         sys.exit(2)
     import torch
     dev = torch.device("cuda:0")
+    if args.only_plugin:
+        print(json.dumps({"plugin": plugin_lines(dev, max(args.steps, 10), args.warmup, args.eager)}), flush=True)
+        return
+    if args.only_ragged:
+        rw = RaggedWorkload(dev)
+        t = time_graph(lambda: [rw.verify(l) for l in range(L)], max(args.steps, 10), args.warmup, args.eager) / L
+        if args.copy_calibration:
+            src = torch.ones(1 << 28, device=dev)
+            dst = torch.empty_like(src)
+            for _ in range(3):
+                dst.copy_(src)
+            torch.cuda.synchronize()
+        print(json.dumps({"ragged_us_per_layer": round(t * 1e3, 2), "bytes_per_launch": rw.bytes_per_launch(),
+                          "kernels": rw.by_kernel()}), flush=True)
+        return
     w = Workload(dev)
     torch.cuda.synchronize()
 
@@ -355,6 +511,12 @@ def main():
                   "nodes": rw.rows, "us_per_layer": round(t_ragged * 1e3, 2),
                   "nodes_per_s_per_layer": round(rw.rows / (t_ragged * 1e-3), 1),
                   "hbm_frac": round(rw.bytes_per_launch() / (t_ragged * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+    plugin = None
+    if not args.no_plugin:
+        if not args.no_ragged:
+            del rw
+        torch.cuda.empty_cache()
+        plugin = plugin_lines(dev, reps_kernel, args.warmup, args.eager)
     if args.copy_calibration:
         src = torch.ones(1 << 28, device=dev)
         dst = torch.empty_like(src)
@@ -427,6 +589,7 @@ def main():
         "mask_pack_us": round(t_mask * 1e3, 2),
         "mask_pack_hbm_frac": frac(w.mask_bytes_per_launch(), t_mask),
         "ragged": ragged,
+        "plugin": plugin,
     }
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
