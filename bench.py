@@ -260,11 +260,12 @@ class PluginWorkload:
     transposed view, the pool's conv state and intermediate window read
     through device slot indices) writes the verify input, then
     tree_gdn_split (fc1_fused.py:74) verifies on the dense fp32 CTX.anc,
-    saving keys per v-head as the reference's Context holds them.  Per step
-    the two-end snapshot commit (fc1_fused.py:77-87) writes the states at the
-    last accepted node and at a tracked earlier one into the intermediate
-    cache.  The same verify on ancestry bits (what tree_struct gives the
-    builder once per step) is timed beside it."""
+    saving keys per v-head as the reference's Context holds them.  As the
+    verify hook does, the first layer packs the dense CTX.anc into bit rows
+    (dft_anc_pack) and every layer's verify reads those; the verify on the
+    dense matrix is timed beside it.  Per step the two-end snapshot commit
+    (fc1_fused.py:77-87) writes the states at the last accepted node and at
+    a tracked earlier one into the intermediate cache."""
     SLOTS, ISLOTS = 4, 2
 
     def __init__(self, dev, nn, seed=7):
@@ -292,7 +293,8 @@ class PluginWorkload:
         parent = synth.tree_parents(nn, "random", g)
         ts = ops.tree_struct(parent.to(dev), 4, batch=1, n_nodes=nn, want=("anc", "anc_bits", "cidx"),
                              index_dtype=torch.int32)
-        self.anc, self.anc_bits, self.cidx = ts["anc"][0], ts["anc_bits"], ts["cidx"]
+        self.anc, self.cidx = ts["anc"][0], ts["cidx"]
+        self.anc_bits = torch.zeros(nn, device=dev, dtype=torch.int64)  # the hook's CTX.anc_bits
         path = synth.accepted_path(parent, MAX_PATH, g)
         self.accept = torch.full((1, MAX_PATH), -1, device=dev, dtype=torch.int32)
         self.accept[0, :len(path)] = path.to(dev)
@@ -317,23 +319,29 @@ class PluginWorkload:
                                 aux=(self.keys[l], self.values[l], self.gains[l]), neg_exp_A=self.neg,
                                 state_indices=self.slot, state_slot_stride=pool.stride(0))
 
-    def verify_bits(self, l):
+    def pack(self):
         from dforktree_amd import ops
+        ops.anc_pack(self.anc, out=self.anc_bits)
+
+    def verify_bits(self, l):
         pool = self.temporal[l]
-        ops.tree_verify(self.y[l, 0], self.a[l].reshape(self.nn, -1), self.b[l].reshape(self.nn, -1), self.A_log,
-                        self.dt_bias, pool.transpose(-1, -2), hk=HK, hv=HV, anc_bits=self.anc_bits, batch=1,
-                        n_nodes=self.nn, neg_exp_A=self.neg, state_indices=self.slot, o=self.o[l],
-                        aux_k=self.keys[l], aux_v=self.values[l], aux_g=self.gains[l])
+        self._tk.tree_gdn_split(self.y[l, 0], self.a[l].reshape(self.nn, -1), self.b[l].reshape(self.nn, -1),
+                                self.A_log, self.dt_bias, pool[0].transpose(-1, -2), self.anc, HK, HV, D, D,
+                                aux=(self.keys[l], self.values[l], self.gains[l]), neg_exp_A=self.neg,
+                                state_indices=self.slot, state_slot_stride=pool.stride(0), anc_bits=self.anc_bits)
 
     def layers(self):
+        """What the hooks launch per forward: the pack at the first layer, then conv + verify per layer."""
         for l in range(L):
             self.conv(l)
-            self.verify_dense(l)
+            if l == 0:
+                self.pack()
+            self.verify_bits(l)
 
     def commit(self):
         from dforktree_amd.plugin import fc1_fused
         fc1_fused.snapshot_commit(self.temporal, self.keys, self.values, self.gains, self.anc, self.accept, self.ends,
-                                  self.slot, self.islot, self.inter)
+                                  self.slot, self.islot, self.inter, anc_bits=self.anc_bits)
 
 
 def plugin_lines(dev, reps, warmup, eager):
@@ -347,17 +355,19 @@ def plugin_lines(dev, reps, warmup, eager):
         t_conv = time_graph(lambda: [pw.conv(l) for l in range(L)], reps, warmup, eager) / L
         t_dense = time_graph(lambda: [pw.verify_dense(l) for l in range(L)], reps, warmup, eager) / L
         t_bits = time_graph(lambda: [pw.verify_bits(l) for l in range(L)], reps, warmup, eager) / L
+        t_pack = time_graph(lambda: [pw.pack() for _ in range(L)], reps, warmup, eager) / L
         t_commit = time_graph(pw.commit, reps, warmup, eager)
         lines[f"nn{nn}"] = {"conv_plus_verify_us_per_layer": round(t_layers * 1e3, 2),
                             "conv_us_per_layer": round(t_conv * 1e3, 2),
+                            "verify_us_per_layer": round(t_bits * 1e3, 2),
                             "verify_dense_anc_us_per_layer": round(t_dense * 1e3, 2),
-                            "verify_anc_bits_us_per_layer": round(t_bits * 1e3, 2),
+                            "anc_pack_us_per_step": round(t_pack * 1e3, 2),
                             "snapshot_commit_us_per_step": round(t_commit * 1e3, 2),
                             "step_us": round((t_layers * L + t_commit) * 1e3, 1)}
         del pw
         torch.cuda.empty_cache()
-    lines["workload"] = ("batch 1, one random tree per step, 24 layers at full width: hooked conv + tree_gdn_split "
-                         "(dense CTX.anc) per layer, two-end snapshot commit per step")
+    lines["workload"] = ("batch 1, one random tree per step, 24 layers at full width: CTX.anc packed to bit rows "
+                         "once per step, hooked conv + tree_gdn_split per layer, two-end snapshot commit per step")
     return lines
 
 

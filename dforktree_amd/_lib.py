@@ -109,6 +109,14 @@ class TreeArgs(C.Structure):
     ]
 
 
+class AncPackArgs(C.Structure):
+    _fields_ = [
+        ("batch", i32), ("n_nodes", i32),
+        ("anc", vp), ("anc_row_stride", i64), ("anc_req_stride", i64),
+        ("anc_bits", vp),
+    ]
+
+
 class PackbitsArgs(C.Structure):
     _fields_ = [
         ("n_segments", i32), ("bit_order", i32),
@@ -135,7 +143,8 @@ class MaskArgs(C.Structure):
 DFT_BITS_LITTLE, DFT_BITS_BIG = 0, 1
 
 EXPORTS = ("dft_tree_verify", "dft_tree_commit_verify", "dft_tree_conv", "dft_tree_commit", "dft_tree_struct",
-           "dft_block_inverse", "dft_packbits", "dft_tree_mask_pack", "dft_error_string", "dft_abi_version")
+           "dft_anc_pack", "dft_block_inverse", "dft_packbits", "dft_tree_mask_pack", "dft_error_string",
+           "dft_abi_version")
 
 
 class LibraryMissing(RuntimeError):
@@ -165,6 +174,7 @@ def load() -> C.CDLL:
                        ("dft_tree_conv", [C.POINTER(ConvArgs), vp]),
                        ("dft_tree_commit", [C.POINTER(CommitArgs), vp]),
                        ("dft_tree_struct", [C.POINTER(TreeArgs), vp]),
+                       ("dft_anc_pack", [C.POINTER(AncPackArgs), vp]),
                        ("dft_packbits", [C.POINTER(PackbitsArgs), vp]),
                        ("dft_tree_mask_pack", [C.POINTER(MaskArgs), vp]),
                        ("dft_block_inverse", [vp, i32, i32, i64, vp])):

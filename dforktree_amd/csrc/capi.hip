@@ -11,6 +11,7 @@ int launch_block_inverse(float* x, int n_mats, int n, int64_t mat_stride, hipStr
 int launch_tree_conv(const dft_conv_args* a, hipStream_t stream);
 int launch_tree_commit(const dft_commit_args* a, hipStream_t stream);
 int launch_tree_struct(const dft_tree_args* a, hipStream_t stream);
+int launch_anc_pack(const dft_anc_pack_args* a, hipStream_t stream);
 int launch_packbits(const dft_packbits_args* a, hipStream_t stream);
 int launch_tree_mask(const dft_mask_args* a, hipStream_t stream);
 }  // namespace dft
@@ -149,6 +150,15 @@ int dft_tree_struct(const dft_tree_args* a, void* stream) {
   if (a->cidx && (!index_tag(a->cidx_dtype) || a->kc < 1)) return DFT_ERR_INVALID;
   if ((a->nxt || a->sib) && !index_tag(a->link_dtype)) return DFT_ERR_INVALID;
   return dft::launch_tree_struct(a, static_cast<hipStream_t>(stream));
+}
+
+int dft_anc_pack(const dft_anc_pack_args* a, void* stream) {
+  if (!a) return DFT_ERR_INVALID;
+  if (a->batch < 0 || a->n_nodes < 0 || a->n_nodes > 64) return DFT_ERR_INVALID;
+  if (a->batch == 0 || a->n_nodes == 0) return DFT_OK;
+  if (((int64_t)a->batch + 3) / 4 > max_blocks(256)) return DFT_ERR_UNSUPPORTED;  // a wave per request
+  if (!a->anc || !a->anc_bits) return DFT_ERR_INVALID;
+  return dft::launch_anc_pack(a, static_cast<hipStream_t>(stream));
 }
 
 int dft_packbits(const dft_packbits_args* a, void* stream) {

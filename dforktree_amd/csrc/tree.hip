@@ -101,6 +101,35 @@ __global__ void __launch_bounds__(256) tree_struct_kernel(const dft_tree_args p)
   }
 }
 
+// Dense 0/1 ancestry rows -> the uint64 rows the verify and commit read.
+// One wave per request: lane j loads column j of every row first (coalesced
+// rows, all loads in flight at once), then the wave's ballot of each row is
+// that row's mask; bits above the diagonal are dropped, as the kernels that
+// read dense rows drop them.  Lane i keeps row i and writes it at the end.
+__global__ void __launch_bounds__(256) anc_pack_kernel(const dft_anc_pack_args p) {
+  const int lane = threadIdx.x & 63;
+  const int b = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (b >= p.batch) return;  // no barrier in this kernel
+  const int n = p.n_nodes;
+  const float* base = p.anc + (int64_t)b * p.anc_req_stride + (lane < n ? lane : 0);
+  float v[64];
+#pragma unroll
+  for (int i = 0; i < 64; ++i) v[i] = (i < n && lane < n) ? base[(int64_t)i * p.anc_row_stride] : 0.f;
+  uint64_t mine = 0;
+#pragma unroll
+  for (int i = 0; i < 64; ++i) {
+    const uint64_t row = __ballot(v[i] > 0.5f) & mask_upto(i);
+    if (lane == i) mine = row;
+  }
+  if (lane < n) p.anc_bits[(int64_t)b * n + lane] = mine;
+}
+
+int launch_anc_pack(const dft_anc_pack_args* a, hipStream_t stream) {
+  const dim3 grid((unsigned)((a->batch + 3) / 4));
+  hipLaunchKernelGGL(anc_pack_kernel, grid, dim3(256), 0, stream, *a);
+  return hipGetLastError() == hipSuccess ? DFT_OK : DFT_ERR_LAUNCH;
+}
+
 int launch_tree_struct(const dft_tree_args* a, hipStream_t stream) {
   const dim3 grid((unsigned)((a->batch + 3) / 4));
   hipLaunchKernelGGL(tree_struct_kernel, grid, dim3(256), 0, stream, *a);

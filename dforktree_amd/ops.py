@@ -19,8 +19,8 @@ from typing import Optional
 import torch
 
 from . import _lib
-from ._lib import (DFT_BF16, DFT_BITS_BIG, DFT_BITS_LITTLE, DFT_F16, DFT_F32, DFT_I32, DFT_I64, CommitArgs,
-                   ConvArgs, MaskArgs, PackbitsArgs, PendingArgs, TreeArgs, VerifyArgs, check, load)
+from ._lib import (DFT_BF16, DFT_BITS_BIG, DFT_BITS_LITTLE, DFT_F16, DFT_F32, DFT_I32, DFT_I64, AncPackArgs,
+                   CommitArgs, ConvArgs, MaskArgs, PackbitsArgs, PendingArgs, TreeArgs, VerifyArgs, check, load)
 
 _FLOAT_TAG = {torch.float32: DFT_F32, torch.bfloat16: DFT_BF16, torch.float16: DFT_F16}
 _INDEX_TAG = {torch.int32: DFT_I32, torch.int64: DFT_I64}
@@ -523,6 +523,30 @@ def tree_struct(parent: torch.Tensor, kc: int = 4, *, batch: Optional[int] = Non
         out["status"] = torch.empty(batch, device=dev, dtype=torch.int32)
         a.status = out["status"].data_ptr()
     check("dft_tree_struct", load().dft_tree_struct(C.byref(a), _stream(dev)))
+    return out
+
+
+def anc_pack(anc: torch.Tensor, *, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Dense 0/1 ancestry [N, N] or [batch, N, N] (any float dtype cast to
+    fp32 first) -> int64 bit rows [batch * N]: bit j of row i = anc[i][j] >
+    0.5 for j <= i.  With `out` nothing is allocated (for a fp32 input with
+    unit column stride)."""
+    dev = _device_of(anc, out)
+    a3 = anc if anc.dim() == 3 else anc.unsqueeze(0)
+    if a3.dim() != 3 or a3.shape[1] != a3.shape[2] or a3.shape[1] > MAX_NODES:
+        raise ValueError(f"anc must be [N, N] or [batch, N, N] with N <= {MAX_NODES}")
+    if a3.dtype != torch.float32 or a3.stride(2) != 1:
+        a3 = a3.float().contiguous()
+    B, n = a3.shape[0], a3.shape[1]
+    if out is None:
+        out = torch.empty(B * n, device=dev, dtype=torch.int64)
+    if out.dtype != torch.int64 or not out.is_contiguous() or out.numel() < B * n:
+        raise ValueError(f"out must be a contiguous int64 tensor of at least {B * n} entries")
+    a = AncPackArgs()
+    a.batch, a.n_nodes = B, n
+    a.anc, a.anc_row_stride, a.anc_req_stride = a3.data_ptr(), a3.stride(1), a3.stride(0)
+    a.anc_bits = out.data_ptr()
+    check("dft_anc_pack", load().dft_anc_pack(C.byref(a), _stream(dev)))
     return out
 
 

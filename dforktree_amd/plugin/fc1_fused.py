@@ -5,7 +5,10 @@ Keeps the reference's module surface -- ``NN``, ``BS``, ``Context``, ``CTX``,
 and routes the three hooked SGLang entry points to the gfx950 library:
 
 * ``TritonGDNKernel.target_verify``  -> ``tree_kernels.tree_gdn_split`` on the
-  conv output stashed in ``CTX.current_mixed`` (fc1_fused.py:59-75);
+  conv output stashed in ``CTX.current_mixed`` (fc1_fused.py:59-75); the
+  first GDN layer of each forward packs ``CTX.anc`` into bit rows
+  (``CTX.anc_bits``, one ``dft_anc_pack`` launch), which every layer's
+  verify and the commit read instead of the dense matrix;
 * ``commit_mamba_states_after_verify`` -> the snapshot commit into
   ``intermediate_ssm`` at the last / tracked accepted node, then SGLang's own
   commit copies it to the live state (fc1_fused.py:77-87);
@@ -57,6 +60,8 @@ class Context:
 
     def __init__(self, device='cuda'):
         self.anc = torch.eye(NN, device=device, dtype=torch.float32)
+        # anc packed to bit rows, once per forward by the first layer's verify
+        self.anc_bits = torch.zeros(NN, device=device, dtype=torch.int64)
         self.keys = torch.empty(N_LAYERS, N_HEADS, NN, D_HEAD, device=device)
         self.values = torch.empty_like(self.keys)
         self.gains = torch.empty(N_LAYERS, N_HEADS, NN, device=device)
@@ -81,18 +86,20 @@ LAYER_STATS = []
 
 
 def snapshot_commit(temporal, keys, values, gains, anc, accept_index, ends, slots, inter_indices,
-                    intermediate_ssm):
+                    intermediate_ssm, anc_bits=None):
     """fc1_fused.py:26-49 for every (layer, head, end):
     intermediate_ssm[l, dst, u, h] = e^{G_u} S + sum_t on_t e^{G_u-G_t} k_t vn_t^T,
     on_t = path node t is an ancestor-or-self of u; u in ``ends`` (-1 = skip).
     temporal [L, slots, H, V, K]; keys/values [>=L, H, NN, 128];
-    accept_index [batch, P] (-1 padded); ends [batch*E] or [batch, E]."""
+    accept_index [batch, P] (-1 padded); ends [batch*E] or [batch, E].
+    ``anc_bits`` (anc packed to rows) replaces the dense anc when given."""
     L = temporal.shape[0]
     Bq = accept_index.shape[0] if accept_index.dim() == 2 else 1
     n = anc.shape[-1]
+    tree = dict(anc=anc) if anc_bits is None else dict(anc_bits=anc_bits)
     _ops.tree_commit(temporal, keys[:L], values[:L], gains[:L], accept_index.reshape(Bq, -1), n_nodes=n,
-                     ends=ends.reshape(Bq, -1), anc=anc, src_slots=slots, dst=intermediate_ssm,
-                     dst_slots=inter_indices)
+                     ends=ends.reshape(Bq, -1), src_slots=slots, dst=intermediate_ssm, dst_slots=inter_indices,
+                     **tree)
 
 
 class _Snapshots:
@@ -162,10 +169,13 @@ def install():
             return original_verify(self, A_log, dt_bias, q, k, v, a, b, **kw)
         pool = kw['ssm_states']
         try:
+            if li == 0:  # the first GDN layer of a forward: CTX.anc is this step's tree (fc1_branch64.py:29)
+                _ops.anc_pack(ctx.anc, out=ctx.anc_bits)
             out = TK.tree_gdn_split(y, a.reshape(NN, -1), b.reshape(NN, -1), A_log, dt_bias,
                                     pool[0].transpose(-1, -2), ctx.anc, q.shape[2], v.shape[2], q.shape[3],
                                     v.shape[3], aux=(ctx.keys[li], ctx.values[li], ctx.gains[li]), neg_exp_A=neg,
-                                    state_indices=kw['cache_indices'], state_slot_stride=pool.stride(0))
+                                    state_indices=kw['cache_indices'], state_slot_stride=pool.stride(0),
+                                    anc_bits=ctx.anc_bits)
         except _lib.DftError as err:
             if not refused(err):
                 raise
@@ -189,7 +199,7 @@ def install():
             for l0, l1 in layer_runs(CTX.saved):
                 snapshot_commit(state.temporal[l0:l1], CTX.keys[l0:l1], CTX.values[l0:l1], CTX.gains[l0:l1],
                                 CTX.anc, accept_index, ends, slots, CTX.inter_indices,
-                                state.intermediate_ssm[l0:l1])
+                                state.intermediate_ssm[l0:l1], anc_bits=CTX.anc_bits)
         return original_commit(target_worker, batch, accept_lens, accept_index, draft_token_num, prepared_step_indices)
 
     def direct_routing(self, **kwargs):

@@ -78,26 +78,31 @@ def closed_commit(states, keys, values, gains, src, n):
 
 
 def tree_gdn_split(y, aa0, bb0, A_log, dt_bias, S0, Anc, Hk, Hv, Dk, Dv, scale=None, BV=64, num_warps=8, aux=None,
-                   neg_exp_A=None, state_indices=None, state_slot_stride=0):
+                   neg_exp_A=None, state_indices=None, state_slot_stride=0, anc_bits=None):
     """tree_kernels.py:193-208: the verify entry the SGLang hook calls
     (fc1_fused.py:74).  Returns o [N, Hv, Dv] in y.dtype; with
     aux=(k [Hv,N,Dk], vn [Hv,N,Dv], G [Hv,N]) also saves the commit inputs.
     S0 is the [Hv, Dk, Dv] view of slot 0; the slot max(state_indices[0], 0)
-    is read on the device and offset by state_slot_stride."""
+    is read on the device and offset by state_slot_stride.  ``anc_bits``
+    (an extension: Anc packed to int64 rows by ``ops.anc_pack``) replaces
+    the dense Anc when given."""
     N = y.shape[0]
     BN = _pow2(N)
     assert BN <= 64 and Dv % BV == 0
     if N not in (16, 32, 64):
         raise KeyError(N)  # the reference dispatches invert{16,32,64} by N (:206)
     o = torch.empty(N, Hv, Dv, device=y.device, dtype=y.dtype)
-    _verify(y, aa0, bb0, A_log, dt_bias, S0, Anc, Hk, Hv, scale, aux, neg_exp_A, state_indices, state_slot_stride, o)
+    _verify(y, aa0, bb0, A_log, dt_bias, S0, Anc, Hk, Hv, scale, aux, neg_exp_A, state_indices, state_slot_stride, o,
+            anc_bits)
     return o
 
 
-def _verify(y, aa0, bb0, A_log, dt_bias, S0, Anc, Hk, Hv, scale, aux, neg_exp_A, state_indices, slot_stride, o):
+def _verify(y, aa0, bb0, A_log, dt_bias, S0, Anc, Hk, Hv, scale, aux, neg_exp_A, state_indices, slot_stride, o,
+            anc_bits=None):
     N = y.shape[0]
     k, vn, G = aux if aux is not None else (None, None, None)
-    _ops.tree_verify(y, aa0.reshape(N, -1), bb0.reshape(N, -1), A_log, dt_bias, S0, hk=Hk, hv=Hv, anc=Anc,
-                     batch=1, n_nodes=N, scale=scale, neg_exp_A=neg_exp_A, state_indices=state_indices,
+    tree = dict(anc=Anc) if anc_bits is None else dict(anc_bits=anc_bits)
+    _ops.tree_verify(y, aa0.reshape(N, -1), bb0.reshape(N, -1), A_log, dt_bias, S0, hk=Hk, hv=Hv, batch=1, n_nodes=N,
+                     scale=scale, neg_exp_A=neg_exp_A, state_indices=state_indices,
                      state_slot_stride=slot_stride if state_indices is not None else 0, o=o,
-                     aux_k=k, aux_v=vn, aux_g=G)
+                     aux_k=k, aux_v=vn, aux_g=G, **tree)

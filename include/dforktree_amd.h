@@ -319,6 +319,23 @@ typedef struct dft_tree_args {
 DFT_API int dft_tree_struct(const dft_tree_args* args, void* stream);
 
 /* ---------------------------------------------------------------------------
+ * Dense ancestry to bit rows: anc_bits[b*n_nodes + i] bit j = (anc[b][i][j]
+ * > 0.5) for j <= i (bits above the diagonal are dropped), n_nodes <= 64.
+ * No counterpart in the reference: the plugin keeps each tree's ancestry as
+ * the dense fp32 matrix that fc1_branch64.py:29 copies into
+ * fc1_fused.CTX.anc once per step; packing it once lets every layer's
+ * verify read 8 bytes per node instead of a dense row.
+ * ------------------------------------------------------------------------- */
+typedef struct dft_anc_pack_args {
+  int32_t batch, n_nodes;
+  const float* anc; /* [b][i][j], column stride 1 */
+  int64_t anc_row_stride, anc_req_stride;
+  uint64_t* anc_bits; /* [batch * n_nodes] */
+} dft_anc_pack_args;
+
+DFT_API int dft_anc_pack(const dft_anc_pack_args* args, void* stream);
+
+/* ---------------------------------------------------------------------------
  * Bit-packed attention masks (numpy.packbits semantics).
  *
  * A segment of `bits` elements becomes ceil(bits / 8) bytes: element 8j + k

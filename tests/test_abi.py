@@ -37,7 +37,8 @@ def c_layouts(tmp_path_factory):
     from dforktree_amd import _lib
     structs = {"dft_verify_args": _lib.VerifyArgs, "dft_pending_commit": _lib.PendingArgs, "dft_conv_args": _lib.ConvArgs,
                "dft_commit_args": _lib.CommitArgs, "dft_tree_args": _lib.TreeArgs,
-               "dft_packbits_args": _lib.PackbitsArgs, "dft_mask_args": _lib.MaskArgs}
+               "dft_packbits_args": _lib.PackbitsArgs, "dft_mask_args": _lib.MaskArgs,
+               "dft_anc_pack_args": _lib.AncPackArgs}
     lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"', "int main(void) {",
              'printf("{");']
     first = True
@@ -111,6 +112,13 @@ def test_validation_rejects_bad_descriptors_without_launching():
     t = _lib.TreeArgs()
     t.batch, t.n_nodes, t.kc = 1, 65, 4
     assert lib.dft_tree_struct(ctypes.byref(t), None) == _lib.DFT_ERR_INVALID
+    ap = _lib.AncPackArgs()
+    ap.batch, ap.n_nodes = 1, 65
+    assert lib.dft_anc_pack(ctypes.byref(ap), None) == _lib.DFT_ERR_INVALID         # > 64 nodes
+    ap.n_nodes = 32
+    assert lib.dft_anc_pack(ctypes.byref(ap), None) == _lib.DFT_ERR_INVALID         # null pointers
+    ap.batch = 0
+    assert lib.dft_anc_pack(ctypes.byref(ap), None) == _lib.DFT_OK                  # empty: no-op
     k = _lib.ConvArgs()
     k.batch, k.n_nodes, k.channels, k.width = 1, 4, 8, 9
     assert lib.dft_tree_conv(ctypes.byref(k), None) == _lib.DFT_ERR_UNSUPPORTED

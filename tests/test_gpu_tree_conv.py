@@ -217,3 +217,21 @@ def test_conv_negative_slots(cuda, layout):
             assert np.array_equal(got[int(dsts[b])], rwin), b
     for untouched in (0, 3):
         assert np.all(got[untouched] == 5.0), f"window slot {untouched} was written"
+
+
+@pytest.mark.parametrize("n", [1, 20, 32, 64])
+def test_anc_pack_matches_oracle_bits(cuda, n):
+    """dft_anc_pack: the dense ancestry (as tree_struct / the builder give it)
+    packed into bit rows, bit-exact against the oracle's rows (bit 63 is the
+    sign bit of the int64 row at n = 64); a batch of three trees at once."""
+    from dforktree_amd import ops, synth
+    announce(f"anc_pack n={n}")
+    g = torch.Generator().manual_seed(90 + n)
+    pars = [synth.tree_parents(n, k, g) for k in ("random", "chain", "bushy")]
+    dense = np.stack([O.tree_struct(p.numpy())[0] for p in pars]).astype(np.float32)
+    want = np.concatenate([O.anc_bits(d) for d in dense]).view(np.int64)
+    got = ops.anc_pack(torch.from_numpy(dense).to(cuda))
+    one = ops.anc_pack(torch.from_numpy(dense[1]).to(cuda))
+    torch.cuda.synchronize()
+    assert np.array_equal(got.cpu().numpy(), want)
+    assert np.array_equal(one.cpu().numpy(), want[n:2 * n])

@@ -22,6 +22,9 @@ def hooked(monkeypatch):
     mods, calls, saved = install_fakes(step_indices)
     monkeypatch.setattr(F, "CTX", F.Context(device="cpu"))
     monkeypatch.setattr(F, "NATIVE_REFERENCE", False)
+    packed = []  # the hook's dft_anc_pack launches, recorded (no device here)
+    monkeypatch.setattr(F._ops, "anc_pack", lambda anc, out=None: packed.append((anc, out)) or out)
+    F.packed = packed
     F.install()
     fc1_conv.install()
     yield F, fc1_conv, mods, calls
@@ -63,6 +66,9 @@ def test_verify_hook_routes_tree_verifies_to_split(hooked, monkeypatch):
     assert aa.shape == (F.NN, 32) and (Hk, Hv, Dk, Dv) == (16, 32, 128, 128)
     assert S0.shape == (32, 128, 128) and S0.stride() == pool[0].transpose(-1, -2).stride()
     assert kw["state_indices"] is slots and kw["state_slot_stride"] == pool.stride(0)
+    # layer 0 packs this step's CTX.anc into bit rows, which the verify reads
+    assert kw["anc_bits"] is F.CTX.anc_bits
+    assert len(F.packed) == 1 and F.packed[0][0] is F.CTX.anc and F.packed[0][1] is F.CTX.anc_bits
     assert torch.allclose(kw["neg_exp_A"], -A_log.exp())
     keys, vals, gains = kw["aux"]
     assert keys.data_ptr() == F.CTX.keys[0].data_ptr() and gains.data_ptr() == F.CTX.gains[0].data_ptr()
@@ -75,6 +81,7 @@ def test_verify_hook_routes_tree_verifies_to_split(hooked, monkeypatch):
                           intermediate_state_indices=islots)
     assert [s[1]["aux"][0].data_ptr() for s in seen] == [F.CTX.keys[i].data_ptr() for i in (0, 1, 0)]
     assert calls.names() == [] and F.CTX.saved == {0, 1}
+    assert len(F.packed) == 2, "packed once per forward: at layer 0 only"
 
 
 def test_verify_hook_falls_back_for_other_step_counts(hooked):
@@ -107,7 +114,7 @@ def _worker(temporal, inter, slots):
 def test_commit_hook_snapshots_both_ends_then_calls_original(hooked, monkeypatch, track):
     F, _, mods, calls = hooked
     seen = []
-    monkeypatch.setattr(F, "snapshot_commit", lambda *args: seen.append(args))
+    monkeypatch.setattr(F, "snapshot_commit", lambda *args, **kw: seen.append(args + (kw,)))
     commit = mods["sglang.srt.speculative.eagle_worker_common"].commit_mamba_states_after_verify
     temporal, inter, slots = torch.zeros(2, 3, 4, 1, 1), torch.zeros(2, 2, F.NN, 4, 1, 1), torch.tensor([2])
     F.CTX.inter_indices = torch.tensor([1])
@@ -119,7 +126,8 @@ def test_commit_hook_snapshots_both_ends_then_calls_original(hooked, monkeypatch
     assert out == "original_commit"
     assert calls.names() == ["step_indices", "original_commit"]
     (args,), = [seen]
-    S, keys, vals, gains, anc, acc, ends, sl, isl, dst = args
+    S, keys, vals, gains, anc, acc, ends, sl, isl, dst, kw = args
+    assert kw["anc_bits"] is F.CTX.anc_bits
     assert S.data_ptr() == temporal.data_ptr() and S.shape == temporal.shape
     assert dst.data_ptr() == inter.data_ptr() and dst.shape == inter.shape
     assert sl is slots and isl is F.CTX.inter_indices
@@ -130,7 +138,7 @@ def test_commit_hook_snapshots_both_ends_then_calls_original(hooked, monkeypatch
 
 def test_commit_hook_skips_other_draft_sizes(hooked, monkeypatch):
     F, _, mods, calls = hooked
-    monkeypatch.setattr(F, "snapshot_commit", lambda *args: pytest.fail("must not commit"))
+    monkeypatch.setattr(F, "snapshot_commit", lambda *args, **kw: pytest.fail("must not commit"))
     commit = mods["sglang.srt.speculative.eagle_worker_common"].commit_mamba_states_after_verify
     batch = types.SimpleNamespace(req_pool_indices=torch.tensor([0]))
     assert commit(None, batch, torch.tensor([1]), torch.tensor([[0]]), F.NN - 1) == "original_commit"
@@ -200,7 +208,7 @@ def test_refused_verify_falls_back_and_is_not_committed(hooked, monkeypatch):
     with pytest.raises(_lib.DftError):
         K().target_verify(A_log, dt_bias, q, k, v, a, b, **kw)
     # no layer was verified here: the commit launches nothing and calls SGLang's commit
-    monkeypatch.setattr(F, "snapshot_commit", lambda *args: pytest.fail("must not commit"))
+    monkeypatch.setattr(F, "snapshot_commit", lambda *args, **kw: pytest.fail("must not commit"))
     commit = mods["sglang.srt.speculative.eagle_worker_common"].commit_mamba_states_after_verify
     batch = types.SimpleNamespace(req_pool_indices=torch.tensor([0]))
     assert commit(None, batch, torch.tensor([1]), torch.tensor([[0]]), F.NN) == "original_commit"
@@ -244,7 +252,7 @@ def test_commit_covers_only_layers_verified_here(hooked, monkeypatch):
     from dforktree_amd import _lib
     F, _, mods, calls = hooked
     seen = []
-    monkeypatch.setattr(F, "snapshot_commit", lambda *args: seen.append(args))
+    monkeypatch.setattr(F, "snapshot_commit", lambda *args, **kw: seen.append(args + (kw,)))
     commit = mods["sglang.srt.speculative.eagle_worker_common"].commit_mamba_states_after_verify
     L = 6
     temporal, inter = torch.zeros(L, 3, 4, 1, 1), torch.zeros(L, 2, F.NN, 4, 1, 1)
