@@ -233,6 +233,7 @@ struct VerifySmem : VRegion<NP, (NP > 32)> {
 };
 static_assert(sizeof(VerifySmem<64>) <= 80 * 1024, "two 64-wide workgroups per CU");
 static_assert(2 * 32 * 36 >= 16 * kD && 2 * 64 * 68 >= 16 * kD, "am + x hold the 16 staged path keys");
+static_assert(2 * 32 * 36 >= 4 * 512, "am + x hold the four waves' 2 KiB write-back staging buffers");
 
 __device__ __forceinline__ f32x4 mfma_bf16_16x16x32(bf16x8 a, bf16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
@@ -497,14 +498,40 @@ __device__ __forceinline__ void issue_state_group(const float* S0, int64_t v_str
   }
 }
 
-// the committed tile goes back where it was read (16-byte stores)
-__device__ __forceinline__ void store_state(float* S, int64_t v_stride, int wave, int lane, const f32x4 (&s0r)[2][8]) {
+// The committed tile goes back where it was read, as whole 128-byte lines.
+// In the MFMA layout a lane group holds 64 bytes of each of 16 rows, so a
+// direct store writes half lines; non-temporal half lines reach memory
+// unmerged, and ordinary stores are slower still (fused kernel at batch 64:
+// 81.2 us with half-line non-temporal stores, 84.8 with ordinary ones).  So
+// each 16-row x 32-column piece (registers j = 2s, 2s + 1 of tile t) goes
+// through the wave's own 2 KiB of LDS, `stage`, and comes back as 8 lanes
+// per 128-byte row.  The piece's rows are 32 floats, so 16-byte chunk c of
+// row r sits at chunk c ^ (r & 7): the writes (8 lanes = 8 rows at one
+// chunk) and the read-backs (8 lanes = 8 chunks of one row) then hit 32
+// distinct banks.  A wave's LDS operations run in order, so the buffer is
+// reused piece after piece without waits.
+__device__ __forceinline__ void store_state(float* S, int64_t v_stride, int wave, int lane, const f32x4 (&s0r)[2][8],
+                                            float* stage) {
   const int n16 = lane & 15, g4 = lane >> 4;
+  const int r8 = lane >> 3, c8 = lane & 7;
+  const int64_t step8 = 8 * v_stride;
+  f32x4* st = reinterpret_cast<f32x4*>(stage);  // 8 chunks of 16 bytes per row
+  f32x4* w0 = st + 8 * n16 + (g4 ^ (n16 & 7));
+  f32x4* w1 = st + 8 * n16 + ((4 + g4) ^ (n16 & 7));
+  const f32x4* rd = st + 8 * r8 + (c8 ^ r8);  // rows r8 and 8 + r8 share the swizzle
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
-    float* rowp = S + (int64_t)(32 * wave + 16 * t + n16) * v_stride + 4 * g4;
+    float* r0 = S + (int64_t)(32 * wave + 16 * t + r8) * v_stride + 4 * c8;  // rows r8 and 8 + r8 of the tile
+    float* r1 = r0 + step8;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) __builtin_nontemporal_store(s0r[t][j], reinterpret_cast<f32x4*>(rowp + 16 * j));
+    for (int s = 0; s < 4; ++s) {
+      // row n16 of the piece (tile t, columns 32 s ..): columns 4 g4 .. and 16 + 4 g4 ..
+      *w0 = s0r[t][2 * s];
+      *w1 = s0r[t][2 * s + 1];
+      const f32x4 v0 = rd[0], v1 = rd[64];
+      __builtin_nontemporal_store(v0, reinterpret_cast<f32x4*>(r0 + 32 * s));
+      __builtin_nontemporal_store(v1, reinterpret_cast<f32x4*>(r1 + 32 * s));
+    }
   }
 }
 
@@ -1145,7 +1172,8 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
       issue_state<true>(S0, p.state_v_stride, wave, lane, s0r);
       issue_pending(P.c, pd, it.h, wave, lane, S0, kr, vnr, gp);
       commit_tile(pd, sm.pkey(), kr, vnr, gp, wave, lane, s0r);
-      store_state(const_cast<float*>(S0), p.state_v_stride, wave, lane, s0r);
+      __syncthreads();  // every wave has read the staged keys: am + x take the write-back staging
+      store_state(const_cast<float*>(S0), p.state_v_stride, wave, lane, s0r, sm.amx + wave * 512);
       return;
     }
   }
@@ -1218,8 +1246,11 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
     // everything this wave loaded has been consumed: no load is left in
     // flight past the (conditional) write-back
     __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 15));
-    if (pd.last >= 0) store_state(const_cast<float*>(S0), p.state_v_stride, wave, lane, s0r);
-    __syncthreads();  // every wave has read its keys: am and x take the Gram tiles and X
+    if (pd.last >= 0) {  // uniform over the workgroup (one request)
+      __syncthreads();  // every wave has read the staged keys: am + x take the write-back staging
+      store_state(const_cast<float*>(S0), p.state_v_stride, wave, lane, s0r, sm.amx + wave * 512);
+    }
+    __syncthreads();  // am and x take the Gram tiles and X
   }
   if constexpr (kSplit) issue_state_group<false>(S0, p.state_v_stride, wave, lane, 1, s0r);
   phase_saves<NP, COMMIT>(P, it, tid, sm, sm);
