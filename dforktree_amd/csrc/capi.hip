@@ -45,7 +45,8 @@ int verify_status(const dft_verify_args* a) {
   if (a->state_indices && !index_tag(a->state_indices_dtype)) return DFT_ERR_INVALID;
   // q/k/v rows are copied as 16-byte pieces
   if (!aligned16(a->y) || a->y_row_stride % 8 != 0) return DFT_ERR_INVALID;
-  if ((int64_t)a->batch * a->hv > max_blocks(256)) return DFT_ERR_UNSUPPORTED;
+  // one workgroup per (request, v-head): 4 waves for trees of up to 32 nodes, 8 beyond
+  if ((int64_t)a->batch * a->hv > max_blocks(a->n_nodes > 32 ? 512 : 256)) return DFT_ERR_UNSUPPORTED;
   return DFT_OK;
 }
 

@@ -41,6 +41,18 @@
 namespace dft {
 
 constexpr int kD = 128;
+
+// Waves per workgroup: 4 for trees of up to 32 nodes, 8 for 33-64 (WavesFor).
+// Wave w owns value columns CW w .. CW w + CW - 1 (CW = 128 / NW), as TT = CW / 16
+// MFMA column tiles; phase 1 spreads its tiles and blocks over all NW waves.
+template <int NW>
+struct Waves {
+  static constexpr int NT = 64 * NW;  // threads
+  static constexpr int CW = kD / NW;  // value columns per wave
+  static constexpr int TT = CW / 16;  // 16-column tiles per wave
+};
+template <int NP>
+constexpr int WavesFor() { return NP > 32 ? 8 : 4; }
 // q/k/v rows in LDS: 256-byte rows of 16 chunks of 8 bf16, chunk c of row i
 // stored at position c ^ (i & 15).  The swizzle keeps the column reads of
 // 16 consecutive rows on distinct banks without padding, so a row group is
@@ -233,7 +245,7 @@ struct VerifySmem : VRegion<NP, (NP > 32)> {
 };
 static_assert(sizeof(VerifySmem<64>) <= 80 * 1024, "two 64-wide workgroups per CU");
 static_assert(2 * 32 * 36 >= 16 * kD && 2 * 64 * 68 >= 16 * kD, "am + x hold the 16 staged path keys");
-static_assert(2 * 32 * 36 >= 4 * 512, "am + x hold the four waves' 2 KiB write-back staging buffers");
+static_assert(2 * 32 * 36 >= 4 * 512 && 2 * 64 * 68 >= 8 * 512, "am + x hold every wave's 2 KiB write-back staging");
 
 __device__ __forceinline__ f32x4 mfma_bf16_16x16x32(bf16x8 a, bf16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
@@ -411,16 +423,20 @@ __device__ __forceinline__ Pending decode_pending(const PendingHead& ph, int lan
 // so that no register is left waiting on a load that only some paths issue
 // (the compiler would then make later code wait for every store since).
 
+// (NW = 8: one 16-byte piece per thread, columns 4n + 64 (w / 4) ..)
+template <int NW>
 __device__ __forceinline__ void issue_pending(const dft_pending_commit& c, const Pending& pd, int h, int wave, int lane,
-                                              const float* dummy, f32x4 (&kr)[2], float (&vnr)[4][2],
-                                              float (&gp)[4]) {
+                                              const float* dummy, f32x4 (&kr)[8 / NW],
+                                              float (&vnr)[4][Waves<NW>::TT], float (&gp)[4]) {
+  constexpr int KP = 8 / NW, TT = Waves<NW>::TT, CW = Waves<NW>::CW;
   const bool any = pd.last >= 0;
   const int n16 = lane & 15, g4 = lane >> 4;
   const float* kb = any ? c.keys + (int64_t)(h / c.k_head_div) * c.k_h_stride + pd.prow0 * c.k_row_stride : dummy;
   const int64_t ks = any ? c.k_row_stride : 0;
-  const int krow = __shfl(pd.ent, 4 * wave + g4);
+  const int krow = __shfl(pd.ent, 4 * (wave & 3) + g4);
 #pragma unroll
-  for (int m = 0; m < 2; ++m) kr[m] = *reinterpret_cast<const f32x4*>(kb + krow * ks + 4 * (n16 + 16 * m));
+  for (int m = 0; m < KP; ++m)
+    kr[m] = *reinterpret_cast<const f32x4*>(kb + krow * ks + 4 * (n16 + 16 * (m + KP * (wave >> 2))));
   const float* vb = any ? c.values + (int64_t)h * c.v_h_stride + pd.prow0 * c.v_row_stride : dummy;
   const float* gb = any ? c.gains + (int64_t)h * c.g_h_stride + pd.prow0 * c.g_row_stride : dummy;
   const int64_t vs = any ? c.v_row_stride : 0, gs = any ? c.g_row_stride : 0;
@@ -428,7 +444,7 @@ __device__ __forceinline__ void issue_pending(const dft_pending_commit& c, const
   for (int s = 0; s < 4; ++s) {
     const int row = __shfl(pd.ent, 4 * s + g4);
 #pragma unroll
-    for (int t = 0; t < 2; ++t) vnr[s][t] = vb[row * vs + 32 * wave + 16 * t + n16];
+    for (int t = 0; t < TT; ++t) vnr[s][t] = vb[row * vs + CW * wave + 16 * t + n16];
     gp[s] = gb[row * gs];
   }
 }
@@ -438,10 +454,14 @@ __device__ __forceinline__ void issue_pending(const dft_pending_commit& c, const
 // columns v = 32w + 16t + n): fp32 MFMA 16x16x4, path slots as the inner
 // dimension (A = keys from LDS, B = weighted values from registers).
 // thread (w, l) holds chunks n and n + 16 of the key of path slot 4w + g
-__device__ __forceinline__ void stage_pending_keys(float* pkey, const f32x4 (&kr)[2], int wave, int lane) {
-  const int rs = 4 * wave + (lane >> 4), n16 = lane & 15;
+// (NW = 8: chunk n + 16 (w / 4) of path slot 4 (w % 4) + g)
+template <int NW>
+__device__ __forceinline__ void stage_pending_keys(float* pkey, const f32x4 (&kr)[8 / NW], int wave, int lane) {
+  constexpr int KP = 8 / NW;
+  const int rs = 4 * (wave & 3) + (lane >> 4), n16 = lane & 15;
 #pragma unroll
-  for (int m = 0; m < 2; ++m) *reinterpret_cast<f32x4*>(&pkey[pkey_at(rs, 4 * (n16 + 16 * m))]) = kr[m];
+  for (int m = 0; m < KP; ++m)
+    *reinterpret_cast<f32x4*>(&pkey[pkey_at(rs, 4 * (n16 + 16 * (m + KP * (wave >> 2))))]) = kr[m];
 }
 
 // e^{G_u}, the decay of the whole path, broadcast from the lane that holds G_u
@@ -454,16 +474,18 @@ __device__ __forceinline__ float pending_decay_log(const Pending& pd, const floa
 // The commit of a landed tile (a no-op when nothing is pending).  pkey:
 // 16 x 128 floats of LDS that no other wave touches until the next barrier;
 // every thread arrives here (the staging is followed by a barrier).
-__device__ __forceinline__ void commit_tile(const Pending& pd, float* pkey, const f32x4 (&kr)[2],
-                                            const float (&vnr)[4][2], const float (&gp)[4], int wave, int lane,
-                                            f32x4 (&s0r)[2][8]) {
+template <int NW>
+__device__ __forceinline__ void commit_tile(const Pending& pd, float* pkey, const f32x4 (&kr)[8 / NW],
+                                            const float (&vnr)[4][Waves<NW>::TT], const float (&gp)[4], int wave,
+                                            int lane, f32x4 (&s0r)[Waves<NW>::TT][8]) {
+  constexpr int TT = Waves<NW>::TT;
   const int n16 = lane & 15, g4 = lane >> 4;
-  stage_pending_keys(pkey, kr, wave, lane);
+  stage_pending_keys<NW>(pkey, kr, wave, lane);
   __syncthreads();
   const float gu = pending_decay_log(pd, gp);
   const float eu = pd.last >= 0 ? __expf(gu) : 1.f;
 #pragma unroll
-  for (int t = 0; t < 2; ++t)
+  for (int t = 0; t < TT; ++t)
 #pragma unroll
     for (int j = 0; j < 8; ++j) s0r[t][j] *= eu;
 #pragma unroll
@@ -471,24 +493,26 @@ __device__ __forceinline__ void commit_tile(const Pending& pd, float* pkey, cons
     if (4 * s > pd.last) break;  // uniform
     const int p = 4 * s + g4;
     const float wgt = ((pd.vmask >> p) & 1u) ? __expf(gu - gp[s]) : 0.f;
-    const float bv[2] = {wgt * vnr[s][0], wgt * vnr[s][1]};
+    float bv[TT];
+#pragma unroll
+    for (int t = 0; t < TT; ++t) bv[t] = wgt * vnr[s][t];
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const float av = pkey[pkey_at(p, 16 * j + n16)];
 #pragma unroll
-      for (int t = 0; t < 2; ++t) s0r[t][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv[t], s0r[t][j], 0, 0, 0);
+      for (int t = 0; t < TT; ++t) s0r[t][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv[t], s0r[t][j], 0, 0, 0);
     }
   }
 }
 
-// k-step group s of the state tile (j = 2s, 2s + 1 of both column tiles)
-template <bool NT>
+// k-step group s of the state tile (j = 2s, 2s + 1 of every column tile)
+template <bool NT, int NW>
 __device__ __forceinline__ void issue_state_group(const float* S0, int64_t v_stride, int wave, int lane, int s,
-                                                  f32x4 (&s0r)[2][8]) {
+                                                  f32x4 (&s0r)[Waves<NW>::TT][8]) {
   const int n16 = lane & 15, g4 = lane >> 4;
 #pragma unroll
-  for (int t = 0; t < 2; ++t) {
-    const float* rowp = S0 + (int64_t)(32 * wave + 16 * t + n16) * v_stride + 4 * g4;
+  for (int t = 0; t < Waves<NW>::TT; ++t) {
+    const float* rowp = S0 + (int64_t)(Waves<NW>::CW * wave + 16 * t + n16) * v_stride + 4 * g4;
 #pragma unroll
     for (int jj = 0; jj < 2; ++jj) {
       const int j = 2 * s + jj;
@@ -510,8 +534,9 @@ __device__ __forceinline__ void issue_state_group(const float* S0, int64_t v_str
 // chunk) and the read-backs (8 lanes = 8 chunks of one row) then hit 32
 // distinct banks.  A wave's LDS operations run in order, so the buffer is
 // reused piece after piece without waits.
-__device__ __forceinline__ void store_state(float* S, int64_t v_stride, int wave, int lane, const f32x4 (&s0r)[2][8],
-                                            float* stage) {
+template <int NW>
+__device__ __forceinline__ void store_state(float* S, int64_t v_stride, int wave, int lane,
+                                            const f32x4 (&s0r)[Waves<NW>::TT][8], float* stage) {
   const int n16 = lane & 15, g4 = lane >> 4;
   const int r8 = lane >> 3, c8 = lane & 7;
   const int64_t step8 = 8 * v_stride;
@@ -520,8 +545,8 @@ __device__ __forceinline__ void store_state(float* S, int64_t v_stride, int wave
   f32x4* w1 = st + 8 * n16 + ((4 + g4) ^ (n16 & 7));
   const f32x4* rd = st + 8 * r8 + (c8 ^ r8);  // rows r8 and 8 + r8 share the swizzle
 #pragma unroll
-  for (int t = 0; t < 2; ++t) {
-    float* r0 = S + (int64_t)(32 * wave + 16 * t + r8) * v_stride + 4 * c8;  // rows r8 and 8 + r8 of the tile
+  for (int t = 0; t < Waves<NW>::TT; ++t) {
+    float* r0 = S + (int64_t)(Waves<NW>::CW * wave + 16 * t + r8) * v_stride + 4 * c8;  // rows r8, 8 + r8 of the tile
     float* r1 = r0 + step8;
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
@@ -658,19 +683,19 @@ __device__ __forceinline__ void decode_gates(const dft_verify_args& p, const Ite
 
 // dense ancestry rows become bit masks (loads and waits right away: only the
 // dense form, used by the batch-1 drop-in, takes this path)
-template <int NP, class WK>
+template <int NP, int NW, class WK>
 __device__ __forceinline__ void dense_ancestry(const dft_verify_args& p, const Item& it, int wave, int lane, WK& wk) {
   const float* ab = p.anc_f32 + (int64_t)it.b * p.anc_req_stride;
-  for (int i = wave; i < NP; i += 4) {
+  for (int i = wave; i < NP; i += NW) {
     const float v = (i < it.n && lane < it.n) ? ab[i * p.anc_row_stride + lane] : 0.f;
     const uint64_t bits = __ballot(v > 0.5f);
     if (lane == 0) wk.anc[i] = bits & mask_upto(i);
   }
 }
 
-// q/k/v rows -> LDS: one 1 KiB copy fills 4 swizzled rows (NP/16 per wave and
-// plane).  Planes M0 .. M1-1 of (q, k, v).
-template <int NP, int M0, int M1, class RW>
+// q/k/v rows -> LDS: one 1 KiB copy fills 4 swizzled rows (NP/(4 NW) per wave
+// and plane).  Planes M0 .. M1-1 of (q, k, v).
+template <int NP, int M0, int M1, int NW, class RW>
 __device__ __forceinline__ void issue_rows(const dft_verify_args& p, const Item& it, int wave, int lane,
                                            const void* alt, RW& rw) {
   const int KD = p.hk * kD;
@@ -680,8 +705,8 @@ __device__ __forceinline__ void issue_rows(const dft_verify_args& p, const Item&
   uint16_t* dsts[3] = {rw.q, rw.k, rw.vrows()};
   const int pc = lane & 15;
 #pragma unroll
-  for (int u = 0; u < NP / 16; ++u) {
-    const int blk = wave + 4 * u;  // rows 4 blk .. 4 blk + 3
+  for (int u = 0; u < NP / (4 * NW); ++u) {
+    const int blk = wave + NW * u;  // rows 4 blk .. 4 blk + 3
     const int i = 4 * blk + (lane >> 4);
     const int isrc = i < it.n ? i : it.n - 1;  // rows past the tree repeat a real row (finite, masked later)
     const int64_t goff = isrc * ys + 8 * ((pc ^ i) & 15);
@@ -706,12 +731,13 @@ __device__ __forceinline__ void issue_rows(const dft_verify_args& p, const Item&
 // batch 64 (interleaved runs): the read-only verify is 2.9% faster with
 // ordinary loads, the fused commit -> verify (which writes the tile back)
 // 0.7% faster with non-temporal ones.
-template <bool NT>
-__device__ __forceinline__ void issue_state(const float* S0, int64_t v_stride, int wave, int lane, f32x4 (&s0r)[2][8]) {
+template <bool NT, int NW>
+__device__ __forceinline__ void issue_state(const float* S0, int64_t v_stride, int wave, int lane,
+                                            f32x4 (&s0r)[Waves<NW>::TT][8]) {
   const int n16 = lane & 15, g4 = lane >> 4;
 #pragma unroll
-  for (int t = 0; t < 2; ++t) {
-    const float* rowp = S0 + (int64_t)(32 * wave + 16 * t + n16) * v_stride + 4 * g4;
+  for (int t = 0; t < Waves<NW>::TT; ++t) {
+    const float* rowp = S0 + (int64_t)(Waves<NW>::CW * wave + 16 * t + n16) * v_stride + 4 * g4;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const f32x4* src = reinterpret_cast<const f32x4*>(rowp + 16 * j);
@@ -721,11 +747,13 @@ __device__ __forceinline__ void issue_state(const float* S0, int64_t v_stride, i
 }
 
 // 1a: row norms (4 threads per q/k row) and the path-cumulative decay
-// (256 / NP threads per node), spread over all four waves
-template <int NP, class RW, class WK>
+// (NT / NP threads per node), spread over all waves
+template <int NP, int NW, class RW, class WK>
 __device__ __forceinline__ void phase_norms(const dft_verify_args& p, int tid, const RW& rw, WK& wk) {
+  constexpr int NT = Waves<NW>::NT;
+  static_assert((2 * NP) % (NT / 4) == 0, "whole passes of q and k rows");
 #pragma unroll
-  for (int r0 = 0; r0 < 2 * NP; r0 += 64) {
+  for (int r0 = 0; r0 < 2 * NP; r0 += NT / 4) {
     const int r = r0 + (tid >> 2), qd = tid & 3, i = r % NP;
     const uint16_t* rows = r < NP ? rw.q : rw.k;
     float ss = 0.f;
@@ -747,7 +775,7 @@ __device__ __forceinline__ void phase_norms(const dft_verify_args& p, int tid, c
       else wk.rk[i] = rn;
     }
   }
-  constexpr int TPN = 256 / NP;  // threads per node
+  constexpr int TPN = NT / NP;  // threads per node
   const int i = tid / TPN, sub = tid % TPN;
   const uint64_t bits = wk.anc[i];
   float G = 0.f;
@@ -763,14 +791,14 @@ __device__ __forceinline__ void phase_norms(const dft_verify_args& p, int tid, c
 
 // The saves for the commit: normalised keys (once per k-head when saved per
 // k-head) and G.  Needs the norms and G; reads the k rows.
-template <int NP, bool LATE, class RW, class WK>
+template <int NP, bool LATE, int NW, class RW, class WK>
 __device__ __forceinline__ void phase_saves(const VerifyParams& P, const Item& it, int tid, const RW& rw,
                                             const WK& wk) {
   const OutArgs p = out_args<LATE>(P);
   const bool per_khead = (p.flags & DFT_VERIFY_AUX_K_PER_KHEAD) != 0;
   if (p.aux_k && (!per_khead || it.rr == 0)) {
     float* dk = p.aux_k + (int64_t)(per_khead ? it.hk : it.h) * p.aux_k_h_stride + it.row0 * p.aux_k_row_stride;
-    for (int c = tid; c < it.n * 32; c += 256) {
+    for (int c = tid; c < it.n * 32; c += Waves<NW>::NT) {
       const int i = c >> 5, d = (c & 31) * 4;
       const uint2 u = *reinterpret_cast<const uint2*>(&rw.k[qkv_at(i, d)]);
       const float r = wk.rk[i];
@@ -820,8 +848,9 @@ __device__ __forceinline__ void a_tile(const RW& rw, WK& wk, int ti, int tj, int
   }
 }
 
-template <int NP, class RW, class WK>
-__device__ __forceinline__ void phase_gram_diag(int tid, const RW& rw, WK& wk) {
+// mtn: 16-row tiles that hold nodes (the rest are padding and are skipped)
+template <int NP, int NW, class RW, class WK>
+__device__ __forceinline__ void phase_gram_diag(int tid, const RW& rw, WK& wk, int mtn) {
   constexpr int MT = NP / 16;
   constexpr int LDA = WK::LDA;
   const int lane = tid & 63, wave = tid >> 6, n16 = lane & 15, g4 = lane >> 4;
@@ -830,7 +859,7 @@ __device__ __forceinline__ void phase_gram_diag(int tid, const RW& rw, WK& wk) {
     wk.gc[tid] = eG * wk.rk[tid];  // g is no longer needed
     wk.cO[tid] = eG * wk.rq[tid];
   }
-  if (wave < MT) {
+  if (wave < mtn) {
     a_tile<NP>(rw, wk, wave, wave, n16, g4);
     if (lane < 16) {
       const int bb = wave, j = lane;
@@ -848,21 +877,22 @@ __device__ __forceinline__ void phase_gram_diag(int tid, const RW& rw, WK& wk) {
   for (int ti = 1; ti < MT; ++ti)
 #pragma unroll
     for (int tj = 0; tj < ti; ++tj, ++item)
-      if (((MT + item) & 3) == wave) a_tile<NP>(rw, wk, ti, tj, n16, g4);
+      if (ti < mtn && (MT + item) % NW == wave) a_tile<NP>(rw, wk, ti, tj, n16, g4);
+  if (tid < 256)  // one element of each 16 x 16 block per thread
 #pragma unroll
-  for (int b = 0; b + 1 < MT; b += 2) wk.x()[(16 * b + (tid >> 4)) * LDA + 16 * (b + 1) + (tid & 15)] = 0.f;
+    for (int b = 0; b + 1 < MT; b += 2) wk.x()[(16 * b + (tid >> 4)) * LDA + 16 * (b + 1) + (tid & 15)] = 0.f;
 }
 
 
 // 1d, one level: off-diagonal blocks X_ij = -D_i sum_{m=j}^{i-1} A_im X_mj at
 // distance d = i - j (each level needs the previous ones)
-template <int NP, class WK>
-__device__ __forceinline__ void phase_offdiag(int tid, int d, WK& wk) {
+template <int NP, int NW, class WK>
+__device__ __forceinline__ void phase_offdiag(int tid, int d, WK& wk, int mtn) {
   constexpr int MT = NP / 16;
   constexpr int LDA = WK::LDA;
   const int lane = tid & 63, wave = tid >> 6, n16 = lane & 15, g4 = lane >> 4;
   const int bj = wave, bi = wave + d;
-  if (bi < MT) {
+  if (bi < mtn) {
     f32x4 T = {};
 #pragma unroll
     for (int bm = 0; bm < MT; ++bm)
@@ -901,13 +931,18 @@ __device__ __forceinline__ f32x4 pq_tile(const RW& rw, const WK& wk, int bi, int
 // Wave that forms M block (bi, bj).  Block (bi, bj <= bi) sums bi - bj + 1
 // Pq X terms.  For 2 x 2 blocks every wave takes one block; for 4 x 4 (20
 // terms) every wave takes 5, where a column per wave would give wave 0 ten.
-template <int MT>
+// With 8 waves and 4 x 4 blocks the largest block (4 terms) sets the pace:
+// every other wave takes at most 3 terms (and the two zero blocks).
+template <int MT, int NW>
 __device__ __forceinline__ constexpr int m_owner(int bi, int bj) {
-  if constexpr (MT == 4) {
+  if constexpr (MT == 4 && NW == 8) {
+    constexpr int own[4][4] = {{6, 3, 0, 0}, {3, 6, 0, 0}, {1, 4, 7, 4}, {0, 2, 5, 7}};
+    return own[bi][bj];
+  } else if constexpr (MT == 4) {
     constexpr int own[4][4] = {{0, 1, 2, 3}, {1, 3, 0, 1}, {2, 3, 3, 2}, {0, 1, 2, 3}};
     return own[bi][bj];
   } else {
-    return (bi * MT + bj) & 3;
+    return (bi * MT + bj) % NW;
   }
 }
 
@@ -916,17 +951,18 @@ __device__ __forceinline__ constexpr int m_owner(int bi, int bj) {
 // takes LDS; a tile shared by several M blocks of different waves is formed
 // once per block.  Above the diagonal only the zero blocks (b, b + 1), b
 // even, are written: phase_out reads no others (as for X).
-template <int NP, class RW, class WK>
-__device__ __forceinline__ void phase_m(int tid, const RW& rw, WK& wk) {
+template <int NP, int NW, class RW, class WK>
+__device__ __forceinline__ void phase_m(int tid, const RW& rw, WK& wk, int mtn) {
   constexpr int MT = NP / 16;
   constexpr int LDA = WK::LDA;
   const int lane = tid & 63, wave = tid >> 6, n16 = lane & 15, g4 = lane >> 4;
 #pragma unroll
-  for (int bi = 0; bi < MT; ++bi)
+  for (int bi = 0; bi < MT; ++bi) {
+    if (bi >= mtn) break;  // padding rows: never read
 #pragma unroll
     for (int bj = 0; bj < MT; ++bj) {
       if (bj > bi && (bj != bi + 1 || (bi & 1))) continue;
-      if (m_owner<MT>(bi, bj) != wave) continue;
+      if (m_owner<MT, NW>(bi, bj) != wave) continue;
       f32x4 acc = {};
       if (bj <= bi) {
 #pragma unroll
@@ -939,6 +975,7 @@ __device__ __forceinline__ void phase_m(int tid, const RW& rw, WK& wk) {
       }
       store_block<LDA>(wk.am(), bi, bj, acc, n16, g4);
     }
+  }
 }
 
 // 2: Cq = q_raw S0, Ck = k_raw S0 for the wave's 32 columns.  k-step s, lane
@@ -950,36 +987,39 @@ __device__ __forceinline__ void phase_m(int tid, const RW& rw, WK& wk) {
 // column 16t + 4g + r), the layout of the output tiles.
 // WHICH: 3 = both products, 1 = Cq only, 2 = Ck only (a two-pass form that
 // splits the state into hi/lo twice but frees the q rows after the first).
-template <int NP, int WHICH = 3, class RW>
-__device__ __forceinline__ void phase_cq_ck(int lane, const RW& rw, const f32x4 (&s0r)[2][8], f32x4 (&cq)[NP / 16][2],
-                                            f32x4 (&ck)[NP / 16][2]) {
+template <int NP, int WHICH, int NW, class RW>
+__device__ __forceinline__ void phase_cq_ck(int lane, const RW& rw, const f32x4 (&s0r)[Waves<NW>::TT][8],
+                                            f32x4 (&cq)[NP / 16][Waves<NW>::TT],
+                                            f32x4 (&ck)[NP / 16][Waves<NW>::TT], int mtn) {
+  constexpr int TT = Waves<NW>::TT;
   constexpr int MT = NP / 16;
   constexpr bool DQ = (WHICH & 1) != 0, DK = (WHICH & 2) != 0;
   const int n16 = lane & 15, g4 = lane >> 4;
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
+    for (int t = 0; t < TT; ++t) {
       if (DQ) cq[mt][t] = f32x4{};
       if (DK) ck[mt][t] = f32x4{};
     }
 #pragma unroll
   for (int s = 0; s < 4; ++s) {
-    bf16x8 bhi[2], blo[2];
+    bf16x8 bhi[TT], blo[TT];
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
+    for (int t = 0; t < TT; ++t) {
       const float xs[8] = {s0r[t][2 * s][0],     s0r[t][2 * s][1],     s0r[t][2 * s][2],     s0r[t][2 * s][3],
                            s0r[t][2 * s + 1][0], s0r[t][2 * s + 1][1], s0r[t][2 * s + 1][2], s0r[t][2 * s + 1][3]};
       split_bf16x8(xs, bhi[t], blo[t]);
     }
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
+      if (mt >= mtn) break;  // padding rows stay zero
       const int row = 16 * mt + n16, c0 = 32 * s + 4 * g4;
       bf16x8 aq{}, ak{};
       if (DQ) aq = lds_bf16x8_split(rw.q + qkv_at(row, c0), rw.q + qkv_at(row, c0 + 16));
       if (DK) ak = lds_bf16x8_split(rw.k + qkv_at(row, c0), rw.k + qkv_at(row, c0 + 16));
 #pragma unroll
-      for (int t = 0; t < 2; ++t) {
+      for (int t = 0; t < TT; ++t) {
         if (DQ) cq[mt][t] = mfma_bf16_16x16x32(bhi[t], aq, cq[mt][t]);
         if (DK) ck[mt][t] = mfma_bf16_16x16x32(ak, bhi[t], ck[mt][t]);
         if (DQ) cq[mt][t] = mfma_bf16_16x16x32(blo[t], aq, cq[mt][t]);
@@ -992,16 +1032,18 @@ __device__ __forceinline__ void phase_cq_ck(int lane, const RW& rw, const f32x4 
 // 3a: W = beta (v - e^G rk Ck) in the accumulator layout, split into bf16
 // hi/lo B operands: k-step ks, lane group g, element e -> node 32ks + 4g + e
 // (e < 4), 32ks + 16 + 4g + e-4, i.e. registers of tiles 2ks, 2ks+1
-template <int NP, class RW, class WK>
-__device__ __forceinline__ void phase_w(int lane, int wave, const RW& rw, const WK& wk, const f32x4 (&ck)[NP / 16][2],
-                                        bf16x8 (&wh)[NP / 32][2], bf16x8 (&wl)[NP / 32][2]) {
+template <int NP, int NW, class RW, class WK>
+__device__ __forceinline__ void phase_w(int lane, int wave, const RW& rw, const WK& wk,
+                                        const f32x4 (&ck)[NP / 16][Waves<NW>::TT],
+                                        bf16x8 (&wh)[NP / 32][Waves<NW>::TT], bf16x8 (&wl)[NP / 32][Waves<NW>::TT]) {
+  constexpr int TT = Waves<NW>::TT, CW = Waves<NW>::CW;
   constexpr int KS = NP / 32;
   const int n16 = lane & 15, g4 = lane >> 4;
 #pragma unroll
   for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      const int col = 32 * wave + 16 * t + n16;
+    for (int t = 0; t < TT; ++t) {
+      const int col = CW * wave + 16 * t + n16;
       float w8[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
@@ -1019,10 +1061,12 @@ __device__ __forceinline__ void phase_w(int lane, int wave, const RW& rw, const 
 // node 16mt + n at the four consecutive columns 16t + 4g .. +3: one 16-byte
 // (vn) or 8-byte (o) write each.  Staged into the (then free) q/k/v region of
 // rw when the flags allow, else stored directly.
-template <int NP, class RW, class WK>
+template <int NP, int NW, class RW, class WK>
 __device__ __forceinline__ void phase_out(const VerifyParams& P, const Item& it, int lane, int wave, RW& rw,
-                                          const WK& wk, const f32x4 (&cq)[NP / 16][2],
-                                          const bf16x8 (&wh)[NP / 32][2], const bf16x8 (&wl)[NP / 32][2]) {
+                                          const WK& wk, const f32x4 (&cq)[NP / 16][Waves<NW>::TT],
+                                          const bf16x8 (&wh)[NP / 32][Waves<NW>::TT],
+                                          const bf16x8 (&wl)[NP / 32][Waves<NW>::TT], int mtn) {
+  constexpr int TT = Waves<NW>::TT, CW = Waves<NW>::CW;
   constexpr int MT = NP / 16;
   constexpr int KS = NP / 32;
   constexpr int LDA = WK::LDA;
@@ -1036,8 +1080,11 @@ __device__ __forceinline__ void phase_out(const VerifyParams& P, const Item& it,
     if constexpr (RW::kLateV)
       if (mo == MT) __syncthreads();
     const int mt = mo % MT;
+    if (mt >= mtn) continue;  // padding rows: not stored
     const float* src = mo < MT ? wk.x() : wk.am();
-    f32x4 acc[2] = {f32x4{}, f32x4{}};
+    f32x4 acc[TT];
+#pragma unroll
+    for (int t = 0; t < TT; ++t) acc[t] = f32x4{};
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
       if (32 * ks > 16 * mt + 15) continue;  // both factors are lower triangular
@@ -1046,7 +1093,7 @@ __device__ __forceinline__ void phase_out(const VerifyParams& P, const Item& it,
       bf16x8 ah, al;
       split_bf16x8(a8, ah, al);
 #pragma unroll
-      for (int t = 0; t < 2; ++t) {
+      for (int t = 0; t < TT; ++t) {
         acc[t] = mfma_bf16_16x16x32(wh[ks][t], ah, acc[t]);
         acc[t] = mfma_bf16_16x16x32(wl[ks][t], ah, acc[t]);
         acc[t] = mfma_bf16_16x16x32(wh[ks][t], al, acc[t]);
@@ -1054,8 +1101,8 @@ __device__ __forceinline__ void phase_out(const VerifyParams& P, const Item& it,
     }
     const int i = 16 * mt + n16;
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      const int col = 32 * wave + 16 * t + 4 * g4;
+    for (int t = 0; t < TT; ++t) {
+      const int col = CW * wave + 16 * t + 4 * g4;
       if (mo < MT) {
         if (P.vn_stage) {
           *reinterpret_cast<f32x4*>(&vn_s[vn_at(i, col)]) = acc[t];
@@ -1087,16 +1134,17 @@ __device__ __forceinline__ void phase_out(const VerifyParams& P, const Item& it,
 // the key saves) are written once and not read back by this launch: they go
 // out as non-temporal stores, which at batch 64 made the verify 6.6% and the
 // fused commit -> verify 3.1% faster than ordinary stores.
-template <int NP, bool LATE, class RW>
+template <int NP, bool LATE, int NW, class RW>
 __device__ __forceinline__ void phase_stores(const VerifyParams& P, const Item& it, int tid, const RW& rw) {
+  constexpr int NT = Waves<NW>::NT;
   const OutArgs p = out_args<LATE>(P);
   const float* vn_s = reinterpret_cast<const float*>(rw.q);
   const uint16_t* o_s = rw.ostage();
   if (p.vn_stage) {  // rows of 32 x 16 bytes
     float* dst = p.aux_v + (int64_t)it.h * p.aux_v_h_stride + it.row0 * p.aux_v_row_stride;
 #pragma unroll
-    for (int u = 0; u < NP / 8; ++u) {
-      const int i = 8 * u + (tid >> 5), q = tid & 31;
+    for (int u = 0; u < NP * 32 / NT; ++u) {
+      const int i = (NT / 32) * u + (tid >> 5), q = tid & 31;
       if (i < it.n)
         __builtin_nontemporal_store(*reinterpret_cast<const f32x4*>(&vn_s[vn_at(i, 4 * q)]),
                                     reinterpret_cast<f32x4*>(dst + i * p.aux_v_row_stride + 4 * q));
@@ -1105,8 +1153,8 @@ __device__ __forceinline__ void phase_stores(const VerifyParams& P, const Item& 
   if (p.o_stage) {  // rows of 16 x 16 bytes
     uint16_t* dst = static_cast<uint16_t*>(p.o) + it.row0 * p.o_row_stride + (int64_t)it.h * p.o_h_stride;
 #pragma unroll
-    for (int u = 0; u < NP / 16; ++u) {
-      const int i = 16 * u + (tid >> 4), q = tid & 15;
+    for (int u = 0; u < NP * 16 / NT; ++u) {
+      const int i = (NT / 16) * u + (tid >> 4), q = tid & 15;
       if (i < it.n)
         __builtin_nontemporal_store(*reinterpret_cast<const u32x4*>(&o_s[qkv_at(i, 8 * q)]),
                                     reinterpret_cast<u32x4*>(dst + i * p.o_row_stride + 8 * q));
@@ -1141,8 +1189,11 @@ __device__ __forceinline__ void fused_status(const Item& it, int lane, uint32_t 
 template <int NP, bool S0VEC, bool COMMIT>
 __device__ __forceinline__ void verify_body(const VerifyParams& P) {
   constexpr int MT = NP / 16;
+  constexpr int NW = WavesFor<NP>();
+  constexpr int TT = Waves<NW>::TT, CW = Waves<NW>::CW;
   constexpr int kPlanes = VerifySmem<NP>::kLateV ? 2 : 3;  // the late form copies its v rows after Cq/Ck
-  constexpr int kQkvDma = kPlanes * (NP / 16);                // row copies per wave
+  constexpr int kQkvDma = kPlanes * (NP / (4 * NW));          // row copies per wave
+  constexpr int kStateLoads = 8 * TT, kGroupLoads = 2 * TT;   // per lane: whole tile, one k-step group
   const dft_verify_args& p = P.a;
   __shared__ VerifySmem<NP> sm;
 
@@ -1167,13 +1218,13 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
       const Pending pd = decode_pending(ph, lane, word);
       if (it.h == 0 && wave == 0) fused_status(it, lane, word);
       if (pd.last < 0) return;
-      f32x4 s0r[2][8], kr[2];
-      float vnr[4][2], gp[4];
-      issue_state<true>(S0, p.state_v_stride, wave, lane, s0r);
-      issue_pending(P.c, pd, it.h, wave, lane, S0, kr, vnr, gp);
-      commit_tile(pd, sm.pkey(), kr, vnr, gp, wave, lane, s0r);
+      f32x4 s0r[TT][8], kr[8 / NW];
+      float vnr[4][TT], gp[4];
+      issue_state<true, NW>(S0, p.state_v_stride, wave, lane, s0r);
+      issue_pending<NW>(P.c, pd, it.h, wave, lane, S0, kr, vnr, gp);
+      commit_tile<NW>(pd, sm.pkey(), kr, vnr, gp, wave, lane, s0r);
       __syncthreads();  // every wave has read the staged keys: am + x take the write-back staging
-      store_state(const_cast<float*>(S0), p.state_v_stride, wave, lane, s0r, sm.amx + wave * 512);
+      store_state<NW>(const_cast<float*>(S0), p.state_v_stride, wave, lane, s0r, sm.amx + wave * 512);
       return;
     }
   }
@@ -1185,11 +1236,11 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
   // state; the state keeps streaming underneath it.
   // (fused form: the pending path's entry words travel in gate row 4)
   if (wave == 0) issue_gates(p, it, lane, S0, sm.graw, COMMIT ? path_word(P.c, it.b, lane) : nullptr);
-  if (p.anc_f32) dense_ancestry<NP>(p, it, wave, lane, sm);
-  issue_rows<NP, 0, kPlanes>(p, it, wave, lane, S0, sm);
+  if (p.anc_f32) dense_ancestry<NP, NW>(p, it, wave, lane, sm);
+  issue_rows<NP, 0, kPlanes, NW>(p, it, wave, lane, S0, sm);
   asm volatile("" ::: "memory");
 
-  f32x4 s0r[2][8];
+  f32x4 s0r[TT][8];
   // The verify issues its state tile in 4 groups (the k-steps phase 2
   // consumes in order) through phase 1: a wave blocked on a full memory queue
   // then stalls between compute phases instead of ahead of all of them
@@ -1197,17 +1248,17 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
   // commit before phase 1 and issues it at once.
   constexpr bool kSplit = S0VEC && !COMMIT;
   if (kSplit) {
-    issue_state_group<false>(S0, p.state_v_stride, wave, lane, 0, s0r);
+    issue_state_group<false, NW>(S0, p.state_v_stride, wave, lane, 0, s0r);
   } else if (S0VEC) {
-    issue_state<COMMIT>(S0, p.state_v_stride, wave, lane, s0r);
+    issue_state<COMMIT, NW>(S0, p.state_v_stride, wave, lane, s0r);
   } else {
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
+    for (int t = 0; t < TT; ++t)
 #pragma unroll
       for (int j = 0; j < 8; ++j)
 #pragma unroll
         for (int e = 0; e < 4; ++e)
-          s0r[t][j][e] = S0[(int64_t)(32 * wave + 16 * t + n16) * p.state_v_stride +
+          s0r[t][j][e] = S0[(int64_t)(CW * wave + 16 * t + n16) * p.state_v_stride +
                             (int64_t)(16 * j + 4 * g4 + e) * p.state_k_stride];
     __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 15));  // element loads: no overlap on this path
   }
@@ -1215,14 +1266,14 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
 
   if (wave == 0) {
     // the gate words were wave 0's first copies: wait for them only
-    __builtin_amdgcn_s_waitcnt(waitcnt_imm(kQkvDma + (kSplit ? 4 : 16), 15));
+    __builtin_amdgcn_s_waitcnt(waitcnt_imm(kQkvDma + (kSplit ? kGroupLoads : kStateLoads), 15));
     asm volatile("" ::: "memory");
     if (lane < NP) decode_gates(p, it, lane, sm.graw, sm);
   }
   // Wait for the row loads and gates (everything issued before the state),
   // then make the LDS writes of all waves visible.  A plain __syncthreads()
   // here would also drain the state loads.
-  __builtin_amdgcn_s_waitcnt(waitcnt_imm(kSplit ? 4 : 16, 0));
+  __builtin_amdgcn_s_waitcnt(waitcnt_imm(kSplit ? kGroupLoads : kStateLoads, 0));
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
 
@@ -1233,66 +1284,71 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
   // and the tile goes back to its slot, so that the write-back streams under
   // the rest of phase 1.
   Pending pd{};
-  f32x4 kr[2];
-  float vnr[4][2], gp[4];
+  f32x4 kr[8 / NW];
+  float vnr[4][TT], gp[4];
   if constexpr (COMMIT) {
     pd = decode_pending(ph, lane, sm.graw[4][lane & 15]);
-    issue_pending(P.c, pd, it.h, wave, lane, S0, kr, vnr, gp);
+    issue_pending<NW>(P.c, pd, it.h, wave, lane, S0, kr, vnr, gp);
   }
-  phase_norms<NP>(p, tid, sm, sm);
+  phase_norms<NP, NW>(p, tid, sm, sm);
   __syncthreads();
   if constexpr (COMMIT) {
-    commit_tile(pd, sm.pkey(), kr, vnr, gp, wave, lane, s0r);
+    commit_tile<NW>(pd, sm.pkey(), kr, vnr, gp, wave, lane, s0r);
     // everything this wave loaded has been consumed: no load is left in
     // flight past the (conditional) write-back
     __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 15));
     if (pd.last >= 0) {  // uniform over the workgroup (one request)
       __syncthreads();  // every wave has read the staged keys: am + x take the write-back staging
-      store_state(const_cast<float*>(S0), p.state_v_stride, wave, lane, s0r, sm.amx + wave * 512);
+      store_state<NW>(const_cast<float*>(S0), p.state_v_stride, wave, lane, s0r, sm.amx + wave * 512);
     }
     __syncthreads();  // am and x take the Gram tiles and X
   }
-  if constexpr (kSplit) issue_state_group<false>(S0, p.state_v_stride, wave, lane, 1, s0r);
-  phase_saves<NP, COMMIT>(P, it, tid, sm, sm);
-  phase_gram_diag<NP>(tid, sm, sm);
-  if constexpr (kSplit) issue_state_group<false>(S0, p.state_v_stride, wave, lane, 2, s0r);
+  if constexpr (kSplit) issue_state_group<false, NW>(S0, p.state_v_stride, wave, lane, 1, s0r);
+  phase_saves<NP, COMMIT, NW>(P, it, tid, sm, sm);
+  const int mtn = (it.n + 15) >> 4;  // uniform over the workgroup
+  phase_gram_diag<NP, NW>(tid, sm, sm, mtn);
+  if constexpr (kSplit) issue_state_group<false, NW>(S0, p.state_v_stride, wave, lane, 2, s0r);
   __syncthreads();
 #pragma unroll
   for (int d = 1; d < MT; ++d) {
-    phase_offdiag<NP>(tid, d, sm);
+    if (d >= mtn) break;
+    phase_offdiag<NP, NW>(tid, d, sm, mtn);
     __syncthreads();
   }
-  if constexpr (kSplit) issue_state_group<false>(S0, p.state_v_stride, wave, lane, 3, s0r);
-  phase_m<NP>(tid, sm, sm);
+  if constexpr (kSplit) issue_state_group<false, NW>(S0, p.state_v_stride, wave, lane, 3, s0r);
+  phase_m<NP, NW>(tid, sm, sm, mtn);
 
-  f32x4 cq[MT][2], ck[MT][2];
+  f32x4 cq[MT][TT], ck[MT][TT];
   if constexpr (VerifySmem<NP>::kLateV) {
     // Cq first; once every wave is done with the q rows, the v rows are
     // copied into their region while Ck computes
-    phase_cq_ck<NP, 1>(lane, sm, s0r, cq, ck);
+    phase_cq_ck<NP, 1, NW>(lane, sm, s0r, cq, ck, mtn);
     __syncthreads();  // X and M complete, the q rows consumed
-    issue_rows<NP, 2, 3>(p, it, wave, lane, S0, sm);
-    phase_cq_ck<NP, 2>(lane, sm, s0r, cq, ck);
+    issue_rows<NP, 2, 3, NW>(p, it, wave, lane, S0, sm);
+    phase_cq_ck<NP, 2, NW>(lane, sm, s0r, cq, ck, mtn);
     __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 15));  // the v row copies (untracked by the backend)
     __syncthreads();
   } else {
-    phase_cq_ck<NP>(lane, sm, s0r, cq, ck);
+    phase_cq_ck<NP, 3, NW>(lane, sm, s0r, cq, ck, mtn);
     __syncthreads();  // X and M complete
   }
-  bf16x8 wh[NP / 32][2], wl[NP / 32][2];
-  phase_w<NP>(lane, wave, sm, sm, ck, wh, wl);
+  bf16x8 wh[NP / 32][TT], wl[NP / 32][TT];
+  phase_w<NP, NW>(lane, wave, sm, sm, ck, wh, wl);
   __syncthreads();  // every wave has read its v rows: the q/k/v region takes the outputs
-  phase_out<NP>(P, it, lane, wave, sm, sm, cq, wh, wl);
+  phase_out<NP, NW>(P, it, lane, wave, sm, sm, cq, wh, wl, mtn);
   if (P.vn_stage || P.o_stage) {
     __syncthreads();
-    phase_stores<NP, COMMIT>(P, it, tid, sm);
+    phase_stores<NP, COMMIT, NW>(P, it, tid, sm);
   }
   if constexpr (COMMIT)
     if (it.h == 0 && wave == 0) fused_status(it, lane, sm.graw[4][lane & 15]);
 }
 
+// Both widths run at 4 waves per SIMD (at most 128 registers): the 32-wide
+// kernel as 4 workgroups of 4 waves per CU, the 64-wide one as 2 of 8 waves
+// (its LDS holds two per CU).
 template <int NP, bool S0VEC>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NP == 32 ? 4 : 1)))
+__global__ void __launch_bounds__(64 * WavesFor<NP>()) __attribute__((amdgpu_waves_per_eu(4)))
 tree_verify_kernel(const VerifyParams P) {
   verify_body<NP, S0VEC, false>(P);
 }
@@ -1301,7 +1357,7 @@ tree_verify_kernel(const VerifyParams P) {
 // back from offset 0 of the kernel-argument segment.
 static_assert(std::is_trivially_copyable<VerifyParams>::value, "VerifyParams is passed by value to the kernels");
 template <int NP>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NP == 32 ? 4 : 1)))
+__global__ void __launch_bounds__(64 * WavesFor<NP>()) __attribute__((amdgpu_waves_per_eu(4)))
 tree_commit_verify_kernel(const VerifyParams P) {
   verify_body<NP, true, true>(P);
 }
@@ -1342,15 +1398,15 @@ static void split_by_size(const dft_verify_args* a, const VerifyParams& P, Verif
 
 int launch_tree_verify(const dft_verify_args* a, hipStream_t stream) {
   const VerifyParams P = make_params(a);
-  const dim3 grid((unsigned)(a->batch * a->hv)), block(256);
+  const dim3 grid((unsigned)(a->batch * a->hv)), block(64 * WavesFor<32>()), block64(64 * WavesFor<64>());
   VerifyParams narrow, wide;
   bool split;
   split_by_size(a, P, narrow, wide, split);
   if (a->n_nodes > 32) {
     if (P.s0_vec)
-      hipLaunchKernelGGL((tree_verify_kernel<64, true>), grid, block, 0, stream, wide);
+      hipLaunchKernelGGL((tree_verify_kernel<64, true>), grid, block64, 0, stream, wide);
     else
-      hipLaunchKernelGGL((tree_verify_kernel<64, false>), grid, block, 0, stream, wide);
+      hipLaunchKernelGGL((tree_verify_kernel<64, false>), grid, block64, 0, stream, wide);
   }
   if (a->n_nodes <= 32 || split) {
     if (P.s0_vec)
@@ -1365,11 +1421,11 @@ int launch_tree_verify(const dft_verify_args* a, hipStream_t stream) {
 int launch_tree_commit_verify(const dft_verify_args* a, const dft_pending_commit* c, hipStream_t stream) {
   VerifyParams P = make_params(a);
   P.c = *c;
-  const dim3 grid((unsigned)(a->batch * a->hv)), block(256);
+  const dim3 grid((unsigned)(a->batch * a->hv)), block(64 * WavesFor<32>()), block64(64 * WavesFor<64>());
   VerifyParams narrow, wide;
   bool split;
   split_by_size(a, P, narrow, wide, split);
-  if (a->n_nodes > 32) hipLaunchKernelGGL((tree_commit_verify_kernel<64>), grid, block, 0, stream, wide);
+  if (a->n_nodes > 32) hipLaunchKernelGGL((tree_commit_verify_kernel<64>), grid, block64, 0, stream, wide);
   if (a->n_nodes <= 32 || split) hipLaunchKernelGGL((tree_commit_verify_kernel<32>), grid, block, 0, stream, narrow);
   return hipGetLastError() == hipSuccess ? DFT_OK : DFT_ERR_LAUNCH;
 }
