@@ -7,11 +7,11 @@
 //   G_i   = sum_{j anc-or-self i} g_j
 //   A_ij  = [j strict anc i] beta_i (k_n,i . k_n,j) e^{G_i - G_j}
 //   Pq_ij = [j anc-or-self i] (q_n,i . k_n,j) e^{G_i - G_j}
-//   X     = (I + A)^-1,   M = Pq X
+//   X     = (I + A)^-1
 //   Cq    = q_raw S0,  Ck = k_raw S0                   (bf16 MFMA, S0 split hi+lo)
 //   W     = diag(beta) (v - diag(e^G rk) Ck)
 //   vn    = X W  (= X(beta v) - X(beta e^G k) S0 of :182-186)
-//   o     = diag(e^G rq) Cq + M W  (= (e^G q) S0 + Pq vn of :190)
+//   o     = diag(e^G rq) Cq + Pq vn  (= (e^G q) S0 + Pq vn of :190)
 //
 // Phases:
 //  0. the 64 KiB state tile streams straight into MFMA B operands of
@@ -22,13 +22,16 @@
 //     the 64-wide form copies its v rows only after Cq (LDS budget).
 //  1. while the state is in flight: norms, G, the Gram tiles of A, the
 //     blocked inverse X (16x16 diagonal blocks by forward substitution,
-//     off-diagonal blocks X_ij = -D_i sum_m A_im X_mj by fp32 MFMA) and
-//     M = Pq X with the Pq tiles formed in registers as they are consumed.
-//  2. Cq, Ck on the wave's 32 value columns.
-//  3. [X; M] W as one bf16x3 MFMA product (hi*hi + hi*lo + lo*hi) whose A
-//     operand is W in the accumulator layout of phase 2, read with the node
-//     permutation that layout implies; the product comes out transposed, so
-//     vn and o leave through LDS as whole row pieces.
+//     off-diagonal blocks X_ij = -D_i sum_m A_im X_mj by fp32 MFMA), then
+//     the masked, scaled Gram Pq into the LDS that A held; X and Pq are kept
+//     as bf16 hi/lo operand pairs from here on (split once, not per wave).
+//  2. Cq, Ck on the wave's value columns.
+//  3. vn = X W, then o = cO Cq + Pq vn (o = cO Cq + M W with M = Pq X, whose
+//     N^3 product is never formed), each a bf16x3 MFMA product (hi*hi +
+//     hi*lo + lo*hi) whose A operand is the right factor in the accumulator
+//     layout of phase 2, read with the node permutation that layout implies;
+//     the products come out transposed, so vn and o leave through LDS as
+//     whole row pieces.
 // Every wave streams its own columns of the state; LDS holds the q/k/v rows
 // and the per-head O(N^2) arrays.  The fused commit -> verify form commits
 // the previous step's accepted path into the tile as soon as it has landed
@@ -58,6 +61,15 @@ constexpr int WavesFor() { return NP > 32 ? 8 : 4; }
 // 16 consecutive rows on distinct banks without padding, so a row group is
 // one contiguous 1 KiB block that a single global->LDS load fills.
 __device__ __forceinline__ int qkv_at(int i, int c) { return i * kD + ((((c >> 3) ^ i) & 15) << 3) + (c & 7); }
+// The MFMA operand reads of these rows, lane (n, g) at row 16mt + n, with the
+// swizzle's lane part computed once: row 16mt + n adds the constant 16mt kD,
+// and k-step s (columns + 32s) flips chunk bits 2-3, i.e. offset ^ 32s.
+//   qkv_op8(n, g):  columns 8g .. + 7          (qkv_at(16mt + n, 32s + 8g) = 16mt kD + (off ^ 32s))
+//   qkv_op4(n, g):  columns 4g .. + 3, and at off ^ 16 columns 16 + 4g .. + 3
+__device__ __forceinline__ int qkv_op8(int n16, int g4) { return (n16 * kD) | (((g4 ^ n16) & 15) << 3); }
+__device__ __forceinline__ int qkv_op4(int n16, int g4) {
+  return (n16 * kD) | (4 * (g4 & 1)) | ((((g4 >> 1) ^ n16) & 15) << 3);
+}
 
 // s_waitcnt immediate (gfx9 encoding): wait until at most vm vector-memory
 // and lgkm LDS/scalar operations of this wave are outstanding
@@ -217,8 +229,10 @@ struct VerifySmem : VRegion<NP, (NP > 32)> {
   static constexpr int LDA = NP + 4;  // fp32 row pitch, rows 16-byte aligned
   static constexpr bool kLateV = NP > 32;
   uint16_t q[NP * kD], k[NP * kD];
-  // am (at[m][i] = A[i][m] until X is formed, then M[i][j]) and x (X[i][j]),
-  // one array so that the 16 staged path keys can span both
+  // am (at[m][i] = A[i][m] until X is formed, then Pq[i][j]) and x (X[i][j]),
+  // one array so that the 16 staged path keys can span both; Pq and, once
+  // every level is formed, X are held in the split operand layout of phase_pq
+  // (the same 4 bytes per element)
   alignas(16) float amx[2 * NP * LDA];
   float gc[NP];        // g, then e^G rk once G is formed
   float G[NP], beta[NP], rq[NP], rk[NP], cO[NP];
@@ -822,8 +836,8 @@ __device__ __forceinline__ void phase_saves(const VerifyParams& P, const Item& i
 // (b, b) and solves it at once by forward substitution (lane j = column j):
 // the solve reads only LDS this wave wrote, and one wave's LDS operations
 // are ordered, so no workgroup barrier stands between the two.  The
-// off-diagonal tiles follow, spread over the waves.  Pq is not stored:
-// phase_m forms its tiles as it needs them.
+// off-diagonal tiles follow, spread over the waves.  Pq is formed after the
+// off-diagonal levels (phase_pq), in the LDS that A holds until then.
 //
 // Of X above its diagonal blocks only blocks (b, b + 1), b even, are ever
 // read: phase_out's 32-wide k-steps pair block columns 2s and 2s + 1 and skip
@@ -831,11 +845,12 @@ __device__ __forceinline__ void phase_saves(const VerifyParams& P, const Item& i
 template <int NP, class RW, class WK>
 __device__ __forceinline__ void a_tile(const RW& rw, WK& wk, int ti, int tj, int n16, int g4) {
   constexpr int LDA = WK::LDA;
+  const int op = qkv_op8(n16, g4);
   f32x4 acc = {};
 #pragma unroll
   for (int s = 0; s < 4; ++s) {
-    const bf16x8 av = *reinterpret_cast<const bf16x8*>(rw.k + qkv_at(16 * ti + n16, 32 * s + 8 * g4));
-    const bf16x8 bv = *reinterpret_cast<const bf16x8*>(rw.k + qkv_at(16 * tj + n16, 32 * s + 8 * g4));
+    const bf16x8 av = *reinterpret_cast<const bf16x8*>(rw.k + 16 * ti * kD + (op ^ (32 * s)));
+    const bf16x8 bv = *reinterpret_cast<const bf16x8*>(rw.k + 16 * tj * kD + (op ^ (32 * s)));
     acc = mfma_bf16_16x16x32(av, bv, acc);
   }
   const int j = 16 * tj + n16;
@@ -901,19 +916,19 @@ __device__ __forceinline__ void phase_offdiag(int tid, int d, WK& wk, int mtn) {
   }
 }
 
-// Pq(bi, bm) for phase_m, in the A-operand layout of the fp32 16x16x4 MFMA
-// whose k-step s covers column 16bm + 4g + s: the Gram of the k rows of
-// block bm against the q rows of block bi.  The operands are swapped so the
+// Pq(bi, bm): the Gram of the k rows of block bm against the q rows of
+// block bi, lane (n, g) holding row 16bi + n at columns 16bm + 4g .. + 3.  The operands are swapped so the
 // tile comes out transposed (lane (n, g), element r -> i = 16bi + n,
 // j = 16bm + 4g + r), then masked to ancestors-or-self and scaled by
 // rq_i rk_j e^{G_i - G_j}.
 template <class RW, class WK>
 __device__ __forceinline__ f32x4 pq_tile(const RW& rw, const WK& wk, int bi, int bm, int n16, int g4) {
+  const int op = qkv_op8(n16, g4);
   f32x4 acc = {};
 #pragma unroll
   for (int s = 0; s < 4; ++s) {
-    const bf16x8 kv = *reinterpret_cast<const bf16x8*>(rw.k + qkv_at(16 * bm + n16, 32 * s + 8 * g4));
-    const bf16x8 qv = *reinterpret_cast<const bf16x8*>(rw.q + qkv_at(16 * bi + n16, 32 * s + 8 * g4));
+    const bf16x8 kv = *reinterpret_cast<const bf16x8*>(rw.k + 16 * bm * kD + (op ^ (32 * s)));
+    const bf16x8 qv = *reinterpret_cast<const bf16x8*>(rw.q + 16 * bi * kD + (op ^ (32 * s)));
     acc = mfma_bf16_16x16x32(kv, qv, acc);
   }
   const int i = 16 * bi + n16;
@@ -928,54 +943,81 @@ __device__ __forceinline__ f32x4 pq_tile(const RW& rw, const WK& wk, int bi, int
   return out;
 }
 
-// Wave that forms M block (bi, bj).  Block (bi, bj <= bi) sums bi - bj + 1
-// Pq X terms.  For 2 x 2 blocks every wave takes one block; for 4 x 4 (20
-// terms) every wave takes 5, where a column per wave would give wave 0 ten.
-// With 8 waves and 4 x 4 blocks the largest block (4 terms) sets the pace:
-// every other wave takes at most 3 terms (and the two zero blocks).
-template <int MT, int NW>
-__device__ __forceinline__ constexpr int m_owner(int bi, int bj) {
-  if constexpr (MT == 4 && NW == 8) {
-    constexpr int own[4][4] = {{6, 3, 0, 0}, {3, 6, 0, 0}, {1, 4, 7, 4}, {0, 2, 5, 7}};
-    return own[bi][bj];
-  } else if constexpr (MT == 4) {
-    constexpr int own[4][4] = {{0, 1, 2, 3}, {1, 3, 0, 1}, {2, 3, 3, 2}, {0, 1, 2, 3}};
-    return own[bi][bj];
-  } else {
-    return (bi * MT + bj) % NW;
-  }
+// The output products read X and Pq as bf16 hi/lo operand pairs, split once
+// here rather than by every wave: in row i, the 32 floats of k-step ks hold
+// four 32-byte chunks, chunk g = the 8 hi then the 8 lo halves of columns
+// 32ks + 4g .. + 3 and 32ks + 16 + 4g .. + 3 (the order of one MFMA operand),
+// so an operand is two 16-byte reads at float 32ks + 8g and 32ks + 8g + 4.
+__device__ __forceinline__ void split_bf16x4(f32x4 x, uint2& hi, uint2& lo) {
+  const float xs[8] = {x[0], x[1], x[2], x[3], 0.f, 0.f, 0.f, 0.f};
+  bf16x8 h, l;
+  split_bf16x8(xs, h, l);
+  const u32x4 hw = __builtin_bit_cast(u32x4, h), lw = __builtin_bit_cast(u32x4, l);
+  hi = uint2{hw[0], hw[1]};
+  lo = uint2{lw[0], lw[1]};
 }
 
-// 1e: M = Pq X (block lower triangular; overwrites A).  A block's Pq tiles are
-// formed in registers (pq_tile) and fed straight to the MFMA, so Pq never
-// takes LDS; a tile shared by several M blocks of different waves is formed
-// once per block.  Above the diagonal only the zero blocks (b, b + 1), b
-// even, are written: phase_out reads no others (as for X).
+// 1e: Pq into am, which A no longer needs (the last off-diagonal level has
+// read it), in the split operand layout: the blocks (bi, bm <= bi) and the
+// zero blocks (b, b + 1), b even, that the output products' 32-wide k-steps
+// also read.  Lane (n, g) of tile (bi, bm) holds columns 16bm + 4g .. + 3 of
+// row 16bi + n: half bm & 1 of chunk g of k-step bm / 2.  The output takes
+// o = cO Cq + Pq vn, which equals cO Cq + M W with M = Pq X because
+// vn = X W: the N^3 product M = Pq X is never formed.  Tiles are dealt to
+// the waves round robin; rows of padding tiles are skipped.
 template <int NP, int NW, class RW, class WK>
-__device__ __forceinline__ void phase_m(int tid, const RW& rw, WK& wk, int mtn) {
+__device__ __forceinline__ void phase_pq(int tid, const RW& rw, WK& wk, int mtn) {
   constexpr int MT = NP / 16;
   constexpr int LDA = WK::LDA;
   const int lane = tid & 63, wave = tid >> 6, n16 = lane & 15, g4 = lane >> 4;
+  int item = 0;
 #pragma unroll
   for (int bi = 0; bi < MT; ++bi) {
     if (bi >= mtn) break;  // padding rows: never read
 #pragma unroll
-    for (int bj = 0; bj < MT; ++bj) {
-      if (bj > bi && (bj != bi + 1 || (bi & 1))) continue;
-      if (m_owner<MT, NW>(bi, bj) != wave) continue;
-      f32x4 acc = {};
-      if (bj <= bi) {
-#pragma unroll
-        for (int bm = 0; bm < MT; ++bm) {
-          if (bm < bj || bm > bi) continue;
-          const f32x4 a = pq_tile(rw, wk, bi, bm, n16, g4);
-#pragma unroll
-          for (int s = 0; s < 4; ++s) acc = mfma_f32_16x16x4(a[s], wk.x()[(16 * bm + 4 * g4 + s) * LDA + 16 * bj + n16], acc);
-        }
-      }
-      store_block<LDA>(wk.am(), bi, bj, acc, n16, g4);
+    for (int bm = 0; bm < MT; ++bm) {
+      if (bm > bi && (bm != bi + 1 || (bi & 1))) continue;
+      if (item++ % NW != wave) continue;
+      const f32x4 t = bm <= bi ? pq_tile(rw, wk, bi, bm, n16, g4) : f32x4{};
+      uint2 hi, lo;
+      split_bf16x4(t, hi, lo);
+      float* chunk = &wk.am()[(16 * bi + n16) * LDA + 32 * (bm >> 1) + 8 * g4 + 2 * (bm & 1)];
+      *reinterpret_cast<uint2*>(chunk) = hi;
+      *reinterpret_cast<uint2*>(chunk + 4) = lo;
     }
   }
+}
+
+// 1e': X into the split operand layout, in place.  The 4 lanes of one
+// (row, k-step) read its 32 floats before any of them writes (one wave, one
+// read instruction before the write: a wave's LDS operations run in order).
+// Rows < 32 need k-step 0 only (the products skip the steps wholly above the
+// diagonal), rows 32 .. 63 both; rows of padding tiles are skipped.
+template <int NP, int NW, class WK>
+__device__ __forceinline__ void phase_split_x(int tid, WK& wk, int mtn) {
+  constexpr int LDA = WK::LDA;
+  constexpr int U0 = 4 * (NP < 32 ? NP : 32);
+  constexpr int U = U0 + (NP > 32 ? 8 * (NP - 32) : 0);
+  static_assert(U <= Waves<NW>::NT && U0 % 64 == 0, "one unit per thread, whole waves per row range");
+  if (tid >= U) return;
+  int i, ks;
+  if (tid < U0) {
+    i = tid >> 2;
+    ks = 0;
+  } else {
+    i = 32 + ((tid - U0) >> 3);
+    ks = ((tid - U0) >> 2) & 1;
+  }
+  const int g = tid & 3;
+  if (i >= 16 * mtn) return;
+  float* row = wk.x() + i * LDA + 32 * ks;
+  float a8[8];
+  lds_f32x8_split(row, 4 * g, a8);
+  asm volatile("" ::: "memory");  // every lane's reads stay before the writes
+  bf16x8 hi, lo;
+  split_bf16x8(a8, hi, lo);
+  *reinterpret_cast<bf16x8*>(row + 8 * g) = hi;
+  *reinterpret_cast<bf16x8*>(row + 8 * g + 4) = lo;
 }
 
 // 2: Cq = q_raw S0, Ck = k_raw S0 for the wave's 32 columns.  k-step s, lane
@@ -995,6 +1037,7 @@ __device__ __forceinline__ void phase_cq_ck(int lane, const RW& rw, const f32x4 
   constexpr int MT = NP / 16;
   constexpr bool DQ = (WHICH & 1) != 0, DK = (WHICH & 2) != 0;
   const int n16 = lane & 15, g4 = lane >> 4;
+  const int op = qkv_op4(n16, g4);
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
@@ -1011,13 +1054,13 @@ __device__ __forceinline__ void phase_cq_ck(int lane, const RW& rw, const f32x4 
                            s0r[t][2 * s + 1][0], s0r[t][2 * s + 1][1], s0r[t][2 * s + 1][2], s0r[t][2 * s + 1][3]};
       split_bf16x8(xs, bhi[t], blo[t]);
     }
+    const int o1 = op ^ (32 * s), o2 = op ^ (32 * s + 16);  // columns 32s + 4g .., 32s + 16 + 4g ..
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
       if (mt >= mtn) break;  // padding rows stay zero
-      const int row = 16 * mt + n16, c0 = 32 * s + 4 * g4;
       bf16x8 aq{}, ak{};
-      if (DQ) aq = lds_bf16x8_split(rw.q + qkv_at(row, c0), rw.q + qkv_at(row, c0 + 16));
-      if (DK) ak = lds_bf16x8_split(rw.k + qkv_at(row, c0), rw.k + qkv_at(row, c0 + 16));
+      if (DQ) aq = lds_bf16x8_split(rw.q + 16 * mt * kD + o1, rw.q + 16 * mt * kD + o2);
+      if (DK) ak = lds_bf16x8_split(rw.k + 16 * mt * kD + o1, rw.k + 16 * mt * kD + o2);
 #pragma unroll
       for (int t = 0; t < TT; ++t) {
         if (DQ) cq[mt][t] = mfma_bf16_16x16x32(bhi[t], aq, cq[mt][t]);
@@ -1056,11 +1099,13 @@ __device__ __forceinline__ void phase_w(int lane, int wave, const RW& rw, const 
     }
 }
 
-// 3b: [X; M] W, tiles mo < MT give vn and tiles mo >= MT give M W (o adds
-// cO * Cq); every wave does its vn tiles before its o tiles.  Computed transposed (W as the A operand), so lane (n, g) holds
-// node 16mt + n at the four consecutive columns 16t + 4g .. +3: one 16-byte
-// (vn) or 8-byte (o) write each.  Staged into the (then free) q/k/v region of
-// rw when the flags allow, else stored directly.
+// 3b: vn = X W, then o = cO Cq + Pq vn.  Both products are computed
+// transposed, the left factor (W, then vn) as the A operand, so lane (n, g)
+// holds node 16mt + n at the four consecutive columns 16t + 4g .. +3: one
+// 16-byte (vn) or 8-byte (o) write each.  vn always goes to its staging rows
+// in the (then free) q/k region, from which each wave reads its own columns
+// back in W's operand layout; vn and o leave through LDS when the flags
+// allow, else they are stored directly.
 template <int NP, int NW, class RW, class WK>
 __device__ __forceinline__ void phase_out(const VerifyParams& P, const Item& it, int lane, int wave, RW& rw,
                                           const WK& wk, const f32x4 (&cq)[NP / 16][Waves<NW>::TT],
@@ -1074,57 +1119,83 @@ __device__ __forceinline__ void phase_out(const VerifyParams& P, const Item& it,
   const int n16 = lane & 15, g4 = lane >> 4;
   float* vn_s = reinterpret_cast<float*>(rw.q);  // spans q and k
   uint16_t* o_s = rw.ostage();
-#pragma unroll
-  for (int mo = 0; mo < 2 * MT; ++mo) {
-    // the late-v form stages o in x: every wave must be done with X first
-    if constexpr (RW::kLateV)
-      if (mo == MT) __syncthreads();
-    const int mt = mo % MT;
-    if (mt >= mtn) continue;  // padding rows: not stored
-    const float* src = mo < MT ? wk.x() : wk.am();
-    f32x4 acc[TT];
+  // tile mt of [F; V] (F = X or Pq in the split operand layout, V = W or
+  // vn): lane (n, g) gets node 16mt + n
+  auto product = [&](const float* f, const bf16x8 (&vh)[KS][TT], const bf16x8 (&vl)[KS][TT], int mt, f32x4 (&acc)[TT]) {
 #pragma unroll
     for (int t = 0; t < TT; ++t) acc[t] = f32x4{};
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
       if (32 * ks > 16 * mt + 15) continue;  // both factors are lower triangular
-      float a8[8];
-      lds_f32x8_split(src + (16 * mt + n16) * LDA, 32 * ks + 4 * g4, a8);
-      bf16x8 ah, al;
-      split_bf16x8(a8, ah, al);
+      const float* chunk = f + (16 * mt + n16) * LDA + 32 * ks + 8 * g4;
+      const bf16x8 ah = *reinterpret_cast<const bf16x8*>(chunk);
+      const bf16x8 al = *reinterpret_cast<const bf16x8*>(chunk + 4);
 #pragma unroll
       for (int t = 0; t < TT; ++t) {
-        acc[t] = mfma_bf16_16x16x32(wh[ks][t], ah, acc[t]);
-        acc[t] = mfma_bf16_16x16x32(wl[ks][t], ah, acc[t]);
-        acc[t] = mfma_bf16_16x16x32(wh[ks][t], al, acc[t]);
+        acc[t] = mfma_bf16_16x16x32(vh[ks][t], ah, acc[t]);
+        acc[t] = mfma_bf16_16x16x32(vl[ks][t], ah, acc[t]);
+        acc[t] = mfma_bf16_16x16x32(vh[ks][t], al, acc[t]);
       }
     }
+  };
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    if (mt >= mtn) break;  // padding rows: not stored
+    f32x4 acc[TT];
+    product(wk.x(), wh, wl, mt, acc);
     const int i = 16 * mt + n16;
 #pragma unroll
     for (int t = 0; t < TT; ++t) {
       const int col = CW * wave + 16 * t + 4 * g4;
-      if (mo < MT) {
-        if (P.vn_stage) {
-          *reinterpret_cast<f32x4*>(&vn_s[vn_at(i, col)]) = acc[t];
-        } else if (p.aux_v && i < it.n) {
-          float* dst = p.aux_v + (int64_t)it.h * p.aux_v_h_stride + (it.row0 + i) * p.aux_v_row_stride + col;
+      *reinterpret_cast<f32x4*>(&vn_s[vn_at(i, col)]) = acc[t];
+      if (!P.vn_stage && p.aux_v && i < it.n) {
+        float* dst = p.aux_v + (int64_t)it.h * p.aux_v_h_stride + (it.row0 + i) * p.aux_v_row_stride + col;
 #pragma unroll
-          for (int r = 0; r < 4; ++r) dst[r] = acc[t][r];
-        }
-      } else {
-        const f32x4 ov = wk.cO[i] * cq[mt][t] + acc[t];
-        if (P.o_stage) {
-          const bf16x2 lo = __builtin_convertvector((f32x2{ov[0], ov[1]}), bf16x2);  // round to nearest even
-          const bf16x2 hi = __builtin_convertvector((f32x2{ov[2], ov[3]}), bf16x2);
-          uint2 w;
-          __builtin_memcpy(&w.x, &lo, 4);
-          __builtin_memcpy(&w.y, &hi, 4);
-          *reinterpret_cast<uint2*>(&o_s[qkv_at(i, col)]) = w;
-        } else if (i < it.n) {
+        for (int r = 0; r < 4; ++r) dst[r] = acc[t][r];
+      }
+    }
+  }
+  // vn back in W's layout (k-step ks, lane (n, g), element e -> node
+  // 32ks + 4g + e (e < 4), 32ks + 16 + 4g + e-4; column 16t + n), the wave's
+  // own columns only (its LDS writes are ordered before these reads); rows
+  // past the tree are zero
+  bf16x8 vh[KS][TT], vl[KS][TT];
 #pragma unroll
-          for (int r = 0; r < 4; ++r)
-            st_f(p.o, (it.row0 + i) * p.o_row_stride + (int64_t)it.h * p.o_h_stride + col + r, p.o_dtype, ov[r]);
-        }
+  for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+    for (int t = 0; t < TT; ++t) {
+      const int col = CW * wave + 16 * t + n16;
+      float v8[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int i = 32 * ks + 16 * (e >> 2) + 4 * g4 + (e & 3);
+        v8[e] = i < it.n ? vn_s[vn_at(i, col)] : 0.f;
+      }
+      split_bf16x8(v8, vh[ks][t], vl[ks][t]);
+    }
+  // the late-v form stages o in x: every wave must be done with X first
+  if constexpr (RW::kLateV) __syncthreads();
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    if (mt >= mtn) break;
+    f32x4 acc[TT];
+    product(wk.am(), vh, vl, mt, acc);
+    const int i = 16 * mt + n16;
+#pragma unroll
+    for (int t = 0; t < TT; ++t) {
+      const int col = CW * wave + 16 * t + 4 * g4;
+      const f32x4 ov = wk.cO[i] * cq[mt][t] + acc[t];
+      if (P.o_stage) {
+        const bf16x2 lo = __builtin_convertvector((f32x2{ov[0], ov[1]}), bf16x2);  // round to nearest even
+        const bf16x2 hi = __builtin_convertvector((f32x2{ov[2], ov[3]}), bf16x2);
+        uint2 w;
+        __builtin_memcpy(&w.x, &lo, 4);
+        __builtin_memcpy(&w.y, &hi, 4);
+        *reinterpret_cast<uint2*>(&o_s[qkv_at(i, col)]) = w;
+      } else if (i < it.n) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          st_f(p.o, (it.row0 + i) * p.o_row_stride + (int64_t)it.h * p.o_h_stride + col + r, p.o_dtype, ov[r]);
       }
     }
   }
@@ -1316,21 +1387,22 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
     __syncthreads();
   }
   if constexpr (kSplit) issue_state_group<false, NW>(S0, p.state_v_stride, wave, lane, 3, s0r);
-  phase_m<NP, NW>(tid, sm, sm, mtn);
+  phase_pq<NP, NW>(tid, sm, sm, mtn);
+  phase_split_x<NP, NW>(tid, sm, mtn);
 
   f32x4 cq[MT][TT], ck[MT][TT];
   if constexpr (VerifySmem<NP>::kLateV) {
     // Cq first; once every wave is done with the q rows, the v rows are
     // copied into their region while Ck computes
     phase_cq_ck<NP, 1, NW>(lane, sm, s0r, cq, ck, mtn);
-    __syncthreads();  // X and M complete, the q rows consumed
+    __syncthreads();  // X and Pq complete, the q rows consumed
     issue_rows<NP, 2, 3, NW>(p, it, wave, lane, S0, sm);
     phase_cq_ck<NP, 2, NW>(lane, sm, s0r, cq, ck, mtn);
     __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 15));  // the v row copies (untracked by the backend)
     __syncthreads();
   } else {
     phase_cq_ck<NP, 3, NW>(lane, sm, s0r, cq, ck, mtn);
-    __syncthreads();  // X and M complete
+    __syncthreads();  // X and Pq complete
   }
   bf16x8 wh[NP / 32][TT], wl[NP / 32][TT];
   phase_w<NP, NW>(lane, wave, sm, sm, ck, wh, wl);
