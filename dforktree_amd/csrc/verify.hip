@@ -770,15 +770,15 @@ __device__ __forceinline__ void phase_norms(const dft_verify_args& p, int tid, c
   for (int r0 = 0; r0 < 2 * NP; r0 += NT / 4) {
     const int r = r0 + (tid >> 2), qd = tid & 3, i = r % NP;
     const uint16_t* rows = r < NP ? rw.q : rw.k;
-    float ss = 0.f;
+    float ss = 0.f;  // bf16 pair dot products, accumulated in fp32
 #pragma unroll
     for (int c = 32 * qd; c < 32 * qd + 32; c += 8) {
       const uint4 u = *reinterpret_cast<const uint4*>(rows + qkv_at(i, c));
       const uint32_t w[4] = {u.x, u.y, u.z, u.w};
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const float lo = __uint_as_float(w[e] << 16), hi = __uint_as_float(w[e] & 0xffff0000u);
-        ss += lo * lo + hi * hi;
+        const bf16x2 v = __builtin_bit_cast(bf16x2, w[e]);
+        ss = __builtin_amdgcn_fdot2_f32_bf16(v, v, ss, false);
       }
     }
     ss += __shfl_xor(ss, 1);
@@ -1157,19 +1157,25 @@ __device__ __forceinline__ void phase_out(const VerifyParams& P, const Item& it,
   }
   // vn back in W's layout (k-step ks, lane (n, g), element e -> node
   // 32ks + 4g + e (e < 4), 32ks + 16 + 4g + e-4; column 16t + n), the wave's
-  // own columns only (its LDS writes are ordered before these reads); rows
-  // past the tree are zero
+  // own columns only (its LDS writes are ordered before these reads).  Rows
+  // of the tree's last tile past the tree are exact zeros (beta = 0 there,
+  // so W and vn are), and Pq is zero in their columns; padding tiles were
+  // never written and are replaced by zeros.  With i = 32ks + 16h + 4g + r,
+  // vn_at(i, c) = 4g kD + (c & 3) + (32ks + 16h + r) kD + (lane chunk ^ (16h + r)) * 4.
   bf16x8 vh[KS][TT], vl[KS][TT];
 #pragma unroll
   for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
     for (int t = 0; t < TT; ++t) {
       const int col = CW * wave + 16 * t + n16;
+      const float* base = vn_s + 4 * g4 * kD + (col & 3);
+      const int ch = ((col >> 2) ^ (4 * g4)) & 31;
       float v8[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const int i = 32 * ks + 16 * (e >> 2) + 4 * g4 + (e & 3);
-        v8[e] = i < it.n ? vn_s[vn_at(i, col)] : 0.f;
+        const int h = e >> 2, r = e & 3;
+        const float v = base[(32 * ks + 16 * h + r) * kD + ((ch ^ (16 * h + r)) << 2)];
+        v8[e] = 2 * ks + h < mtn ? v : 0.f;  // uniform
       }
       split_bf16x8(v8, vh[ks][t], vl[ks][t]);
     }
