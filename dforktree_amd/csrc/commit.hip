@@ -22,6 +22,13 @@ struct CommitParams {
   int src_vec, dst_vec;  // 16-byte vector path usable
 };
 
+// a value the workgroup agrees on, as a scalar
+__device__ __forceinline__ int64_t uniform64(int64_t v) {
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)((uint64_t)v >> 32));
+  return (int64_t)(((uint64_t)hi << 32) | lo);
+}
+
 // path entries of request b that count (path_len, or all path_cols)
 __device__ __forceinline__ int path_entries(const dft_commit_args& p, int b) {
   int len = p.path_cols;
@@ -46,13 +53,10 @@ __device__ __forceinline__ void commit_status(const dft_commit_args& p, int b, i
 
 // Five waves per SIMD (five workgroups per CU instead of four, 64 KiB more
 // state in flight per CU): 48.3 -> 46.4 us per layer at batch 64 in
-// interleaved runs.  At the 96-register budget this takes, 14 registers are
-// spilled (values of the element-wise path for layouts without 16-byte rows
-// among them); their stores add about 11% to the launch's HBM writes, and
-// the kernel is still faster.  Forms without the spills measured slower:
-// a separate 16-byte-only instantiation (47.3 us), 128-float rows addressed
-// by immediate offsets (48.9 us), the path entries read before the tile
-// (47.0 us).
+// interleaved runs.  The tile takes 64 of the 96 registers this leaves; the
+// element-wise paths (layouts without 16-byte rows) walk a row pointer and
+// the slot indices are scalars, so that no row index or slot is held in
+// vector registers through the update and nothing is spilled.
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(5)))
 tree_commit_kernel(const CommitParams P) {
   const dft_commit_args& p = P.a;
@@ -97,6 +101,10 @@ tree_commit_kernel(const CommitParams P) {
   if (p.dst_slots) dslot = ld_i(p.dst_slots, b, p.dst_slots_dtype);
   if (dslot < 0) return;
   if (slot < 0) slot = 0;
+  // uniform over the workgroup: scalar registers, not two vector ones held
+  // through the update
+  slot = uniform64(slot);
+  dslot = uniform64(dslot);
 
   // ---- state tile: thread owns rows 16*rg .. 16*rg+15, cols 4*c4 .. 4*c4+3
   const int c4 = tid & 31, rg = tid >> 5;
@@ -107,12 +115,12 @@ tree_commit_kernel(const CommitParams P) {
     for (int m = 0; m < 16; ++m)
       st[m] = __builtin_nontemporal_load(
           reinterpret_cast<const f32x4*>(srcp + (int64_t)(16 * rg + m) * p.src_row_stride + 4 * c4));
-  } else {
+  } else {  // element loads, walking the rows (no per-row index is kept live)
+    const float* rowp = srcp + (int64_t)(16 * rg) * p.src_row_stride + (int64_t)(4 * c4) * p.src_col_stride;
 #pragma unroll
-    for (int m = 0; m < 16; ++m)
+    for (int m = 0; m < 16; ++m, rowp += p.src_row_stride)
 #pragma unroll
-      for (int q = 0; q < 4; ++q)
-        st[m][q] = srcp[(int64_t)(16 * rg + m) * p.src_row_stride + (int64_t)(4 * c4 + q) * p.src_col_stride];
+      for (int q = 0; q < 4; ++q) st[m][q] = rowp[(int64_t)q * p.src_col_stride];
   }
 
   // ---- path bookkeeping on wave 0: the nodes that contribute, in path order
@@ -176,11 +184,12 @@ tree_commit_kernel(const CommitParams P) {
   for (int t = 0; t < T; ++t) {
     const f32x4 cc = *reinterpret_cast<const f32x4*>(&cv[t * kCD + 4 * c4]);
     const f32x4* rp = reinterpret_cast<const f32x4*>(&rv[t * kCD + 16 * rg]);
-    const f32x4 r0 = rp[0], r1 = rp[1], r2 = rp[2], r3 = rp[3];
-    const float rvals[16] = {r0.x, r0.y, r0.z, r0.w, r1.x, r1.y, r1.z, r1.w,
-                             r2.x, r2.y, r2.z, r2.w, r3.x, r3.y, r3.z, r3.w};
 #pragma unroll
-    for (int m = 0; m < 16; ++m) st[m] += rvals[m] * cc;
+    for (int q = 0; q < 4; ++q) {
+      const f32x4 r = rp[q];
+#pragma unroll
+      for (int m = 0; m < 4; ++m) st[4 * q + m] += r[m] * cc;
+    }
   }
 
   float* dstp = p.dst + (int64_t)l * p.dst_layer_stride + dslot * p.dst_slot_stride + (int64_t)u * p.dst_node_stride +
@@ -190,11 +199,11 @@ tree_commit_kernel(const CommitParams P) {
     for (int m = 0; m < 16; ++m)
       __builtin_nontemporal_store(st[m], reinterpret_cast<f32x4*>(dstp + (int64_t)(16 * rg + m) * p.dst_row_stride + 4 * c4));
   } else {
+    float* rowp = dstp + (int64_t)(16 * rg) * p.dst_row_stride + (int64_t)(4 * c4) * p.dst_col_stride;
 #pragma unroll
-    for (int m = 0; m < 16; ++m)
+    for (int m = 0; m < 16; ++m, rowp += p.dst_row_stride)
 #pragma unroll
-      for (int q = 0; q < 4; ++q)
-        dstp[(int64_t)(16 * rg + m) * p.dst_row_stride + (int64_t)(4 * c4 + q) * p.dst_col_stride] = st[m][q];
+      for (int q = 0; q < 4; ++q) rowp[(int64_t)q * p.dst_col_stride] = st[m][q];
   }
 }
 
