@@ -234,9 +234,14 @@ struct VerifySmem : VRegion<NP, (NP > 32)> {
   // every level is formed, X are held in the split operand layout of phase_pq
   // (the same 4 bytes per element)
   alignas(16) float amx[2 * NP * LDA];
-  float gc[NP];        // g, then e^G rk once G is formed
-  float G[NP], beta[NP], rq[NP], rk[NP], cO[NP];
-  uint64_t anc[NP];
+  // per-node arrays, 16-byte aligned: the tile epilogues read 4 consecutive nodes at once
+  alignas(16) float gc[NP];  // g, then e^G rk once G is formed
+  alignas(16) float G[NP];
+  alignas(16) float beta[NP];
+  alignas(16) float rq[NP];
+  alignas(16) float rk[NP];
+  alignas(16) float cO[NP];
+  alignas(16) uint64_t anc[NP];
   uint32_t graw[6][64];  // per lane of wave 0: words of a, b, ancestry bits lo / hi, dt_bias, decay
   __device__ float* am() { return amx; }
   __device__ const float* am() const { return amx; }
@@ -853,14 +858,22 @@ __device__ __forceinline__ void a_tile(const RW& rw, WK& wk, int ti, int tj, int
     const bf16x8 bv = *reinterpret_cast<const bf16x8*>(rw.k + 16 * tj * kD + (op ^ (32 * s)));
     acc = mfma_bf16_16x16x32(av, bv, acc);
   }
-  const int j = 16 * tj + n16;
+  // nodes i0 .. i0 + 3 of this lane: their per-node values in one read each,
+  // then selects (no load under a branch), then one 16-byte store
+  const int j = 16 * tj + n16, i0 = 16 * ti + 4 * g4;
   const float rkj = wk.rk[j], Gj = wk.G[j];
+  const f32x4 bi = *reinterpret_cast<const f32x4*>(&wk.beta[i0]);
+  const f32x4 ri = *reinterpret_cast<const f32x4*>(&wk.rk[i0]);
+  const f32x4 gi = *reinterpret_cast<const f32x4*>(&wk.G[i0]);
+  f32x4 out;
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
-    const int i = 16 * ti + 4 * g4 + r;
-    const bool on = (wk.anc[i] >> j) & 1ull;
-    wk.am()[j * LDA + i] = (on && j < i) ? wk.beta[i] * wk.rk[i] * rkj * acc[r] * __expf(wk.G[i] - Gj) : 0.f;
+    const int i = i0 + r;
+    const bool on = ((wk.anc[i] >> j) & 1ull) && j < i;
+    const float v = bi[r] * ri[r] * rkj * acc[r] * __expf(gi[r] - Gj);
+    out[r] = on ? v : 0.f;
   }
+  *reinterpret_cast<f32x4*>(&wk.am()[j * LDA + i0]) = out;
 }
 
 // mtn: 16-row tiles that hold nodes (the rest are padding and are skipped)
@@ -931,14 +944,16 @@ __device__ __forceinline__ f32x4 pq_tile(const RW& rw, const WK& wk, int bi, int
     const bf16x8 qv = *reinterpret_cast<const bf16x8*>(rw.q + 16 * bi * kD + (op ^ (32 * s)));
     acc = mfma_bf16_16x16x32(kv, qv, acc);
   }
-  const int i = 16 * bi + n16;
+  const int i = 16 * bi + n16, j0 = 16 * bm + 4 * g4;
   const uint64_t ai = wk.anc[i];
   const float rqi = wk.rq[i], Gi = wk.G[i];
+  const f32x4 rkj = *reinterpret_cast<const f32x4*>(&wk.rk[j0]);
+  const f32x4 gj = *reinterpret_cast<const f32x4*>(&wk.G[j0]);
   f32x4 out;
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
-    const int j = 16 * bm + 4 * g4 + r;
-    out[r] = ((ai >> j) & 1ull) ? rqi * wk.rk[j] * acc[r] * __expf(Gi - wk.G[j]) : 0.f;
+    const float v = rqi * rkj[r] * acc[r] * __expf(Gi - gj[r]);
+    out[r] = ((ai >> (j0 + r)) & 1ull) ? v : 0.f;
   }
   return out;
 }
@@ -1083,20 +1098,28 @@ __device__ __forceinline__ void phase_w(int lane, int wave, const RW& rw, const 
   constexpr int KS = NP / 32;
   const int n16 = lane & 15, g4 = lane >> 4;
 #pragma unroll
-  for (int ks = 0; ks < KS; ++ks)
+  for (int ks = 0; ks < KS; ++ks) {
+    // beta and e^G rk of nodes 16mt + 4g .. + 3, mt = 2ks, 2ks + 1
+    f32x4 bt[2], gcv[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      bt[h] = *reinterpret_cast<const f32x4*>(&wk.beta[16 * (2 * ks + h) + 4 * g4]);
+      gcv[h] = *reinterpret_cast<const f32x4*>(&wk.gc[16 * (2 * ks + h) + 4 * g4]);
+    }
 #pragma unroll
     for (int t = 0; t < TT; ++t) {
       const int col = CW * wave + 16 * t + n16;
       float w8[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const int mt = 2 * ks + (e >> 2), r = e & 3;
+        const int h = e >> 2, mt = 2 * ks + h, r = e & 3;
         const int i = 16 * mt + 4 * g4 + r;
         const float vv = bf16_bits_to_f32(rw.vrows()[qkv_at(i, col)]);
-        w8[e] = wk.beta[i] * (vv - wk.gc[i] * ck[mt][t][r]);
+        w8[e] = bt[h][r] * (vv - gcv[h][r] * ck[mt][t][r]);
       }
       split_bf16x8(w8, wh[ks][t], wl[ks][t]);
     }
+  }
 }
 
 // 3b: vn = X W, then o = cO Cq + Pq vn.  Both products are computed
