@@ -794,14 +794,18 @@ __device__ __forceinline__ void phase_norms(const dft_verify_args& p, int tid, c
       else wk.rk[i] = rn;
     }
   }
-  constexpr int TPN = NT / NP;  // threads per node
+  constexpr int TPN = NT / NP;  // threads per node, each summing NP / TPN consecutive nodes
+  constexpr int JPT = NP / TPN;
+  static_assert(JPT % 4 == 0, "whole 16-byte reads of g");
   const int i = tid / TPN, sub = tid % TPN;
   const uint64_t bits = wk.anc[i];
   float G = 0.f;
 #pragma unroll
-  for (int jj = 0; jj < NP / TPN; ++jj) {
-    const int j = jj * TPN + sub;
-    if ((bits >> j) & 1ull) G += wk.gc[j];
+  for (int q = 0; q < JPT / 4; ++q) {
+    const int j0 = sub * JPT + 4 * q;
+    const f32x4 g = *reinterpret_cast<const f32x4*>(&wk.gc[j0]);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) G += ((bits >> (j0 + e)) & 1ull) ? g[e] : 0.f;
   }
 #pragma unroll
   for (int o = 1; o < TPN; o <<= 1) G += __shfl_xor(G, o);
