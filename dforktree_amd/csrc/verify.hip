@@ -1339,9 +1339,22 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
   // state tile into registers.  Phase 1 only waits for what precedes the
   // state; the state keeps streaming underneath it.
   // (fused form: the pending path's entry words travel in gate row 4)
+  // Fused form: every wave loads the previous step's path entry words first,
+  // decodes them as soon as they land (the gate and row copies issued behind
+  // them need not have) and issues the path's keys, values and gains ahead of
+  // the state tile, so that they are in when the tile is.
+  Pending pd{};
+  f32x4 kr[8 / NW];
+  float vnr[4][TT], gp[4];
+  uint32_t pword = 0;
+  if constexpr (COMMIT) pword = *path_word(P.c, it.b, lane);
   if (wave == 0) issue_gates(p, it, lane, S0, sm.graw, COMMIT ? path_word(P.c, it.b, lane) : nullptr);
   if (p.anc_f32) dense_ancestry<NP, NW>(p, it, wave, lane, sm);
   issue_rows<NP, 0, kPlanes, NW>(p, it, wave, lane, S0, sm);
+  if constexpr (COMMIT) {
+    pd = decode_pending(ph, lane, pword);
+    issue_pending<NW>(P.c, pd, it.h, wave, lane, S0, kr, vnr, gp);
+  }
   asm volatile("" ::: "memory");
 
   f32x4 s0r[TT][8];
@@ -1369,8 +1382,9 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
   asm volatile("" ::: "memory");
 
   if (wave == 0) {
-    // the gate words were wave 0's first copies: wait for them only
-    __builtin_amdgcn_s_waitcnt(waitcnt_imm(kQkvDma + (kSplit ? kGroupLoads : kStateLoads), 15));
+    // the gate words were wave 0's first copies: wait for them only (the
+    // fused form: for everything before the state, the path loads included)
+    __builtin_amdgcn_s_waitcnt(waitcnt_imm(COMMIT ? kStateLoads : kQkvDma + (kSplit ? kGroupLoads : kStateLoads), 15));
     asm volatile("" ::: "memory");
     if (lane < NP) decode_gates(p, it, lane, sm.graw, sm);
   }
@@ -1381,19 +1395,10 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
 
-  // Fused form: the previous step's path (its entry words came with the
-  // gates) is decoded and its keys, values and gains are fetched behind the
-  // state; the norms overlap both streams.  As soon as they have landed the
-  // path is committed into the tile (keys staged in am + x, still unused)
-  // and the tile goes back to its slot, so that the write-back streams under
-  // the rest of phase 1.
-  Pending pd{};
-  f32x4 kr[8 / NW];
-  float vnr[4][TT], gp[4];
-  if constexpr (COMMIT) {
-    pd = decode_pending(ph, lane, sm.graw[4][lane & 15]);
-    issue_pending<NW>(P.c, pd, it.h, wave, lane, S0, kr, vnr, gp);
-  }
+  // Fused form: the norms overlap the state stream.  As soon as the tile has
+  // landed the path is committed into it (keys staged in am + x, still
+  // unused) and the tile goes back to its slot, so that the write-back
+  // streams under the rest of phase 1.
   phase_norms<NP, NW>(p, tid, sm, sm);
   __syncthreads();
   if constexpr (COMMIT) {
