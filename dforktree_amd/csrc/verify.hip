@@ -34,8 +34,10 @@
 //     whole row pieces.
 // Every wave streams its own columns of the state; LDS holds the q/k/v rows
 // and the per-head O(N^2) arrays.  The fused commit -> verify form commits
-// the previous step's accepted path into the tile as soon as it has landed
-// and writes it back before the Gram phase.
+// the previous step's accepted path into the tile and writes it back: the
+// 64-wide form as soon as the tile has landed, before the Gram phase; the
+// 32-wide form after phase 1 (which needs no state), so that phase 1 runs
+// under the state stream and only phases 2-3 follow the write-back.
 #include <climits>
 #include <type_traits>
 
@@ -210,8 +212,10 @@ __device__ __forceinline__ int vn_at(int i, int c) { return i * kD + ((((c >> 2)
 // so the MFMA operand reads of 4 rows x 16 columns hit 64 distinct banks.
 __device__ __forceinline__ int pkey_at(int p, int c) { return p * kD + ((((c >> 2) ^ ((p & 3) << 2)) & 31) << 2) + (c & 3); }
 
-// The fused commit stages the previous step's 16 path keys (16 x 128 floats)
-// in am + x before the Gram tiles are formed; the two arrays are adjacent.
+// The 64-wide fused commit stages the previous step's 16 path keys (16 x 128
+// floats) in am + x before the Gram tiles are formed; the two arrays are
+// adjacent.  The 32-wide one stages them, and then its write-back, in the v
+// region (exactly 16 x 128 floats), before the v rows are copied in.
 //
 // Trees of 33-64 nodes (NP = 64) keep no v region: their v rows are copied
 // into the q region once Cq/Ck have consumed it, and o is staged in x once the
@@ -1295,7 +1299,11 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
   constexpr int MT = NP / 16;
   constexpr int NW = WavesFor<NP>();
   constexpr int TT = Waves<NW>::TT, CW = Waves<NW>::CW;
-  constexpr int kPlanes = VerifySmem<NP>::kLateV ? 2 : 3;  // the late form copies its v rows after Cq/Ck
+  // The 32-wide fused form runs phase 1 (which needs no state) before its
+  // commit, under the state stream, and stages the commit's keys and
+  // write-back in the v region, whose rows it copies in afterwards.
+  constexpr bool kEarly = COMMIT && !VerifySmem<NP>::kLateV;
+  constexpr int kPlanes = (VerifySmem<NP>::kLateV || kEarly) ? 2 : 3;  // the late forms copy v rows later
   constexpr int kQkvDma = kPlanes * (NP / (4 * NW));          // row copies per wave
   constexpr int kStateLoads = 8 * TT, kGroupLoads = 2 * TT;   // per lane: whole tile, one k-step group
   const dft_verify_args& p = P.a;
@@ -1339,19 +1347,21 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
   // state tile into registers.  Phase 1 only waits for what precedes the
   // state; the state keeps streaming underneath it.
   // (fused form: the pending path's entry words travel in gate row 4)
-  // Fused form: every wave loads the previous step's path entry words first,
-  // decodes them as soon as they land (the gate and row copies issued behind
-  // them need not have) and issues the path's keys, values and gains ahead of
-  // the state tile, so that they are in when the tile is.
+  // 64-wide fused form: every wave loads the previous step's path entry words
+  // first, decodes them as soon as they land (the gate and row copies issued
+  // behind them need not have) and issues the path's keys, values and gains
+  // ahead of the state tile, so that they are in when the tile is.  (The
+  // 32-wide form issues them after phase 1: held in registers through phase 1
+  // beside the tile, they would be spilled.)
   Pending pd{};
   f32x4 kr[8 / NW];
   float vnr[4][TT], gp[4];
   uint32_t pword = 0;
-  if constexpr (COMMIT) pword = *path_word(P.c, it.b, lane);
+  if constexpr (COMMIT && !kEarly) pword = *path_word(P.c, it.b, lane);
   if (wave == 0) issue_gates(p, it, lane, S0, sm.graw, COMMIT ? path_word(P.c, it.b, lane) : nullptr);
   if (p.anc_f32) dense_ancestry<NP, NW>(p, it, wave, lane, sm);
   issue_rows<NP, 0, kPlanes, NW>(p, it, wave, lane, S0, sm);
-  if constexpr (COMMIT) {
+  if constexpr (COMMIT && !kEarly) {
     pd = decode_pending(ph, lane, pword);
     issue_pending<NW>(P.c, pd, it.h, wave, lane, S0, kr, vnr, gp);
   }
@@ -1395,13 +1405,13 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
 
-  // Fused form: the norms overlap the state stream.  As soon as the tile has
-  // landed the path is committed into it (keys staged in am + x, still
-  // unused) and the tile goes back to its slot, so that the write-back
+  // 64-wide fused form: the norms overlap the state stream.  As soon as the
+  // tile has landed the path is committed into it (keys staged in am + x,
+  // still unused) and the tile goes back to its slot, so that the write-back
   // streams under the rest of phase 1.
   phase_norms<NP, NW>(p, tid, sm, sm);
   __syncthreads();
-  if constexpr (COMMIT) {
+  if constexpr (COMMIT && !kEarly) {
     commit_tile<NW>(pd, sm.pkey(), kr, vnr, gp, wave, lane, s0r);
     // everything this wave loaded has been consumed: no load is left in
     // flight past the (conditional) write-back
@@ -1427,6 +1437,21 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
   if constexpr (kSplit) issue_state_group<false, NW>(S0, p.state_v_stride, wave, lane, 3, s0r);
   phase_pq<NP, NW>(tid, sm, sm, mtn);
   phase_split_x<NP, NW>(tid, sm, mtn);
+  if constexpr (kEarly) {
+    // the path's entry words came with the gates (row 4); its loads go out
+    // now, so that they are not held in registers through phase 1
+    pd = decode_pending(ph, lane, sm.graw[4][lane & 15]);
+    issue_pending<NW>(P.c, pd, it.h, wave, lane, S0, kr, vnr, gp);
+    float* stage = reinterpret_cast<float*>(sm.vrows());  // 8 KiB: the 16 path keys, then the write-back
+    commit_tile<NW>(pd, stage, kr, vnr, gp, wave, lane, s0r);
+    __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 15));
+    if (pd.last >= 0) {  // uniform over the workgroup (one request)
+      __syncthreads();  // every wave has read the staged keys
+      store_state<NW>(const_cast<float*>(S0), p.state_v_stride, wave, lane, s0r, stage + wave * 512);
+    }
+    __syncthreads();  // every wave has read its staging back: the v region takes the v rows
+    issue_rows<NP, 2, 3, NW>(p, it, wave, lane, S0, sm);
+  }
 
   f32x4 cq[MT][TT], ck[MT][TT];
   if constexpr (VerifySmem<NP>::kLateV) {
@@ -1440,6 +1465,7 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
     __syncthreads();
   } else {
     phase_cq_ck<NP, 3, NW>(lane, sm, s0r, cq, ck, mtn);
+    if constexpr (kEarly) __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 15));  // the v row copies (untracked)
     __syncthreads();  // X and Pq complete
   }
   bf16x8 wh[NP / 32][TT], wl[NP / 32][TT];
