@@ -1,6 +1,7 @@
-// Fused GDN tree verify for gfx950: one workgroup (4 wave64) per
-// (request, v-head) does prepare + (I+A)^-1 + finish of
-// tree_kernels.py:135-208 in a single pass over the recurrent state.
+// Fused GDN tree verify for gfx950: one workgroup per (request, v-head)
+// (4 wave64 for trees of up to 32 nodes, 8 for 33-64) does prepare +
+// (I+A)^-1 + finish of tree_kernels.py:135-208 in a single pass over the
+// recurrent state.
 //
 // Math (per head; q_n = rq q_raw, k_n = rk k_raw with q_raw/k_raw the exact
 // bf16 rows, so every MFMA left operand on the state is exact):
