@@ -914,7 +914,8 @@ __device__ __forceinline__ void phase_gram_diag(int tid, const RW& rw, WK& wk, i
   for (int ti = 1; ti < MT; ++ti)
 #pragma unroll
     for (int tj = 0; tj < ti; ++tj, ++item)
-      if (ti < mtn && (MT + item) % NW == wave) a_tile<NP>(rw, wk, ti, tj, n16, g4);
+      // off the waves that solve a diagonal block when there are spare ones
+      if (ti < mtn && (NW > MT ? MT + item % (NW - MT) : (MT + item) % NW) == wave) a_tile<NP>(rw, wk, ti, tj, n16, g4);
   if (tid < 256)  // one element of each 16 x 16 block per thread
 #pragma unroll
     for (int b = 0; b + 1 < MT; b += 2) wk.x()[(16 * b + (tid >> 4)) * LDA + 16 * (b + 1) + (tid & 15)] = 0.f;
