@@ -162,6 +162,11 @@ def install():
         ctx = _context()
         li, neg = ctx.layer(A_log)
         assert li < N_LAYERS and q.shape[0] == 1 and q.shape[1] == NN
+        if li == 0:
+            # the first GDN layer of a forward: CTX.anc is this step's tree (fc1_branch64.py:29).  Packed
+            # whatever this layer does, so that later layers and the commit never read the previous step's
+            # rows (CTX.anc is a fixed [NN, NN] fp32 buffer: nothing to refuse)
+            _ops.anc_pack(ctx.anc, out=ctx.anc_bits)
         # the conv hook's output for this layer; None when this layer's conv ran in SGLang
         y, ctx.current_mixed = ctx.current_mixed, None
         ctx.saved.discard(li)
@@ -169,8 +174,6 @@ def install():
             return original_verify(self, A_log, dt_bias, q, k, v, a, b, **kw)
         pool = kw['ssm_states']
         try:
-            if li == 0:  # the first GDN layer of a forward: CTX.anc is this step's tree (fc1_branch64.py:29)
-                _ops.anc_pack(ctx.anc, out=ctx.anc_bits)
             out = TK.tree_gdn_split(y, a.reshape(NN, -1), b.reshape(NN, -1), A_log, dt_bias,
                                     pool[0].transpose(-1, -2), ctx.anc, q.shape[2], v.shape[2], q.shape[3],
                                     v.shape[3], aux=(ctx.keys[li], ctx.values[li], ctx.gains[li]), neg_exp_A=neg,

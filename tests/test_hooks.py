@@ -84,6 +84,27 @@ def test_verify_hook_routes_tree_verifies_to_split(hooked, monkeypatch):
     assert len(F.packed) == 2, "packed once per forward: at layer 0 only"
 
 
+def test_anc_is_packed_at_layer_0_even_when_its_conv_fell_back(hooked, monkeypatch):
+    """Layer 0's conv ran in SGLang (no current_mixed): its verify falls back,
+    but this step's tree is still packed, so a later layer verified here and
+    the step's commit read this step's bit rows."""
+    F, _, mods, calls = hooked
+    seen = []
+    monkeypatch.setattr(F.TK, "tree_gdn_split", lambda *args, **kw: seen.append(kw) or torch.zeros(F.NN, 32, 128))
+    K = mods["sglang.srt.layers.attention.linear.kernels.gdn_triton"].TritonGDNKernel
+    pool = torch.zeros(3, 32, 128, 128)
+    A_log, dt_bias, q, k, v, a, b = _verify_args(F.NN)
+    kw = dict(cache_steps=F.NN, ssm_states=pool, cache_indices=torch.tensor([2]),
+              intermediate_state_indices=torch.tensor([1]))
+    F.CTX.current_mixed = None
+    assert K().target_verify(A_log, dt_bias, q, k, v, a, b, **kw) == "original_verify"
+    assert len(F.packed) == 1 and F.packed[0][1] is F.CTX.anc_bits and F.CTX.saved == set()
+    F.CTX.current_mixed = torch.zeros(F.NN, 8192, dtype=torch.bfloat16)
+    K().target_verify(A_log.clone(), dt_bias, q, k, v, a, b, **kw)  # layer 1, verified here
+    assert len(F.packed) == 1 and seen[0]["anc_bits"] is F.CTX.anc_bits and F.CTX.saved == {1}
+    assert calls.names() == ["original_verify"]
+
+
 def test_verify_hook_falls_back_for_other_step_counts(hooked):
     F, _, mods, calls = hooked
     K = mods["sglang.srt.layers.attention.linear.kernels.gdn_triton"].TritonGDNKernel
