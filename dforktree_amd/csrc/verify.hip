@@ -1425,7 +1425,9 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
     __syncthreads();  // am and x take the Gram tiles and X
   }
   if constexpr (kSplit) issue_state_group<false, NW>(S0, p.state_v_stride, wave, lane, 1, s0r);
-  phase_saves<NP, COMMIT, NW>(P, it, tid, sm, sm);
+  // (the 32-wide fused form saves after Cq/Ck: at this point its tile is
+  // still streaming in, and the saves' stores would wait on the full queue)
+  if constexpr (!kEarly) phase_saves<NP, COMMIT, NW>(P, it, tid, sm, sm);
   const int mtn = (it.n + 15) >> 4;  // uniform over the workgroup
   phase_gram_diag<NP, NW>(tid, sm, sm, mtn);
   if constexpr (kSplit) issue_state_group<false, NW>(S0, p.state_v_stride, wave, lane, 2, s0r);
@@ -1470,6 +1472,7 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
     if constexpr (kEarly) __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 15));  // the v row copies (untracked)
     __syncthreads();  // X and Pq complete
   }
+  if constexpr (kEarly) phase_saves<NP, COMMIT, NW>(P, it, tid, sm, sm);  // the k rows are intact until phase 3
   bf16x8 wh[NP / 32][TT], wl[NP / 32][TT];
   phase_w<NP, NW>(lane, wave, sm, sm, ck, wh, wl);
   __syncthreads();  // every wave has read its v rows: the q/k/v region takes the outputs
