@@ -473,6 +473,44 @@ __device__ __forceinline__ void issue_pending(const dft_pending_commit& c, const
   }
 }
 
+// Whole-line state loads (the 32-wide fused form).  In the MFMA layout
+// (s0r[t][j] = S0[k = 16j + 4g + e][v = CW w + 16t + n]) one load covers 64
+// bytes of each of 16 rows, and a line's two halves come from two
+// instructions; a memory-only probe of this tile shape read 128 MiB in
+// 24.5 us that way and in 20.9 us as whole lines.  So load (t, 2s + e) reads
+// rows 8e + r of tile t (r = lane & 7), chunk 8s + 4 b3 + g of each (b3 =
+// lane bit 3, g = lane >> 4): 8 whole lines per instruction, each line over
+// 8 lanes 8 apart.  lines_to_mfma then swaps lane bit 3 with e, giving rows
+// 8 b3 + r = n at chunks 8s + g (j = 2s) and 8s + 4 + g (j = 2s + 1).
+// Fused kernel at batch 64: 73.2 -> 71.8 us.  The verify kernels keep the
+// MFMA layout: the 32-wide one gained nothing (its state groups stream in
+// under phase 1), and the 64-wide ones, latency-bound, lost 3% to the swap.
+__device__ __forceinline__ float row_ror8(float x) {  // lane l ^ 8 of the same 16-lane row
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x128, 0xf, 0xf, false));
+}
+__device__ __forceinline__ void lines_to_mfma(f32x4& a, f32x4& b, bool b3) {
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    // one lane move per pair: u's row_ror8 is b of lane l ^ 8 where b3 is
+    // set, a of lane l ^ 8 where it is not
+    const float ru = row_ror8(b3 ? a[e] : b[e]);
+    a[e] = b3 ? ru : a[e];
+    b[e] = b3 ? b[e] : ru;
+  }
+}
+// k-step group s of a tile loaded by issue_state / issue_state_group
+template <int NW>
+__device__ __forceinline__ void state_group_to_mfma(f32x4 (&s0r)[Waves<NW>::TT][8], int s, int lane) {
+  const bool b3 = (lane >> 3) & 1;
+#pragma unroll
+  for (int t = 0; t < Waves<NW>::TT; ++t) lines_to_mfma(s0r[t][2 * s], s0r[t][2 * s + 1], b3);
+}
+template <int NW>
+__device__ __forceinline__ void state_to_mfma(f32x4 (&s0r)[Waves<NW>::TT][8], int lane) {
+#pragma unroll
+  for (int s = 0; s < 4; ++s) state_group_to_mfma<NW>(s0r, s, lane);
+}
+
 // s0r <- e^{G_u} s0r + sum_p e^{G_u - G_p} k_p vn_p^T on the wave's tiles
 // (s0r[t][j] is the accumulator of a 16x16 MFMA with rows k = 16j + 4g + r and
 // columns v = 32w + 16t + n): fp32 MFMA 16x16x4, path slots as the inner
@@ -495,10 +533,14 @@ __device__ __forceinline__ float pending_decay_log(const Pending& pd, const floa
   return __shfl(gsel, (cu & 3) * 16);
 }
 
-// The commit of a landed tile (a no-op when nothing is pending).  pkey:
-// 16 x 128 floats of LDS that no other wave touches until the next barrier;
-// every thread arrives here (the staging is followed by a barrier).
-template <int NW>
+// The commit of a landed tile (a no-op when nothing is pending; the tile
+// leaves in the MFMA layout either way).  pkey: 16 x 128 floats of LDS that
+// no other wave touches until the next barrier; every thread arrives here
+// (the staging is followed by a barrier).  LINES: the tile was loaded as
+// whole lines, and is turned into the MFMA layout after the keys are staged:
+// they were loaded after it, so it has landed, and their registers are free
+// by then.
+template <int NW, bool LINES>
 __device__ __forceinline__ void commit_tile(const Pending& pd, float* pkey, const f32x4 (&kr)[8 / NW],
                                             const float (&vnr)[4][Waves<NW>::TT], const float (&gp)[4], int wave,
                                             int lane, f32x4 (&s0r)[Waves<NW>::TT][8]) {
@@ -506,6 +548,7 @@ __device__ __forceinline__ void commit_tile(const Pending& pd, float* pkey, cons
   const int n16 = lane & 15, g4 = lane >> 4;
   stage_pending_keys<NW>(pkey, kr, wave, lane);
   __syncthreads();
+  if constexpr (LINES) state_to_mfma<NW>(s0r, lane);
   const float gu = pending_decay_log(pd, gp);
   const float eu = pd.last >= 0 ? __expf(gu) : 1.f;
 #pragma unroll
@@ -529,19 +572,22 @@ __device__ __forceinline__ void commit_tile(const Pending& pd, float* pkey, cons
   }
 }
 
-// k-step group s of the state tile (j = 2s, 2s + 1 of every column tile)
-template <bool NT, int NW>
+// k-step group s of the state tile (j = 2s, 2s + 1 of every column tile).
+// LINES: as whole lines (state_group_to_mfma turns it into the MFMA layout);
+// otherwise straight into the MFMA layout.
+template <bool NT, bool LINES, int NW>
 __device__ __forceinline__ void issue_state_group(const float* S0, int64_t v_stride, int wave, int lane, int s,
                                                   f32x4 (&s0r)[Waves<NW>::TT][8]) {
   const int n16 = lane & 15, g4 = lane >> 4;
+  const int r8 = lane & 7, c8 = 4 * ((lane >> 3) & 1) + g4;  // LINES: row in 8, chunk in the line
 #pragma unroll
   for (int t = 0; t < Waves<NW>::TT; ++t) {
-    const float* rowp = S0 + (int64_t)(Waves<NW>::CW * wave + 16 * t + n16) * v_stride + 4 * g4;
+    const float* rowp = LINES ? S0 + (int64_t)(Waves<NW>::CW * wave + 16 * t + r8) * v_stride + 4 * c8 + 32 * s
+                              : S0 + (int64_t)(Waves<NW>::CW * wave + 16 * t + n16) * v_stride + 4 * g4 + 32 * s;
 #pragma unroll
-    for (int jj = 0; jj < 2; ++jj) {
-      const int j = 2 * s + jj;
-      const f32x4* src = reinterpret_cast<const f32x4*>(rowp + 16 * j);
-      s0r[t][j] = NT ? __builtin_nontemporal_load(src) : *src;
+    for (int e = 0; e < 2; ++e) {
+      const f32x4* src = reinterpret_cast<const f32x4*>(LINES ? rowp + (int64_t)(8 * e) * v_stride : rowp + 16 * e);
+      s0r[t][2 * s + e] = NT ? __builtin_nontemporal_load(src) : *src;
     }
   }
 }
@@ -750,24 +796,15 @@ __device__ __forceinline__ void issue_rows(const dft_verify_args& p, const Item&
   }
 }
 
-// s0r[t][j] = S0[k = 16j + 4g + e][v = 32w + 16t + n]: 16 16-byte loads per
-// lane, 4 lanes per 64-byte sector.  NT: non-temporal loads.  Measured at
-// batch 64 (interleaved runs): the read-only verify is 2.9% faster with
-// ordinary loads, the fused commit -> verify (which writes the tile back)
-// 0.7% faster with non-temporal ones.
-template <bool NT, int NW>
+// The whole state tile, group by group (16 16-byte loads per lane).  NT:
+// non-temporal loads.  Measured at batch 64 (interleaved runs): the
+// read-only verify is 2.9% faster with ordinary loads, the fused commit ->
+// verify (which writes the tile back) 0.7% faster with non-temporal ones.
+template <bool NT, bool LINES, int NW>
 __device__ __forceinline__ void issue_state(const float* S0, int64_t v_stride, int wave, int lane,
                                             f32x4 (&s0r)[Waves<NW>::TT][8]) {
-  const int n16 = lane & 15, g4 = lane >> 4;
 #pragma unroll
-  for (int t = 0; t < Waves<NW>::TT; ++t) {
-    const float* rowp = S0 + (int64_t)(Waves<NW>::CW * wave + 16 * t + n16) * v_stride + 4 * g4;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const f32x4* src = reinterpret_cast<const f32x4*>(rowp + 16 * j);
-      s0r[t][j] = NT ? __builtin_nontemporal_load(src) : *src;
-    }
-  }
+  for (int s = 0; s < 4; ++s) issue_state_group<NT, LINES, NW>(S0, v_stride, wave, lane, s, s0r);
 }
 
 // 1a: row norms (4 threads per q/k row) and the path-cumulative decay
@@ -1334,9 +1371,9 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
       if (pd.last < 0) return;
       f32x4 s0r[TT][8], kr[8 / NW];
       float vnr[4][TT], gp[4];
-      issue_state<true, NW>(S0, p.state_v_stride, wave, lane, s0r);
+      issue_state<true, kEarly, NW>(S0, p.state_v_stride, wave, lane, s0r);
       issue_pending<NW>(P.c, pd, it.h, wave, lane, S0, kr, vnr, gp);
-      commit_tile<NW>(pd, sm.pkey(), kr, vnr, gp, wave, lane, s0r);
+      commit_tile<NW, kEarly>(pd, sm.pkey(), kr, vnr, gp, wave, lane, s0r);
       __syncthreads();  // every wave has read the staged keys: am + x take the write-back staging
       store_state<NW>(const_cast<float*>(S0), p.state_v_stride, wave, lane, s0r, sm.amx + wave * 512);
       return;
@@ -1377,9 +1414,9 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
   // commit before phase 1 and issues it at once.
   constexpr bool kSplit = S0VEC && !COMMIT;
   if (kSplit) {
-    issue_state_group<false, NW>(S0, p.state_v_stride, wave, lane, 0, s0r);
+    issue_state_group<false, false, NW>(S0, p.state_v_stride, wave, lane, 0, s0r);
   } else if (S0VEC) {
-    issue_state<COMMIT, NW>(S0, p.state_v_stride, wave, lane, s0r);
+    issue_state<COMMIT, kEarly, NW>(S0, p.state_v_stride, wave, lane, s0r);
   } else {
 #pragma unroll
     for (int t = 0; t < TT; ++t)
@@ -1414,7 +1451,7 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
   phase_norms<NP, NW>(p, tid, sm, sm);
   __syncthreads();
   if constexpr (COMMIT && !kEarly) {
-    commit_tile<NW>(pd, sm.pkey(), kr, vnr, gp, wave, lane, s0r);
+    commit_tile<NW, false>(pd, sm.pkey(), kr, vnr, gp, wave, lane, s0r);
     // everything this wave loaded has been consumed: no load is left in
     // flight past the (conditional) write-back
     __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 15));
@@ -1424,13 +1461,13 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
     }
     __syncthreads();  // am and x take the Gram tiles and X
   }
-  if constexpr (kSplit) issue_state_group<false, NW>(S0, p.state_v_stride, wave, lane, 1, s0r);
+  if constexpr (kSplit) issue_state_group<false, false, NW>(S0, p.state_v_stride, wave, lane, 1, s0r);
   // (the 32-wide fused form saves after Cq/Ck: at this point its tile is
   // still streaming in, and the saves' stores would wait on the full queue)
   if constexpr (!kEarly) phase_saves<NP, COMMIT, NW>(P, it, tid, sm, sm);
   const int mtn = (it.n + 15) >> 4;  // uniform over the workgroup
   phase_gram_diag<NP, NW>(tid, sm, sm, mtn);
-  if constexpr (kSplit) issue_state_group<false, NW>(S0, p.state_v_stride, wave, lane, 2, s0r);
+  if constexpr (kSplit) issue_state_group<false, false, NW>(S0, p.state_v_stride, wave, lane, 2, s0r);
   __syncthreads();
 #pragma unroll
   for (int d = 1; d < MT; ++d) {
@@ -1438,7 +1475,7 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
     phase_offdiag<NP, NW>(tid, d, sm, mtn);
     __syncthreads();
   }
-  if constexpr (kSplit) issue_state_group<false, NW>(S0, p.state_v_stride, wave, lane, 3, s0r);
+  if constexpr (kSplit) issue_state_group<false, false, NW>(S0, p.state_v_stride, wave, lane, 3, s0r);
   phase_pq<NP, NW>(tid, sm, sm, mtn);
   phase_split_x<NP, NW>(tid, sm, mtn);
   if constexpr (kEarly) {
@@ -1447,14 +1484,18 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
     pd = decode_pending(ph, lane, sm.graw[4][lane & 15]);
     issue_pending<NW>(P.c, pd, it.h, wave, lane, S0, kr, vnr, gp);
     float* stage = reinterpret_cast<float*>(sm.vrows());  // 8 KiB: the 16 path keys, then the write-back
-    commit_tile<NW>(pd, stage, kr, vnr, gp, wave, lane, s0r);
+    commit_tile<NW, true>(pd, stage, kr, vnr, gp, wave, lane, s0r);
     __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 15));
     if (pd.last >= 0) {  // uniform over the workgroup (one request)
       __syncthreads();  // every wave has read the staged keys
       store_state<NW>(const_cast<float*>(S0), p.state_v_stride, wave, lane, s0r, stage + wave * 512);
     }
     __syncthreads();  // every wave has read its staging back: the v region takes the v rows
-    issue_rows<NP, 2, 3, NW>(p, it, wave, lane, S0, sm);
+    // (row addresses recomputed from an opaque copy of the lane id: shared
+    // with the q/k copies at the start, they would be held through the commit)
+    int lane_v = lane;
+    asm volatile("" : "+v"(lane_v));
+    issue_rows<NP, 2, 3, NW>(p, it, wave, lane_v, S0, sm);
   }
 
   f32x4 cq[MT][TT], ck[MT][TT];
@@ -1479,7 +1520,11 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
   phase_out<NP, NW>(P, it, lane, wave, sm, sm, cq, wh, wl, mtn);
   if (P.vn_stage || P.o_stage) {
     __syncthreads();
-    phase_stores<NP, COMMIT, NW>(P, it, tid, sm);
+    // fused form: an opaque thread id, so that the store offsets are
+    // recomputed here instead of held (and spilled) from phase 1
+    int tid_s = tid;
+    if constexpr (COMMIT) asm volatile("" : "+v"(tid_s));
+    phase_stores<NP, COMMIT, NW>(P, it, tid_s, sm);
   }
   if constexpr (COMMIT)
     if (it.h == 0 && wave == 0) fused_status(it, lane, sm.graw[4][lane & 15]);
