@@ -1090,11 +1090,15 @@ __device__ __forceinline__ void phase_split_x(int tid, WK& wk, int mtn) {
 // node 16mt + 4g + r, column 16t + n), Cq as [column][node] (node 16mt + n,
 // column 16t + 4g + r), the layout of the output tiles.
 // WHICH: 3 = both products, 1 = Cq only, 2 = Ck only (a two-pass form that
-// splits the state into hi/lo twice but frees the q rows after the first).
-template <int NP, int WHICH, int NW, class RW>
+// frees the q rows after the first).
+// KEEP: 0 = split the state here, 1 = split it here and keep the split in
+// sh / sl, 2 = take the split kept by an earlier pass (the two-pass form
+// splits once).
+template <int NP, int WHICH, int NW, int KEEP, class RW>
 __device__ __forceinline__ void phase_cq_ck(int lane, const RW& rw, const f32x4 (&s0r)[Waves<NW>::TT][8],
                                             f32x4 (&cq)[NP / 16][Waves<NW>::TT],
-                                            f32x4 (&ck)[NP / 16][Waves<NW>::TT], int mtn) {
+                                            f32x4 (&ck)[NP / 16][Waves<NW>::TT], int mtn,
+                                            bf16x8 (&sh)[4][Waves<NW>::TT], bf16x8 (&sl)[4][Waves<NW>::TT]) {
   constexpr int TT = Waves<NW>::TT;
   constexpr int MT = NP / 16;
   constexpr bool DQ = (WHICH & 1) != 0, DK = (WHICH & 2) != 0;
@@ -1112,9 +1116,18 @@ __device__ __forceinline__ void phase_cq_ck(int lane, const RW& rw, const f32x4 
     bf16x8 bhi[TT], blo[TT];
 #pragma unroll
     for (int t = 0; t < TT; ++t) {
-      const float xs[8] = {s0r[t][2 * s][0],     s0r[t][2 * s][1],     s0r[t][2 * s][2],     s0r[t][2 * s][3],
-                           s0r[t][2 * s + 1][0], s0r[t][2 * s + 1][1], s0r[t][2 * s + 1][2], s0r[t][2 * s + 1][3]};
-      split_bf16x8(xs, bhi[t], blo[t]);
+      if constexpr (KEEP == 2) {
+        bhi[t] = sh[s][t];
+        blo[t] = sl[s][t];
+      } else {
+        const float xs[8] = {s0r[t][2 * s][0],     s0r[t][2 * s][1],     s0r[t][2 * s][2],     s0r[t][2 * s][3],
+                             s0r[t][2 * s + 1][0], s0r[t][2 * s + 1][1], s0r[t][2 * s + 1][2], s0r[t][2 * s + 1][3]};
+        split_bf16x8(xs, bhi[t], blo[t]);
+        if constexpr (KEEP == 1) {
+          sh[s][t] = bhi[t];
+          sl[s][t] = blo[t];
+        }
+      }
     }
     const int o1 = op ^ (32 * s), o2 = op ^ (32 * s + 16);  // columns 32s + 4g .., 32s + 16 + 4g ..
 #pragma unroll
@@ -1502,14 +1515,16 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
   if constexpr (VerifySmem<NP>::kLateV) {
     // Cq first; once every wave is done with the q rows, the v rows are
     // copied into their region while Ck computes
-    phase_cq_ck<NP, 1, NW>(lane, sm, s0r, cq, ck, mtn);
+    bf16x8 sh[4][TT], sl[4][TT];  // the state split once, for both passes
+    phase_cq_ck<NP, 1, NW, 1>(lane, sm, s0r, cq, ck, mtn, sh, sl);
     __syncthreads();  // X and Pq complete, the q rows consumed
     issue_rows<NP, 2, 3, NW>(p, it, wave, lane, S0, sm);
-    phase_cq_ck<NP, 2, NW>(lane, sm, s0r, cq, ck, mtn);
+    phase_cq_ck<NP, 2, NW, 2>(lane, sm, s0r, cq, ck, mtn, sh, sl);
     __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 15));  // the v row copies (untracked by the backend)
     __syncthreads();
   } else {
-    phase_cq_ck<NP, 3, NW>(lane, sm, s0r, cq, ck, mtn);
+    bf16x8 sh[4][TT], sl[4][TT];  // (unused: one pass)
+    phase_cq_ck<NP, 3, NW, 0>(lane, sm, s0r, cq, ck, mtn, sh, sl);
     if constexpr (kEarly) __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 15));  // the v row copies (untracked)
     __syncthreads();  // X and Pq complete
   }

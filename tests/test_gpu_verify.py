@@ -106,6 +106,53 @@ def test_verify_packed_ragged(cuda):
     check_against_oracle(batch, *run_gpu(batch, cuda, packed=True))
 
 
+def test_verify_split_order_empty_requests_and_slots(cuda):
+    """A launch split by tree size takes each kernel's requests in its own
+    order (most 16-row tiles first): empty requests between the others,
+    permuted state slots with a -1 (read from slot 0), trees on both sides of
+    32 nodes.  Every request matches the oracle and reports status 0."""
+    from dforktree_amd import ops, synth
+    announce("verify split order: empty requests, slots")
+    sizes = [40, 12, 64, 33, 9, 17, 64, 1, 48]
+    batch = synth.make_batch(23, 0, sizes, hk=2, hv=4, kinds=["random", "chain", "bushy"] * 3)
+    empty_at = [1, 5, 9]  # positions of the empty requests in the launch
+    order = []            # launch position -> index into sizes (None: empty)
+    it = iter(range(len(sizes)))
+    for pos in range(len(sizes) + len(empty_at)):
+        order.append(None if pos in empty_at else next(it))
+    lens = [0 if r is None else sizes[r] for r in order]
+    cu = torch.zeros(len(order) + 1, dtype=torch.int32)
+    cu[1:] = torch.cumsum(torch.tensor(lens, dtype=torch.int32), 0)
+    pool = torch.randn(len(order) + 1, 4, 128, 128) * 0.02
+    slots = torch.randperm(len(order) + 1)[:len(order)].to(torch.int32)
+    slots[3] = -1
+    batch.state = torch.stack([pool[max(int(slots[p]), 0)] for p, r in enumerate(order) if r is not None])
+    g = batch.to(cuda)
+    rows = g.y.shape[0]
+    ts = ops.tree_struct(g.parent, 4, cu_seqlens=g.cu_seqlens, n_nodes=64, batch=batch.batch, want=("anc_bits",))
+    aux_k = torch.zeros(4, rows, 128, device=cuda)
+    aux_v = torch.zeros(4, rows, 128, device=cuda)
+    aux_g = torch.zeros(4, rows, device=cuda)
+    status = torch.full((len(order),), -5, device=cuda, dtype=torch.int32)
+    o = ops.tree_verify(g.y, g.a, g.b, g.A_log, g.dt_bias, pool.to(cuda).transpose(-1, -2), hk=2, hv=4,
+                        anc_bits=ts["anc_bits"], cu_seqlens=cu.to(cuda), n_nodes=64, batch=len(order),
+                        state_indices=slots.to(cuda), aux_k=aux_k, aux_v=aux_v, aux_g=aux_g, status=status)
+    torch.cuda.synchronize()
+    assert status.tolist() == [0] * len(order)
+    check_against_oracle(batch, o, aux_k, aux_v, aux_g)
+
+
+def test_verify_split_beyond_ordered_batch(cuda):
+    """300 requests (more than the split launch orders): the kernels take
+    their requests by block id, skipping the other kernel's."""
+    from dforktree_amd import synth
+    announce("verify split, 300 requests")
+    g = torch.Generator().manual_seed(5)
+    sizes = torch.randint(1, 49, (300,), generator=g).tolist()
+    batch = synth.make_batch(29, 0, sizes, hk=1, hv=1, kinds=["random", "chain", "bushy"] * 100)
+    check_against_oracle(batch, *run_gpu(batch, cuda, packed=True))
+
+
 def test_verify_state_indices(cuda):
     """Slots are read on the device: permuted slots, and -1 clamps to slot 0."""
     from dforktree_amd import synth
