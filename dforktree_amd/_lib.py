@@ -16,7 +16,7 @@ DFT_F32, DFT_BF16, DFT_F16, DFT_I32, DFT_I64 = 0, 1, 2, 3, 4
 DFT_VERIFY_AUX_K_PER_KHEAD = 1
 DFT_COMMIT_KV, DFT_COMMIT_CHECK_ANC, DFT_COMMIT_LEN_IS_LAST = 1, 2, 4
 DFT_STATUS_SPAN, DFT_STATUS_PATH = 1, 2
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 i32, i64, f32, vp = C.c_int32, C.c_int64, C.c_float, C.c_void_p
 
@@ -53,6 +53,7 @@ class PendingArgs(C.Structure):
         ("keys", vp), ("k_h_stride", i64), ("k_row_stride", i64),
         ("values", vp), ("v_h_stride", i64), ("v_row_stride", i64),
         ("gains", vp), ("g_h_stride", i64), ("g_row_stride", i64),
+        ("key_rows", vp), ("kr_h_stride", i64), ("kr_row_stride", i64),
     ]
 
 

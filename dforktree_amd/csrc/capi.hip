@@ -80,7 +80,11 @@ int dft_tree_commit_verify(const dft_verify_args* a, const dft_pending_commit* c
   if (c->path_cols > 16) return DFT_ERR_UNSUPPORTED;
   if (c->k_head_div <= 0 || a->hv % c->k_head_div != 0) return DFT_ERR_INVALID;
   if (!c->prev_cu_seqlens && (c->prev_n_nodes < 0 || c->prev_n_nodes > 64)) return DFT_ERR_INVALID;
-  if (!c->path || !c->keys || !c->values || !c->gains) return DFT_ERR_INVALID;
+  if (!c->path || !c->values || !c->gains) return DFT_ERR_INVALID;
+  if ((c->keys != nullptr) == (c->key_rows != nullptr)) return DFT_ERR_INVALID;  // saved keys or raw rows
+  // raw key rows are read as 8-byte pieces
+  if (c->key_rows && (reinterpret_cast<uintptr_t>(c->key_rows) % 8 || c->kr_row_stride % 4 || c->kr_h_stride % 4))
+    return DFT_ERR_INVALID;
   if (!index_tag(c->path_dtype) || (c->path_len && !index_tag(c->path_len_dtype))) return DFT_ERR_INVALID;
   // the committed tile is written back with the same 16-byte accesses that read it
   if (a->state_k_stride != 1 || !aligned16(a->state) || a->state_v_stride % 4 || a->state_h_stride % 4 ||

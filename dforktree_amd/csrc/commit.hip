@@ -22,13 +22,6 @@ struct CommitParams {
   int src_vec, dst_vec;  // 16-byte vector path usable
 };
 
-// a value the workgroup agrees on, as a scalar
-__device__ __forceinline__ int64_t uniform64(int64_t v) {
-  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
-  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)((uint64_t)v >> 32));
-  return (int64_t)(((uint64_t)hi << 32) | lo);
-}
-
 // path entries of request b that count (path_len, or all path_cols)
 __device__ __forceinline__ int path_entries(const dft_commit_args& p, int b) {
   int len = p.path_cols;

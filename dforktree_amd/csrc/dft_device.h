@@ -54,6 +54,13 @@ __device__ __forceinline__ void st_i(void* p, int64_t i, int dt, int64_t v) {
 }
 
 // bits 0..i set (the ancestor-or-self mask of a topologically ordered node i)
+// a value the workgroup agrees on, as a scalar
+__device__ __forceinline__ int64_t uniform64(int64_t v) {
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)((uint64_t)v >> 32));
+  return (int64_t)(((uint64_t)hi << 32) | lo);
+}
+
 __device__ __forceinline__ uint64_t mask_upto(int i) {
   return i >= 63 ? ~0ull : ((1ull << (i + 1)) - 1ull);
 }

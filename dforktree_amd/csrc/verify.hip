@@ -423,6 +423,10 @@ __device__ __forceinline__ PendingHead pending_head(CP c, int b) {
     const int64_t l = ld_i(c->path_len, b, c->path_len_dtype);
     ph.len = l < 0 ? 0 : (l < ph.len ? (int)l : ph.len);
   }
+  // uniform (one request): kept in scalar registers through phase 1
+  ph.prow0 = uniform64(ph.prow0);
+  ph.bound = __builtin_amdgcn_readfirstlane(ph.bound);
+  ph.len = __builtin_amdgcn_readfirstlane(ph.len);
   return ph;
 }
 
@@ -448,19 +452,40 @@ __device__ __forceinline__ Pending decode_pending(const PendingHead& ph, int lan
 // (the compiler would then make later code wait for every store since).
 
 // (NW = 8: one 16-byte piece per thread, columns 4n + 64 (w / 4) ..)
+//
+// RAWK: the keys are the previous step's raw bf16 rows (c.key_rows), read as
+// two 8-byte pieces per thread (columns 4n .. and 64 + 4n .., both at NW = 8
+// too: the 16 lanes of a slot then hold its whole row, for the norm) and
+// normalised when they are staged.
+template <int NW, bool RAWK>
+struct PathKeys {
+  f32x4 k[8 / NW];
+};
 template <int NW>
+struct PathKeys<NW, true> {
+  uint2 raw[2];
+};
+template <int NW, bool RAWK>
 __device__ __forceinline__ void issue_pending(const dft_pending_commit& c, const Pending& pd, int h, int wave, int lane,
-                                              const float* dummy, f32x4 (&kr)[8 / NW],
+                                              const float* dummy, PathKeys<NW, RAWK>& pk,
                                               float (&vnr)[4][Waves<NW>::TT], float (&gp)[4]) {
   constexpr int KP = 8 / NW, TT = Waves<NW>::TT, CW = Waves<NW>::CW;
   const bool any = pd.last >= 0;
   const int n16 = lane & 15, g4 = lane >> 4;
-  const float* kb = any ? c.keys + (int64_t)(h / c.k_head_div) * c.k_h_stride + pd.prow0 * c.k_row_stride : dummy;
-  const int64_t ks = any ? c.k_row_stride : 0;
   const int krow = __shfl(pd.ent, 4 * (wave & 3) + g4);
+  if constexpr (RAWK) {
+    const uint16_t* kb = any ? c.key_rows + (int64_t)(h / c.k_head_div) * c.kr_h_stride + pd.prow0 * c.kr_row_stride
+                             : reinterpret_cast<const uint16_t*>(dummy);
+    const int64_t ks = any ? c.kr_row_stride : 0;
 #pragma unroll
-  for (int m = 0; m < KP; ++m)
-    kr[m] = *reinterpret_cast<const f32x4*>(kb + krow * ks + 4 * (n16 + 16 * (m + KP * (wave >> 2))));
+    for (int m = 0; m < 2; ++m) pk.raw[m] = *reinterpret_cast<const uint2*>(kb + krow * ks + 4 * n16 + 64 * m);
+  } else {
+    const float* kb = any ? c.keys + (int64_t)(h / c.k_head_div) * c.k_h_stride + pd.prow0 * c.k_row_stride : dummy;
+    const int64_t ks = any ? c.k_row_stride : 0;
+#pragma unroll
+    for (int m = 0; m < KP; ++m)
+      pk.k[m] = *reinterpret_cast<const f32x4*>(kb + krow * ks + 4 * (n16 + 16 * (m + KP * (wave >> 2))));
+  }
   const float* vb = any ? c.values + (int64_t)h * c.v_h_stride + pd.prow0 * c.v_row_stride : dummy;
   const float* gb = any ? c.gains + (int64_t)h * c.g_h_stride + pd.prow0 * c.g_row_stride : dummy;
   const int64_t vs = any ? c.v_row_stride : 0, gs = any ? c.g_row_stride : 0;
@@ -517,13 +542,38 @@ __device__ __forceinline__ void state_to_mfma(f32x4 (&s0r)[Waves<NW>::TT][8], in
 // dimension (A = keys from LDS, B = weighted values from registers).
 // thread (w, l) holds chunks n and n + 16 of the key of path slot 4w + g
 // (NW = 8: chunk n + 16 (w / 4) of path slot 4 (w % 4) + g)
-template <int NW>
-__device__ __forceinline__ void stage_pending_keys(float* pkey, const f32x4 (&kr)[8 / NW], int wave, int lane) {
+// Raw keys are normalised as the verify normalises its k rows, k / sqrt(sum
+// k^2 + 1e-6) (the sum over the slot's 16 lanes, so in another order than
+// the verify's: the staged keys can differ from its saves by an ulp).
+template <int NW, bool RAWK>
+__device__ __forceinline__ void stage_pending_keys(float* pkey, const PathKeys<NW, RAWK>& pk, int wave, int lane) {
   constexpr int KP = 8 / NW;
   const int rs = 4 * (wave & 3) + (lane >> 4), n16 = lane & 15;
+  if constexpr (RAWK) {
+    float ss = 0.f;
 #pragma unroll
-  for (int m = 0; m < KP; ++m)
-    *reinterpret_cast<f32x4*>(&pkey[pkey_at(rs, 4 * (n16 + 16 * (m + KP * (wave >> 2))))]) = kr[m];
+    for (int m = 0; m < 2; ++m) {
+      ss = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, pk.raw[m].x), __builtin_bit_cast(bf16x2, pk.raw[m].x),
+                                           ss, false);
+      ss = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, pk.raw[m].y), __builtin_bit_cast(bf16x2, pk.raw[m].y),
+                                           ss, false);
+    }
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1) ss += __shfl_xor(ss, o);
+    const float rn = rsqrtf(ss + 1e-6f);
+#pragma unroll
+    for (int m = 0; m < KP; ++m) {
+      const int mm = m + KP * (wave >> 2);  // 0 or 1 (uniform)
+      const uint2 u = mm == 0 ? pk.raw[0] : pk.raw[1];
+      const f32x4 v = {__uint_as_float(u.x << 16) * rn, __uint_as_float(u.x & 0xffff0000u) * rn,
+                       __uint_as_float(u.y << 16) * rn, __uint_as_float(u.y & 0xffff0000u) * rn};
+      *reinterpret_cast<f32x4*>(&pkey[pkey_at(rs, 4 * (n16 + 16 * mm))]) = v;
+    }
+  } else {
+#pragma unroll
+    for (int m = 0; m < KP; ++m)
+      *reinterpret_cast<f32x4*>(&pkey[pkey_at(rs, 4 * (n16 + 16 * (m + KP * (wave >> 2))))]) = pk.k[m];
+  }
 }
 
 // e^{G_u}, the decay of the whole path, broadcast from the lane that holds G_u
@@ -540,13 +590,13 @@ __device__ __forceinline__ float pending_decay_log(const Pending& pd, const floa
 // whole lines, and is turned into the MFMA layout after the keys are staged:
 // they were loaded after it, so it has landed, and their registers are free
 // by then.
-template <int NW, bool LINES>
-__device__ __forceinline__ void commit_tile(const Pending& pd, float* pkey, const f32x4 (&kr)[8 / NW],
+template <int NW, bool LINES, bool RAWK>
+__device__ __forceinline__ void commit_tile(const Pending& pd, float* pkey, const PathKeys<NW, RAWK>& kr,
                                             const float (&vnr)[4][Waves<NW>::TT], const float (&gp)[4], int wave,
                                             int lane, f32x4 (&s0r)[Waves<NW>::TT][8]) {
   constexpr int TT = Waves<NW>::TT;
   const int n16 = lane & 15, g4 = lane >> 4;
-  stage_pending_keys<NW>(pkey, kr, wave, lane);
+  stage_pending_keys<NW, RAWK>(pkey, kr, wave, lane);
   __syncthreads();
   if constexpr (LINES) state_to_mfma<NW>(s0r, lane);
   const float gu = pending_decay_log(pd, gp);
@@ -1346,7 +1396,7 @@ __device__ __forceinline__ void fused_status(const Item& it, int lane, uint32_t 
 
 // The body of the one-head-per-workgroup kernels (COMMIT: the fused commit ->
 // verify form).
-template <int NP, bool S0VEC, bool COMMIT>
+template <int NP, bool S0VEC, bool COMMIT, bool RAWK>
 __device__ __forceinline__ void verify_body(const VerifyParams& P) {
   constexpr int MT = NP / 16;
   constexpr int NW = WavesFor<NP>();
@@ -1361,7 +1411,9 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
   const dft_verify_args& p = P.a;
   __shared__ VerifySmem<NP> sm;
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // (the wave index as a scalar: in a vector register it is held, and at the
+  // fused form's register cap spilled, through phase 1)
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n16 = lane & 15, g4 = lane >> 4;
 
   Item it;
@@ -1382,11 +1434,12 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
       const Pending pd = decode_pending(ph, lane, word);
       if (it.h == 0 && wave == 0) fused_status(it, lane, word);
       if (pd.last < 0) return;
-      f32x4 s0r[TT][8], kr[8 / NW];
+      f32x4 s0r[TT][8];
+      PathKeys<NW, RAWK> kr;
       float vnr[4][TT], gp[4];
       issue_state<true, kEarly, NW>(S0, p.state_v_stride, wave, lane, s0r);
-      issue_pending<NW>(P.c, pd, it.h, wave, lane, S0, kr, vnr, gp);
-      commit_tile<NW, kEarly>(pd, sm.pkey(), kr, vnr, gp, wave, lane, s0r);
+      issue_pending<NW, RAWK>(P.c, pd, it.h, wave, lane, S0, kr, vnr, gp);
+      commit_tile<NW, kEarly, RAWK>(pd, sm.pkey(), kr, vnr, gp, wave, lane, s0r);
       __syncthreads();  // every wave has read the staged keys: am + x take the write-back staging
       store_state<NW>(const_cast<float*>(S0), p.state_v_stride, wave, lane, s0r, sm.amx + wave * 512);
       return;
@@ -1406,7 +1459,7 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
   // 32-wide form issues them after phase 1: held in registers through phase 1
   // beside the tile, they would be spilled.)
   Pending pd{};
-  f32x4 kr[8 / NW];
+  PathKeys<NW, RAWK> kr;
   float vnr[4][TT], gp[4];
   uint32_t pword = 0;
   if constexpr (COMMIT && !kEarly) pword = *path_word(P.c, it.b, lane);
@@ -1415,7 +1468,7 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
   issue_rows<NP, 0, kPlanes, NW>(p, it, wave, lane, S0, sm);
   if constexpr (COMMIT && !kEarly) {
     pd = decode_pending(ph, lane, pword);
-    issue_pending<NW>(P.c, pd, it.h, wave, lane, S0, kr, vnr, gp);
+    issue_pending<NW, RAWK>(P.c, pd, it.h, wave, lane, S0, kr, vnr, gp);
   }
   asm volatile("" ::: "memory");
 
@@ -1464,7 +1517,7 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
   phase_norms<NP, NW>(p, tid, sm, sm);
   __syncthreads();
   if constexpr (COMMIT && !kEarly) {
-    commit_tile<NW, false>(pd, sm.pkey(), kr, vnr, gp, wave, lane, s0r);
+    commit_tile<NW, false, RAWK>(pd, sm.pkey(), kr, vnr, gp, wave, lane, s0r);
     // everything this wave loaded has been consumed: no load is left in
     // flight past the (conditional) write-back
     __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 15));
@@ -1495,9 +1548,9 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
     // the path's entry words came with the gates (row 4); its loads go out
     // now, so that they are not held in registers through phase 1
     pd = decode_pending(ph, lane, sm.graw[4][lane & 15]);
-    issue_pending<NW>(P.c, pd, it.h, wave, lane, S0, kr, vnr, gp);
+    issue_pending<NW, RAWK>(P.c, pd, it.h, wave, lane, S0, kr, vnr, gp);
     float* stage = reinterpret_cast<float*>(sm.vrows());  // 8 KiB: the 16 path keys, then the write-back
-    commit_tile<NW, true>(pd, stage, kr, vnr, gp, wave, lane, s0r);
+    commit_tile<NW, true, RAWK>(pd, stage, kr, vnr, gp, wave, lane, s0r);
     __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 15));
     if (pd.last >= 0) {  // uniform over the workgroup (one request)
       __syncthreads();  // every wave has read the staged keys
@@ -1551,16 +1604,17 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
 template <int NP, bool S0VEC>
 __global__ void __launch_bounds__(64 * WavesFor<NP>()) __attribute__((amdgpu_waves_per_eu(4)))
 tree_verify_kernel(const VerifyParams P) {
-  verify_body<NP, S0VEC, false>(P);
+  verify_body<NP, S0VEC, false, false>(P);
 }
 
 // P must stay this kernel's first (only) argument: out_args<true> reads it
 // back from offset 0 of the kernel-argument segment.
 static_assert(std::is_trivially_copyable<VerifyParams>::value, "VerifyParams is passed by value to the kernels");
-template <int NP>
+// RAWK: the pending keys are the previous step's raw bf16 rows
+template <int NP, bool RAWK>
 __global__ void __launch_bounds__(64 * WavesFor<NP>()) __attribute__((amdgpu_waves_per_eu(4)))
 tree_commit_verify_kernel(const VerifyParams P) {
-  verify_body<NP, true, true>(P);
+  verify_body<NP, true, true, RAWK>(P);
 }
 
 static VerifyParams make_params(const dft_verify_args* a) {
@@ -1626,8 +1680,19 @@ int launch_tree_commit_verify(const dft_verify_args* a, const dft_pending_commit
   VerifyParams narrow, wide;
   bool split;
   split_by_size(a, P, narrow, wide, split);
-  if (a->n_nodes > 32) hipLaunchKernelGGL((tree_commit_verify_kernel<64>), grid, block64, 0, stream, wide);
-  if (a->n_nodes <= 32 || split) hipLaunchKernelGGL((tree_commit_verify_kernel<32>), grid, block, 0, stream, narrow);
+  const bool raw = c->keys == nullptr;  // the previous step's raw key rows (validated by the caller)
+  if (a->n_nodes > 32) {
+    if (raw)
+      hipLaunchKernelGGL((tree_commit_verify_kernel<64, true>), grid, block64, 0, stream, wide);
+    else
+      hipLaunchKernelGGL((tree_commit_verify_kernel<64, false>), grid, block64, 0, stream, wide);
+  }
+  if (a->n_nodes <= 32 || split) {
+    if (raw)
+      hipLaunchKernelGGL((tree_commit_verify_kernel<32, true>), grid, block, 0, stream, narrow);
+    else
+      hipLaunchKernelGGL((tree_commit_verify_kernel<32, false>), grid, block, 0, stream, narrow);
+  }
   return hipGetLastError() == hipSuccess ? DFT_OK : DFT_ERR_LAUNCH;
 }
 

@@ -233,8 +233,9 @@ def _verify_args(y, a, b, A_log, dt_bias, state, *, hk, hv, anc, anc_bits, batch
 
 def tree_commit_verify(y: torch.Tensor, a: torch.Tensor, b: torch.Tensor, A_log: Optional[torch.Tensor],
                        dt_bias: torch.Tensor, state: torch.Tensor, *, hk: int, hv: int,
-                       pending_path: torch.Tensor, pending_keys: torch.Tensor, pending_values: torch.Tensor,
+                       pending_path: torch.Tensor, pending_keys: Optional[torch.Tensor], pending_values: torch.Tensor,
                        pending_gains: torch.Tensor, pending_path_len: Optional[torch.Tensor] = None,
+                       pending_key_rows: Optional[torch.Tensor] = None,
                        prev_cu_seqlens: Optional[torch.Tensor] = None, prev_n_nodes: Optional[int] = None,
                        pending_k_head_div: int = 1, anc: Optional[torch.Tensor] = None,
                        anc_bits: Optional[torch.Tensor] = None, batch: Optional[int] = None,
@@ -250,22 +251,34 @@ def tree_commit_verify(y: torch.Tensor, a: torch.Tensor, b: torch.Tensor, A_log:
     write back).  The pending_* tensors are the previous step's saves
     (keys [hv or hk, rows, 128], values [hv, rows, 128], gains [hv, rows])
     and its accepted path [batch, P <= 16] (-1 padded); they must not alias
-    this step's aux outputs.  Previous rows of request b start at
-    prev_cu_seqlens[b] or b * prev_n_nodes.  Returns o.  ``status`` as in
-    ``tree_verify``, plus DFT_STATUS_PATH for a pending entry past the
-    previous tree (the entry is ignored)."""
+    this step's aux outputs.  Instead of saved keys (pending_keys None),
+    ``pending_key_rows`` may give the previous step's raw bf16 key rows
+    [rows, hk, 128], e.g. ``prev_y[:, hk*128:2*hk*128].unflatten(1, (hk, 128))``,
+    which the commit normalises itself: the verify then needs no aux_k.
+    Previous rows of request b start at prev_cu_seqlens[b] or
+    b * prev_n_nodes.  Returns o.  ``status`` as in ``tree_verify``, plus
+    DFT_STATUS_PATH for a pending entry past the previous tree (the entry is
+    ignored)."""
     args, o, dev, _keep = _verify_args(
         y, a, b, A_log, dt_bias, state, hk=hk, hv=hv, anc=anc, anc_bits=anc_bits, batch=batch, n_nodes=n_nodes,
         cu_seqlens=cu_seqlens, scale=scale, neg_exp_A=neg_exp_A, state_indices=state_indices,
         state_slot_stride=state_slot_stride, o=o, o_dtype=o_dtype, aux_k=aux_k, aux_v=aux_v, aux_g=aux_g,
         aux_k_per_khead=aux_k_per_khead, status=status)
-    _device_of(pending_path, pending_keys, pending_values, pending_gains, pending_path_len, prev_cu_seqlens, y)
+    _device_of(pending_path, pending_keys, pending_key_rows, pending_values, pending_gains, pending_path_len,
+               prev_cu_seqlens, y)
+    if (pending_keys is None) == (pending_key_rows is None):
+        raise ValueError("give either pending_keys or pending_key_rows")
     for t, nm, dims in ((pending_keys, "pending_keys", 3), (pending_values, "pending_values", 3),
                         (pending_gains, "pending_gains", 2)):
-        _check_aux(t, nm, torch.float32, dims=dims)
+        if t is not None:
+            _check_aux(t, nm, torch.float32, dims=dims)
+    if pending_key_rows is not None:
+        _check_aux(pending_key_rows, "pending_key_rows", torch.bfloat16, dims=3)
+        if pending_key_rows.shape[-1] != 128:
+            raise ValueError("pending_key_rows is [rows, heads, 128]")
+    saves = [t for t in (pending_keys, pending_values, pending_gains) if t is not None]
     for out in (aux_k, aux_v, aux_g):
-        if out is not None and any(out.data_ptr() == t.data_ptr()
-                                   for t in (pending_keys, pending_values, pending_gains)):
+        if out is not None and any(out.data_ptr() == t.data_ptr() for t in saves):
             raise ValueError("the pending saves must not alias this step's aux outputs")
     path = pending_path.unsqueeze(0) if pending_path.dim() == 1 else pending_path
     if path.stride(1) != 1:
@@ -286,7 +299,11 @@ def tree_commit_verify(y: torch.Tensor, a: torch.Tensor, b: torch.Tensor, A_log:
         if prev_n_nodes is None:
             raise ValueError("give prev_cu_seqlens or prev_n_nodes")
         c.prev_n_nodes = prev_n_nodes
-    c.keys, c.k_h_stride, c.k_row_stride = pending_keys.data_ptr(), *pending_keys.stride()[:2]
+    if pending_keys is not None:
+        c.keys, c.k_h_stride, c.k_row_stride = pending_keys.data_ptr(), *pending_keys.stride()[:2]
+    else:  # [rows, heads, 128]: row stride first
+        c.key_rows = pending_key_rows.data_ptr()
+        c.kr_row_stride, c.kr_h_stride = pending_key_rows.stride(0), pending_key_rows.stride(1)
     c.values, c.v_h_stride, c.v_row_stride = pending_values.data_ptr(), *pending_values.stride()[:2]
     c.gains, c.g_h_stride, c.g_row_stride = pending_gains.data_ptr(), *pending_gains.stride()
     check("dft_tree_commit_verify", load().dft_tree_commit_verify(C.byref(args), C.byref(c), _stream(dev)))

@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define DFT_ABI_VERSION 2
+#define DFT_ABI_VERSION 3
 
 #if defined(__GNUC__)
 #define DFT_API __attribute__((visibility("default")))
@@ -268,7 +268,9 @@ DFT_API int dft_tree_commit(const dft_commit_args* args, void* stream);
  * verify step into the next step's verify, so the state is read once per
  * layer and step instead of twice.  The previous step's keys / values / gains
  * must not alias this step's aux outputs (alternate two sets), and every
- * request's previous rows must exist in them.  A slot that a request commits
+ * request's previous rows must exist in them.  The keys may also be read as
+ * the previous step's raw bf16 rows (key_rows), normalised here; the verify
+ * then writes no keys at all.  A slot that a request commits
  * into must not be another request's slot in the same launch (the tile is
  * updated in place while the other request would read it).
  * ------------------------------------------------------------------------- */
@@ -283,12 +285,22 @@ typedef struct dft_pending_commit {
   int32_t path_len_dtype;
   const int32_t* prev_cu_seqlens; /* previous step's row0(b), or NULL: b * prev_n_nodes */
 
-  const float* keys; /* [h'][row][dk] */
+  const float* keys; /* [h'][row][dk], or NULL: key_rows below */
   int64_t k_h_stride, k_row_stride;
   const float* values; /* [h][row][dv] */
   int64_t v_h_stride, v_row_stride;
   const float* gains; /* [h][row] */
   int64_t g_h_stride, g_row_stride;
+  /* DFT_ABI_VERSION 3 (appended: the fields above keep their offsets).
+   * Instead of saved keys, the previous step's raw bf16 key rows: row r of
+   * keys head h' = h / k_head_div at key_rows + h' kr_h_stride + r kr_row_stride
+   * (elements), e.g. the k part of the previous step's y.  Each row is
+   * normalised here as the verify normalises it, k / sqrt(sum k^2 + 1e-6),
+   * so the verify that precedes it need not save keys (aux_k NULL).  Exactly
+   * one of keys and key_rows is given; key_rows and both strides are 8-byte
+   * aligned (strides multiples of 4 elements). */
+  const uint16_t* key_rows;
+  int64_t kr_h_stride, kr_row_stride;
 } dft_pending_commit;
 
 DFT_API int dft_tree_commit_verify(const dft_verify_args* verify, const dft_pending_commit* pending, void* stream);

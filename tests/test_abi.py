@@ -29,7 +29,7 @@ def test_library_exports_every_declared_symbol():
     out = subprocess.run(["nm", "-D", "--defined-only", str(_lib.LIB_PATH)], capture_output=True, text=True).stdout
     exported = {l.split()[-1] for l in out.splitlines() if " T " in l}
     assert exported == set(names), "only the C ABI is exported"
-    assert lib.dft_abi_version() == _lib.ABI_VERSION == 2
+    assert lib.dft_abi_version() == _lib.ABI_VERSION == 3
 
 
 @pytest.fixture(scope="module")
@@ -92,6 +92,13 @@ def test_validation_rejects_bad_descriptors_without_launching():
     assert lib.dft_tree_commit_verify(ctypes.byref(v), None, None) == _lib.DFT_ERR_INVALID  # no pending
     assert lib.dft_tree_commit_verify(ctypes.byref(v), ctypes.byref(pc), None) == _lib.DFT_ERR_INVALID
     pc.path = pc.keys = pc.values = pc.gains = 16
+    pc.key_rows = 16
+    assert lib.dft_tree_commit_verify(ctypes.byref(v), ctypes.byref(pc), None) == _lib.DFT_ERR_INVALID  # keys twice
+    pc.keys, pc.key_rows = None, 12
+    assert lib.dft_tree_commit_verify(ctypes.byref(v), ctypes.byref(pc), None) == _lib.DFT_ERR_INVALID  # raw rows: 8 B
+    pc.key_rows, pc.kr_row_stride = 16, 6
+    assert lib.dft_tree_commit_verify(ctypes.byref(v), ctypes.byref(pc), None) == _lib.DFT_ERR_INVALID  # stride % 4
+    pc.keys, pc.key_rows, pc.kr_row_stride = 16, None, 0
     pc.path_cols = 17
     assert lib.dft_tree_commit_verify(ctypes.byref(v), ctypes.byref(pc), None) == _lib.DFT_ERR_UNSUPPORTED
     pc.path_cols = 0  # the kernel pads from entry path_cols - 1: at least one column

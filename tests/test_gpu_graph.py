@@ -53,6 +53,7 @@ class Step:
         # in-place inputs and their originals
         self.pool0 = self.g1.state.clone()                    # [B, hv, V, K]
         self.pool = self.pool0.clone()                        # fused commit -> verify
+        self.rpool = self.pool0.clone()                       # the same with raw key rows
         self.cpool0 = self.g1.state.clone().unsqueeze(0)      # [L=1, B, hv, V, K], separate commit
         self.cpool = self.cpool0.clone()
         n = 48
@@ -72,6 +73,8 @@ class Step:
             o2=torch.empty(rows, 4, 128, device=cuda, dtype=torch.bfloat16),
             k1=torch.empty(4, rows, 128, **f32), v1=torch.empty(4, rows, 128, **f32), G1=torch.empty(4, rows, **f32),
             k2=torch.empty(2, rows, 128, **f32), v2=torch.empty(4, rows, 128, **f32), G2=torch.empty(4, rows, **f32),
+            o3=torch.empty(rows, 4, 128, device=cuda, dtype=torch.bfloat16),
+            v3=torch.empty(4, rows, 128, **f32), G3=torch.empty(4, rows, **f32),
             y=torch.empty_like(self.cx), iw=torch.empty(*self.cx.shape, 3, device=cuda, dtype=torch.bfloat16),
             mask=torch.empty(mask_bytes, device=cuda, dtype=torch.uint8),
             mind=torch.empty(self.B + 1, device=cuda, dtype=torch.int32),
@@ -80,6 +83,7 @@ class Step:
 
     def reset(self):
         self.pool.copy_(self.pool0)
+        self.rpool.copy_(self.pool0)
         self.cpool.copy_(self.cpool0)
         self.inv.copy_(self.inv0)
         for t in self.out.values():
@@ -111,6 +115,12 @@ class Step:
                                pending_path=self.idx, pending_keys=o["k1"], pending_values=o["v1"],
                                pending_gains=o["G1"], pending_path_len=self.lens, o=o["o2"], aux_k=o["k2"],
                                aux_v=o["v2"], aux_g=o["G2"], aux_k_per_khead=True, **prev, **self.shape_kw(g2))
+        # the fused entry again, its keys normalised from step 1's raw k rows
+        ops.tree_commit_verify(g2.y, g2.a, g2.b, g2.A_log, g2.dt_bias, self.rpool.transpose(-1, -2), hk=2, hv=4,
+                               anc_bits=ts2["anc_bits"], pending_path=self.idx, pending_keys=None,
+                               pending_key_rows=g1.y[:, 256:512].unflatten(1, (2, 128)), pending_values=o["v1"],
+                               pending_gains=o["G1"], pending_path_len=self.lens, pending_k_head_div=2, o=o["o3"],
+                               aux_v=o["v3"], aux_g=o["G3"], **prev, **self.shape_kw(g2))
         ops.tree_commit(self.cpool, o["k2"][None], o["v2"][None], o["G2"][None], self.idx2, n_nodes=self.N,
                         k_head_div=2, **(dict(cu_seqlens=g2.cu_seqlens) if self.packed else {}))
         ops.block_inverse_(self.inv)
@@ -120,7 +130,7 @@ class Step:
 
     def snapshot(self, ts):
         got = {k: t.clone() for k, t in self.out.items()}
-        got.update(pool=self.pool.clone(), cpool=self.cpool.clone(), inv=self.inv.clone())
+        got.update(pool=self.pool.clone(), rpool=self.rpool.clone(), cpool=self.cpool.clone(), inv=self.inv.clone())
         got.update({f"ts_{k}": v.clone() for k, v in ts.items()})
         return got
 
@@ -138,7 +148,7 @@ def _replays(cuda, step):
     torch.cuda.synchronize()
     want = step.snapshot(step.run())
     torch.cuda.synchronize()
-    for name in ("o1", "o2", "k2", "mask", "pb"):
+    for name in ("o1", "o2", "o3", "k2", "mask", "pb"):
         assert not torch.equal(want[name], torch.full_like(want[name], SENTINEL[want[name].dtype])), name
     assert not torch.equal(want["pool"], step.pool0) and not torch.equal(want["cpool"], step.cpool0)
 
