@@ -70,6 +70,8 @@ class Workload:
         self.y_prev = synth.device_randn_(torch.empty(L, rows, C, device=dev, dtype=torch.bfloat16), seed + 7)
         self.a = synth.device_randn_(torch.empty(L, rows, HV, device=dev, dtype=torch.bfloat16), seed + 1)
         self.b = synth.device_randn_(torch.empty(L, rows, HV, device=dev, dtype=torch.bfloat16), seed + 2)
+        # and its b gates, from which the pipelined commit can recompute the path's values
+        self.b_prev = synth.device_randn_(torch.empty(L, rows, HV, device=dev, dtype=torch.bfloat16), seed + 8)
         self.A_log = torch.full((HV,), -0.6931471805599453, device=dev)
         self.dt_bias = torch.zeros(HV, device=dev)
         self.neg = -self.A_log.exp()
@@ -108,23 +110,29 @@ class Workload:
             self.verify(l)
         self.commit()
 
-    def fused(self, l, raw_keys=True):
+    def fused(self, l, raw_keys=True, raw_values=False):
         """One layer of the pipelined schedule.  raw_keys: the commit reads the
         previous step's raw k rows from its y and normalises them, so this
         step's verify saves no keys; else it reads the previous step's saved
-        keys and this step saves its own."""
+        keys and this step saves its own.  raw_values: likewise the commit
+        recomputes the path's values from the previous step's raw v rows and
+        b gates, so this step's verify saves no values."""
         from dforktree_amd import ops
         if raw_keys:
             keys = dict(pending_keys=None, aux_k=None,
                         pending_key_rows=self.y_prev[l][:, HK * D:2 * HK * D].unflatten(1, (HK, D)))
         else:
             keys = dict(pending_keys=self.keys[l], aux_k=self.keys2[l])
+        if raw_values:
+            keys.update(pending_values=None, aux_v=None, pending_b=self.b_prev[l],
+                        pending_value_rows=self.y_prev[l][:, 2 * HK * D:].unflatten(1, (HV, D)))
+        else:
+            keys.update(pending_values=self.vals[l], aux_v=self.vals2[l])
         ops.tree_commit_verify(self.y[l], self.a[l], self.b[l], self.A_log, self.dt_bias,
                                self.state[l].transpose(-1, -2), hk=HK, hv=HV, anc_bits=self.anc_bits, batch=B,
-                               n_nodes=N, neg_exp_A=self.neg, o=self.o[l], aux_v=self.vals2[l],
-                               aux_g=self.gains2[l], aux_k_per_khead=True, pending_path=self.accept,
-                               pending_values=self.vals[l], pending_gains=self.gains[l], prev_n_nodes=N,
-                               pending_k_head_div=HV // HK, **keys)
+                               n_nodes=N, neg_exp_A=self.neg, o=self.o[l], aux_g=self.gains2[l],
+                               aux_k_per_khead=True, pending_path=self.accept, pending_gains=self.gains[l],
+                               prev_n_nodes=N, pending_k_head_div=HV // HK, **keys)
 
     def fused_step(self):
         for l in range(L):
@@ -185,19 +193,23 @@ class Workload:
                    + HK * N * D * 4)       # normalised k fp32 write (per k-head)
         return B * per_req
 
-    def fused_bytes_per_launch(self, raw_keys=True):
+    def fused_bytes_per_launch(self, raw_keys=True, raw_values=False):
         """verify bytes + the committed tile written back + the path's saves.
         raw_keys: no keys are saved, and the path's keys are read as raw bf16
-        rows (per k-head) instead of saved fp32 ones."""
+        rows (per k-head) instead of saved fp32 ones.  raw_values: no values
+        are saved, and the path's values are recomputed from raw bf16 v rows
+        and bf16 b gates."""
         tot = 0
         for ell in self.path_lens:
             tot += (HV * D * D * 4                                # state write
                     + ell * HK * D * (2 if raw_keys else 4)      # path keys (per k-head)
-                    + ell * HV * D * 4                           # path values
+                    + ell * HV * D * (2 if raw_values else 4)    # path values (raw v rows)
+                    + (ell * HV * 2 if raw_values else 0)        # path b gates
                     + ell * HV * 4                               # path gains
                     + MAX_PATH * 4)                              # path indices
         key_saves = B * HK * N * D * 4 if raw_keys else 0
-        return self.verify_bytes_per_launch() - key_saves + tot
+        value_saves = B * HV * N * D * 4 if raw_values else 0
+        return self.verify_bytes_per_launch() - key_saves - value_saves + tot
 
     def commit_bytes_per_launch(self):
         tot = 0
@@ -523,6 +535,8 @@ def main():
     t_fused = t_fused_layers / L
     t_fused_saved = time_graph(lambda: [w.fused(l, raw_keys=False) for l in range(L)], reps_kernel, args.warmup,
                                args.eager) / L
+    t_fused_rv = time_graph(lambda: [w.fused(l, raw_values=True) for l in range(L)], reps_kernel, args.warmup,
+                            args.eager) / L
     t_step = time_graph(w.fused_step, args.steps, args.warmup, args.eager)
     # conv and mask run once per layer in a step: 24 back-to-back launches per replay, as for verify
     w.conv_setup(dev)
@@ -606,6 +620,9 @@ def main():
         # the same launch with the keys saved by the verify and read back by the next commit
         "commit_verify_saved_keys": {"us_per_layer": round(t_fused_saved * 1e3, 2),
                                      "hbm_frac": frac(w.fused_bytes_per_launch(raw_keys=False), t_fused_saved)},
+        # with the path's values recomputed by the commit (the verify saves no values)
+        "commit_verify_recomputed_values": {"us_per_layer": round(t_fused_rv * 1e3, 2),
+                                            "hbm_frac": frac(w.fused_bytes_per_launch(raw_values=True), t_fused_rv)},
         # state bytes the separate kernels need (verify read + commit read and write) per unit time,
         # and the state bytes the pipelined schedule actually moves (one read + one write)
         "state_traffic_hbm_frac": frac(w.state_bytes_per_step(), t_step),

@@ -54,6 +54,8 @@ class PendingArgs(C.Structure):
         ("values", vp), ("v_h_stride", i64), ("v_row_stride", i64),
         ("gains", vp), ("g_h_stride", i64), ("g_row_stride", i64),
         ("key_rows", vp), ("kr_h_stride", i64), ("kr_row_stride", i64),
+        ("value_rows", vp), ("vr_h_stride", i64), ("vr_row_stride", i64),
+        ("prev_b", vp), ("pb_row_stride", i64), ("prev_b_dtype", i32),
     ]
 
 

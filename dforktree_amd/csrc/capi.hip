@@ -80,8 +80,11 @@ int dft_tree_commit_verify(const dft_verify_args* a, const dft_pending_commit* c
   if (c->path_cols > 16) return DFT_ERR_UNSUPPORTED;
   if (c->k_head_div <= 0 || a->hv % c->k_head_div != 0) return DFT_ERR_INVALID;
   if (!c->prev_cu_seqlens && (c->prev_n_nodes < 0 || c->prev_n_nodes > 64)) return DFT_ERR_INVALID;
-  if (!c->path || !c->values || !c->gains) return DFT_ERR_INVALID;
+  if (!c->path || !c->gains) return DFT_ERR_INVALID;
   if ((c->keys != nullptr) == (c->key_rows != nullptr)) return DFT_ERR_INVALID;  // saved keys or raw rows
+  // saved values, or the raw value rows and b gates they are recomputed from
+  if ((c->values != nullptr) == (c->value_rows != nullptr)) return DFT_ERR_INVALID;
+  if (c->value_rows && (!c->prev_b || !float_tag(c->prev_b_dtype))) return DFT_ERR_INVALID;
   // raw key rows are read as 8-byte pieces
   if (c->key_rows && (reinterpret_cast<uintptr_t>(c->key_rows) % 8 || c->kr_row_stride % 4 || c->kr_h_stride % 4))
     return DFT_ERR_INVALID;

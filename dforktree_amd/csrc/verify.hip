@@ -222,6 +222,10 @@ __device__ __forceinline__ int pkey_at(int p, int c) { return p * kD + ((((c >> 
 // into the q region once Cq/Ck have consumed it, and o is staged in x once the
 // vn tiles have consumed X.  That keeps the workgroup under 80 KiB of LDS, so
 // two of them fit on a CU.
+// LDS of the recomputed path values: four 16 x 16 matrices (row pitch 17),
+// then the 16 key norms of the raw-key form
+constexpr int kRvxNorms = 4 * 16 * 17, kRvx = kRvxNorms + 16;
+
 template <int NP, bool LATE_V>
 struct VRegion {
   uint16_t v[NP * kD];
@@ -248,6 +252,7 @@ struct VerifySmem : VRegion<NP, (NP > 32)> {
   alignas(16) float cO[NP];
   alignas(16) uint64_t anc[NP];
   uint32_t graw[6][64];  // per lane of wave 0: words of a, b, ancestry bits lo / hi, dt_bias, decay
+  alignas(16) float rvx[kRvx];  // the fused commit's recomputed path values: A, its powers, X; key norms
   __device__ float* am() { return amx; }
   __device__ const float* am() const { return amx; }
   __device__ float* x() { return amx + NP * LDA; }
@@ -391,6 +396,12 @@ struct Pending {
   int64_t prow0;   // row of the request's node 0 in the previous step's buffers
 };
 
+// The recompute's slot of path position i, and the position of slot i (the
+// map is its own inverse): positions 4m .. 4m + 3 take slots m, 4 + m, 8 + m,
+// 12 + m, the k indices of k-step m of an MFMA 16x16x4 whose B operand is in
+// the accumulator layout (k = 4g + m in lane group g).
+__device__ __forceinline__ int rvn_slot(int i) { return 4 * (i & 3) + (i >> 2); }
+
 // The 32-bit word of path entry l % 16 (the low half of an int64 entry).
 __device__ __forceinline__ const uint32_t* path_word(const dft_pending_commit& c, int b, int lane) {
   const int col = (lane & 15) < c.path_cols ? (lane & 15) : c.path_cols - 1;
@@ -465,10 +476,25 @@ template <int NW>
 struct PathKeys<NW, true> {
   uint2 raw[2];
 };
-template <int NW, bool RAWK>
+// The path's values and gains as a thread holds them until the commit: the
+// saved vn_p[v] and G_p of slots p = 4s + g, or (RVN: recomputed values) the
+// previous step's raw bf16 value rows of path positions 4e + g (slots 4g + e
+// of the recompute, the rows of W's accumulator layout; vr[e][t]: tile t's
+// column, two bf16 per register), with the gain and b gate of position
+// lane % 16.
+template <int NW, bool RVN>
+struct PathVals {
+  float v[4][Waves<NW>::TT];
+  float g[4];
+};
+template <int NW>
+struct PathVals<NW, true> {
+  u16x2 vr[4];
+  float gl, bl;
+};
+template <int NW, bool RAWK, bool RVN>
 __device__ __forceinline__ void issue_pending(const dft_pending_commit& c, const Pending& pd, int h, int wave, int lane,
-                                              const float* dummy, PathKeys<NW, RAWK>& pk,
-                                              float (&vnr)[4][Waves<NW>::TT], float (&gp)[4]) {
+                                              const float* dummy, PathKeys<NW, RAWK>& pk, PathVals<NW, RVN>& pv) {
   constexpr int KP = 8 / NW, TT = Waves<NW>::TT, CW = Waves<NW>::CW;
   const bool any = pd.last >= 0;
   const int n16 = lane & 15, g4 = lane >> 4;
@@ -486,15 +512,35 @@ __device__ __forceinline__ void issue_pending(const dft_pending_commit& c, const
     for (int m = 0; m < KP; ++m)
       pk.k[m] = *reinterpret_cast<const f32x4*>(kb + krow * ks + 4 * (n16 + 16 * (m + KP * (wave >> 2))));
   }
-  const float* vb = any ? c.values + (int64_t)h * c.v_h_stride + pd.prow0 * c.v_row_stride : dummy;
   const float* gb = any ? c.gains + (int64_t)h * c.g_h_stride + pd.prow0 * c.g_row_stride : dummy;
-  const int64_t vs = any ? c.v_row_stride : 0, gs = any ? c.g_row_stride : 0;
+  const int64_t gs = any ? c.g_row_stride : 0;
+  if constexpr (RVN) {
+    const uint16_t* vb = any ? c.value_rows + (int64_t)h * c.vr_h_stride + pd.prow0 * c.vr_row_stride
+                             : reinterpret_cast<const uint16_t*>(dummy);
+    const int64_t vs = any ? c.vr_row_stride : 0;
+    static_assert(TT <= 2, "two bf16 per register");
 #pragma unroll
-  for (int s = 0; s < 4; ++s) {
-    const int row = __shfl(pd.ent, 4 * s + g4);
+    for (int e = 0; e < 4; ++e) {
+      const int64_t row = __shfl(pd.ent, 4 * e + g4);  // slot 4g + e is position 4e + g
 #pragma unroll
-    for (int t = 0; t < TT; ++t) vnr[s][t] = vb[row * vs + CW * wave + 16 * t + n16];
-    gp[s] = gb[row * gs];
+      for (int t = 0; t < TT; ++t) pv.vr[e][t] = vb[row * vs + CW * wave + 16 * t + n16];
+    }
+    pv.gl = gb[pd.ent * gs];
+    // the b gate as the verify reads it: the whole 32-bit word, converted later
+    uint32_t sh;
+    const uint32_t* bw = any ? word_of(c.prev_b, (pd.prow0 + pd.ent) * c.pb_row_stride + h, c.prev_b_dtype, sh)
+                             : reinterpret_cast<const uint32_t*>(dummy);
+    pv.bl = word_to_f(*bw, any ? sh : 0u, any ? c.prev_b_dtype : (int)DFT_F32);
+  } else {
+    const float* vb = any ? c.values + (int64_t)h * c.v_h_stride + pd.prow0 * c.v_row_stride : dummy;
+    const int64_t vs = any ? c.v_row_stride : 0;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const int row = __shfl(pd.ent, 4 * s + g4);
+#pragma unroll
+      for (int t = 0; t < TT; ++t) pv.v[s][t] = vb[row * vs + CW * wave + 16 * t + n16];
+      pv.g[s] = gb[row * gs];
+    }
   }
 }
 
@@ -545,10 +591,13 @@ __device__ __forceinline__ void state_to_mfma(f32x4 (&s0r)[Waves<NW>::TT][8], in
 // Raw keys are normalised as the verify normalises its k rows, k / sqrt(sum
 // k^2 + 1e-6) (the sum over the slot's 16 lanes, so in another order than
 // the verify's: the staged keys can differ from its saves by an ulp).
-template <int NW, bool RAWK>
-__device__ __forceinline__ void stage_pending_keys(float* pkey, const PathKeys<NW, RAWK>& pk, int wave, int lane) {
+template <int NW, bool RAWK, bool RVN>
+__device__ __forceinline__ void stage_pending_keys(float* pkey, float* rvx, const PathKeys<NW, RAWK>& pk, int wave,
+                                                   int lane) {
   constexpr int KP = 8 / NW;
-  const int rs = 4 * (wave & 3) + (lane >> 4), n16 = lane & 15;
+  const int n16 = lane & 15;
+  const int rp = 4 * (wave & 3) + (lane >> 4);  // the path position loaded
+  const int rs = RVN ? rvn_slot(rp) : rp;      // its staging slot
   if constexpr (RAWK) {
     float ss = 0.f;
 #pragma unroll
@@ -561,6 +610,18 @@ __device__ __forceinline__ void stage_pending_keys(float* pkey, const PathKeys<N
 #pragma unroll
     for (int o = 1; o < 16; o <<= 1) ss += __shfl_xor(ss, o);
     const float rn = rsqrtf(ss + 1e-6f);
+    if constexpr (RVN) {
+      // the raw rows in the q/k row layout (bf16 MFMA operands for the
+      // recompute) and the norms beside the recompute's matrices
+      uint16_t* praw = reinterpret_cast<uint16_t*>(pkey);
+#pragma unroll
+      for (int m = 0; m < KP; ++m) {
+        const int mm = m + KP * (wave >> 2);
+        *reinterpret_cast<uint2*>(&praw[qkv_at(rs, 4 * n16 + 64 * mm)]) = mm == 0 ? pk.raw[0] : pk.raw[1];
+      }
+      if (n16 == 0 && wave < 4) rvx[kRvxNorms + rs] = rn;
+      return;
+    }
 #pragma unroll
     for (int m = 0; m < KP; ++m) {
       const int mm = m + KP * (wave >> 2);  // 0 or 1 (uniform)
@@ -583,6 +644,203 @@ __device__ __forceinline__ float pending_decay_log(const Pending& pd, const floa
   return __shfl(gsel, (cu & 3) * 16);
 }
 
+// hi/lo bf16 splits of columns 32s + 4g .. + 3 and 32s + 16 + 4g .. + 3 of
+// staged key p: the A (and B) operand of k-step s of a bf16 MFMA 16x16x32
+// whose B operand is k-step group s of the state tile
+__device__ __forceinline__ void pkey_split(const float* pkey, int p, int s, int g4, bf16x8& hi, bf16x8& lo) {
+  const f32x4 a = *reinterpret_cast<const f32x4*>(&pkey[pkey_at(p, 32 * s + 4 * g4)]);
+  const f32x4 b = *reinterpret_cast<const f32x4*>(&pkey[pkey_at(p, 32 * s + 16 + 4 * g4)]);
+  const float x[8] = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+  split_bf16x8(x, hi, lo);
+}
+
+// D = C + P Q for 16 x 16 row-major LDS matrices (row pitch 17), fp32 MFMA
+// 16x16x4 (k-step m covers k = 4g + m); C and D in the accumulator layout
+// (element e of lane (n, g): row 4g + e, column n).  One wave's LDS
+// operations run in order, so a product may read what the wave stored just
+// before and store over an operand it has read.
+__device__ __forceinline__ f32x4 mat16_mul(const float* P, const float* Q, f32x4 acc, int n16, int g4) {
+#pragma unroll
+  for (int m = 0; m < 4; ++m) acc = mfma_f32_16x16x4(P[n16 * 17 + 4 * g4 + m], Q[(4 * g4 + m) * 17 + n16], acc);
+  return acc;
+}
+__device__ __forceinline__ void mat16_store(float* D, f32x4 acc, int n16, int g4) {
+#pragma unroll
+  for (int e = 0; e < 4; ++e) D[(4 * g4 + e) * 17 + n16] = acc[e];
+}
+
+// RVN: the values of the path's slots, recomputed from the tile before the
+// commit.  For a root walk the ancestors of every path node are the path's
+// earlier nodes, so vn_path = X W over the path alone: A_pq = beta_p (k_p .
+// k_q) e^{G_p - G_q} for valid q < p, X = (I + A)^-1, and W_p = beta_p (v_p -
+// e^{G_p} S0^T k_p) with S0 the tile as the previous verify read it.
+//  * wave 0 forms the 16 x 16 Gram of the staged keys by bf16 MFMA 16x16x32
+//    (RAWK: on the raw bf16 rows, exact products, then scaled by the two
+//    norms; else on hi/lo splits of the fp32 keys, three products), and X =
+//    (I + A)^-1 as the product (I - A)(I + A^2)(I + A^4)(I + A^8), exact for
+//    A strictly lower triangular in path order: with the path's last valid
+//    position at len - 1, A^len = 0, so the factors and powers from A^len on
+//    are skipped (fp32 MFMA 16x16x4 products through LDS matrices; a path of
+//    up to 4 positions takes two, up to 2 none).  A forward substitution holds a 16-float
+//    column per lane, which beside the tile spilled the 32-wide kernel;
+//  * Ck = K S0 by bf16 MFMA 16x16x32 on the tile registers split into hi/lo
+//    bf16 (as the verify's Cq/Ck pass splits them; RAWK: the raw rows, exact,
+//    the norm applied to the result, two products per k-step; else three),
+//    rows = slots 4g + e, and W in place, zero on invalid slots (so vn is
+//    zero there).  The MFMA work here lies on every workgroup's critical
+//    path: at batch 64 the fp32 MFMA 16x16x4 form of Ck cost 4 us per launch,
+//    this one about 1;
+//  * vn = X W by fp32 MFMA 16x16x4.  The keys are staged at rvn_slot of their
+//    path position, so k-step m of this product covers positions 4m .. 4m +
+//    3 (a path of up to 4 positions takes one k-step, not four), and element
+//    s of a lane (slot 4g + s) is position 4s + g: the B-operand layout of
+//    the commit below (vnr[s] = position 4s + g), which reads the key of
+//    position p from slot rvn_slot(p).
+// Every thread arrives here (one barrier, skipped by the whole workgroup
+// when nothing is pending).
+template <int NW, bool RAWK>
+__device__ __forceinline__ void path_values(const Pending& pd, const float* pkey, float* rvx,
+                                            const PathVals<NW, true>& pv, int wave, int lane,
+                                            const f32x4 (&s0r)[Waves<NW>::TT][8], float (&vnr)[4][Waves<NW>::TT]) {
+  constexpr int TT = Waves<NW>::TT;
+  const int n16 = lane & 15, g4 = lane >> 4;
+#pragma unroll
+  for (int s = 0; s < 4; ++s)
+#pragma unroll
+    for (int t = 0; t < TT; ++t) vnr[s][t] = 0.f;
+  if (pd.last < 0) return;  // uniform
+  const u16x2 (&vr)[4] = pv.vr;
+  const float beta = 1.f / (1.f + expf(-pv.bl));  // slot lane % 16, as the verify forms beta
+  if (wave == 0) {
+    // (lane ids laundered in each part: addresses computed where used)
+    int lg = lane;
+    asm volatile("" : "+v"(lg));
+    const int n16 = lg & 15, g4 = lg >> 4;
+    // the Gram K K^T by bf16 MFMA 16x16x32 (the A and B operands are the same
+    // values): k-step s covers columns 32s + 4g .. + 3 and 32s + 16 + 4g .. + 3
+    // of slot n
+    f32x4 gk = {};
+    if constexpr (RAWK) {  // the raw rows: exact products, normed below
+      const uint16_t* praw = reinterpret_cast<const uint16_t*>(pkey);
+      const int op = qkv_op4(n16, g4);
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const bf16x8 kr = lds_bf16x8_split(praw + (op ^ (32 * s)), praw + (op ^ (32 * s + 16)));
+        gk = mfma_bf16_16x16x32(kr, kr, gk);
+      }
+    } else {
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        bf16x8 kh, kl;
+        pkey_split(pkey, n16, s, g4, kh, kl);
+        gk = mfma_bf16_16x16x32(kh, kh, gk);
+        gk = mfma_bf16_16x16x32(kh, kl, gk);
+        gk = mfma_bf16_16x16x32(kl, kh, gk);
+      }
+    }
+    // slots p = 4g + e (row) and n (column), at path positions rvn_slot(p)
+    // and rvn_slot(n): A_pn is on where n's position precedes p's
+    const int iq = rvn_slot(n16);
+    const float gq = __shfl(pv.gl, iq), rq = RAWK ? rvx[kRvxNorms + n16] : 1.f;
+    const bool okq = (pd.vmask >> iq) & 1u;
+    f32x4 ia;  // I - A in the accumulator layout
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int p = 4 * g4 + e, ip = 4 * e + g4;  // element e of lane (n, g): A[4g + e][n]
+      const bool on = iq < ip && okq && ((pd.vmask >> ip) & 1u);
+      // (the shuffles outside the select: inside it they become a branch,
+      // and a lane reads another that the branch has switched off)
+      const float bp = __shfl(beta, ip), gpp = __shfl(pv.gl, ip);
+      const float rp = RAWK ? rvx[kRvxNorms + p] : 1.f;
+      const float a = on ? bp * __expf(gpp - gq) * (rp * rq * gk[e]) : 0.f;
+      rvx[p * 17 + n16] = a;
+      ia[e] = (p == n16 ? 1.f : 0.f) - a;
+    }
+    float* a2 = rvx + 16 * 17;
+    float* a4 = rvx + 2 * 16 * 17;
+    float* a8 = rvx + 3 * 16 * 17;
+    const f32x4 zero = {};
+    const int len = pd.last + 1;  // A^len = 0 (uniform)
+    f32x4 x = ia;                 // I - A: X when A^2 = 0
+    if (len > 2) {
+      mat16_store(a2, mat16_mul(rvx, rvx, zero, n16, g4), n16, g4);
+      if (len > 4) mat16_store(a4, mat16_mul(a2, a2, zero, n16, g4), n16, g4);
+      if (len > 8) mat16_store(a8, mat16_mul(a4, a4, zero, n16, g4), n16, g4);
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {  // (I - A) + (I - A) A^2
+        const int k = 4 * g4 + m;
+        x = mfma_f32_16x16x4((n16 == k ? 1.f : 0.f) - rvx[n16 * 17 + k], a2[k * 17 + n16], x);
+      }
+      if (len > 4) {
+        mat16_store(a2, x, n16, g4);
+        x = mat16_mul(a2, a4, x, n16, g4);  // ... (I + A^4)
+      }
+      if (len > 8) {
+        mat16_store(a2, x, n16, g4);
+        x = mat16_mul(a2, a8, x, n16, g4);  // ... (I + A^8)
+      }
+    }
+    mat16_store(rvx, x, n16, g4);  // X over A
+  }
+  // Ck by bf16 MFMA 16x16x32 on the tile registers: k-step s takes groups 2s
+  // and 2s + 1 of the tile, k = 32s + 4g + e and 32s + 16 + 4g + e, as the
+  // key operand does.  (Its key reads stay below the solve: hoisted above it,
+  // they and the solve's operands together spilled at the 32-wide kernel's
+  // register cap.)
+  asm volatile("" ::: "memory");
+  int lk = lane;
+  asm volatile("" : "+v"(lk));
+  const int n16k = lk & 15, g4k = lk >> 4;
+  f32x4 w[TT];
+#pragma unroll
+  for (int t = 0; t < TT; ++t) w[t] = f32x4{};
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    bf16x8 kh, kl;
+    if constexpr (RAWK) {
+      const uint16_t* praw = reinterpret_cast<const uint16_t*>(pkey);
+      const int op = qkv_op4(n16k, g4k);
+      kh = lds_bf16x8_split(praw + (op ^ (32 * s)), praw + (op ^ (32 * s + 16)));
+    } else {
+      pkey_split(pkey, n16k, s, g4k, kh, kl);
+    }
+#pragma unroll
+    for (int t = 0; t < TT; ++t) {
+      const float xs[8] = {s0r[t][2 * s][0],     s0r[t][2 * s][1],     s0r[t][2 * s][2],     s0r[t][2 * s][3],
+                           s0r[t][2 * s + 1][0], s0r[t][2 * s + 1][1], s0r[t][2 * s + 1][2], s0r[t][2 * s + 1][3]};
+      bf16x8 sh, sl;
+      split_bf16x8(xs, sh, sl);
+      w[t] = mfma_bf16_16x16x32(kh, sh, w[t]);
+      w[t] = mfma_bf16_16x16x32(kh, sl, w[t]);
+      if constexpr (!RAWK) w[t] = mfma_bf16_16x16x32(kl, sh, w[t]);
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int p = 4 * g4 + e, ip = 4 * e + g4;  // slot, position
+    const float bp = __shfl(beta, ip);
+    const float ep = __expf(__shfl(pv.gl, ip)) * (RAWK ? rvx[kRvxNorms + p] : 1.f);
+    const bool ok = (pd.vmask >> ip) & 1u;
+#pragma unroll
+    for (int t = 0; t < TT; ++t) w[t][e] = ok ? bp * (bf16_bits_to_f32(vr[e][t]) - ep * w[t][e]) : 0.f;
+  }
+  __syncthreads();  // X complete
+  f32x4 vn[TT];
+#pragma unroll
+  for (int t = 0; t < TT; ++t) vn[t] = f32x4{};
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    if (4 * m > pd.last) break;  // uniform: k-step m holds positions 4m .. 4m + 3
+    const float a = rvx[n16 * 17 + 4 * g4 + m];  // X[n][k = 4g + m]; B = W[4g + m][v], element m
+#pragma unroll
+    for (int t = 0; t < TT; ++t) vn[t] = mfma_f32_16x16x4(a, w[t][m], vn[t]);
+  }
+#pragma unroll
+  for (int s = 0; s < 4; ++s)
+#pragma unroll
+    for (int t = 0; t < TT; ++t) vnr[s][t] = vn[t][s];
+}
+
 // The commit of a landed tile (a no-op when nothing is pending; the tile
 // leaves in the MFMA layout either way).  pkey: 16 x 128 floats of LDS that
 // no other wave touches until the next barrier; every thread arrives here
@@ -590,17 +848,47 @@ __device__ __forceinline__ float pending_decay_log(const Pending& pd, const floa
 // whole lines, and is turned into the MFMA layout after the keys are staged:
 // they were loaded after it, so it has landed, and their registers are free
 // by then.
-template <int NW, bool LINES, bool RAWK>
-__device__ __forceinline__ void commit_tile(const Pending& pd, float* pkey, const PathKeys<NW, RAWK>& kr,
-                                            const float (&vnr)[4][Waves<NW>::TT], const float (&gp)[4], int wave,
-                                            int lane, f32x4 (&s0r)[Waves<NW>::TT][8]) {
+template <int NW, bool LINES, bool RAWK, bool RVN>
+__device__ __forceinline__ void commit_tile(const Pending& pd, float* pkey, float* rvx, const PathKeys<NW, RAWK>& kr,
+                                            const PathVals<NW, RVN>& pv, int wave, int lane,
+                                            f32x4 (&s0r)[Waves<NW>::TT][8]) {
   constexpr int TT = Waves<NW>::TT;
   const int n16 = lane & 15, g4 = lane >> 4;
-  stage_pending_keys<NW, RAWK>(pkey, kr, wave, lane);
+  stage_pending_keys<NW, RAWK, RVN>(pkey, rvx, kr, wave, lane);
   __syncthreads();
   if constexpr (LINES) state_to_mfma<NW>(s0r, lane);
+  float gp[4], vnr[4][TT];
+  if constexpr (RVN) {
+    // The swapped tile in registers of its own: left to itself the compiler
+    // sinks the swap's selects into their first use, the recompute's MFMAs,
+    // and holds the unswapped tile and the rotated halves (96 registers)
+    // until then.  (No instruction crosses the scheduling barriers: the value
+    // loads and gain shuffles hoisted into the swap were spilled.)
+    if constexpr (LINES)
+#pragma unroll
+      for (int t = 0; t < TT; ++t)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) asm volatile("" : "+v"(s0r[t][j]));
+    __builtin_amdgcn_sched_barrier(0);
+    path_values<NW, RAWK>(pd, pkey, rvx, pv, wave, lane, s0r, vnr);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int s = 0; s < 4; ++s) gp[s] = __shfl(pv.gl, 4 * s + g4);
+  } else {
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      gp[s] = pv.g[s];
+#pragma unroll
+      for (int t = 0; t < TT; ++t) vnr[s][t] = pv.v[s][t];
+    }
+  }
   const float gu = pending_decay_log(pd, gp);
   const float eu = pd.last >= 0 ? __expf(gu) : 1.f;
+  // RVN: the loop's key addresses from an opaque lane id, so that they are
+  // computed here rather than held (and spilled) through the recompute
+  int lane_c = lane;
+  if constexpr (RVN) asm volatile("" : "+v"(lane_c));
+  const int n16c = lane_c & 15, g4c = lane_c >> 4;
 #pragma unroll
   for (int t = 0; t < TT; ++t)
 #pragma unroll
@@ -608,14 +896,19 @@ __device__ __forceinline__ void commit_tile(const Pending& pd, float* pkey, cons
 #pragma unroll
   for (int s = 0; s < 4; ++s) {
     if (4 * s > pd.last) break;  // uniform
-    const int p = 4 * s + g4;
+    const int p = 4 * s + g4c;
     const float wgt = ((pd.vmask >> p) & 1u) ? __expf(gu - gp[s]) : 0.f;
     float bv[TT];
 #pragma unroll
     for (int t = 0; t < TT; ++t) bv[t] = wgt * vnr[s][t];
+    // (raw-key recompute form: the raw rows staged, normed as they are read,
+    // which rounds as the staged fp32 keys of the other forms do)
+    const int ks = RVN ? rvn_slot(p) : p;  // the key's staging slot
+    const float rkp = (RAWK && RVN) ? rvx[kRvxNorms + ks] : 1.f;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      const float av = pkey[pkey_at(p, 16 * j + n16)];
+      const float av = (RAWK && RVN) ? bf16_bits_to_f32(reinterpret_cast<const uint16_t*>(pkey)[qkv_at(ks, 16 * j + n16c)]) * rkp
+                                     : pkey[pkey_at(ks, 16 * j + n16c)];
 #pragma unroll
       for (int t = 0; t < TT; ++t) s0r[t][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv[t], s0r[t][j], 0, 0, 0);
     }
@@ -1396,7 +1689,7 @@ __device__ __forceinline__ void fused_status(const Item& it, int lane, uint32_t 
 
 // The body of the one-head-per-workgroup kernels (COMMIT: the fused commit ->
 // verify form).
-template <int NP, bool S0VEC, bool COMMIT, bool RAWK>
+template <int NP, bool S0VEC, bool COMMIT, bool RAWK, bool RVN>
 __device__ __forceinline__ void verify_body(const VerifyParams& P) {
   constexpr int MT = NP / 16;
   constexpr int NW = WavesFor<NP>();
@@ -1436,10 +1729,10 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
       if (pd.last < 0) return;
       f32x4 s0r[TT][8];
       PathKeys<NW, RAWK> kr;
-      float vnr[4][TT], gp[4];
+      PathVals<NW, RVN> pv;
       issue_state<true, kEarly, NW>(S0, p.state_v_stride, wave, lane, s0r);
-      issue_pending<NW, RAWK>(P.c, pd, it.h, wave, lane, S0, kr, vnr, gp);
-      commit_tile<NW, kEarly, RAWK>(pd, sm.pkey(), kr, vnr, gp, wave, lane, s0r);
+      issue_pending<NW, RAWK, RVN>(P.c, pd, it.h, wave, lane, S0, kr, pv);
+      commit_tile<NW, kEarly, RAWK, RVN>(pd, sm.pkey(), sm.rvx, kr, pv, wave, lane, s0r);
       __syncthreads();  // every wave has read the staged keys: am + x take the write-back staging
       store_state<NW>(const_cast<float*>(S0), p.state_v_stride, wave, lane, s0r, sm.amx + wave * 512);
       return;
@@ -1460,7 +1753,7 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
   // beside the tile, they would be spilled.)
   Pending pd{};
   PathKeys<NW, RAWK> kr;
-  float vnr[4][TT], gp[4];
+  PathVals<NW, RVN> pv;
   uint32_t pword = 0;
   if constexpr (COMMIT && !kEarly) pword = *path_word(P.c, it.b, lane);
   if (wave == 0) issue_gates(p, it, lane, S0, sm.graw, COMMIT ? path_word(P.c, it.b, lane) : nullptr);
@@ -1468,7 +1761,7 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
   issue_rows<NP, 0, kPlanes, NW>(p, it, wave, lane, S0, sm);
   if constexpr (COMMIT && !kEarly) {
     pd = decode_pending(ph, lane, pword);
-    issue_pending<NW, RAWK>(P.c, pd, it.h, wave, lane, S0, kr, vnr, gp);
+    issue_pending<NW, RAWK, RVN>(P.c, pd, it.h, wave, lane, S0, kr, pv);
   }
   asm volatile("" ::: "memory");
 
@@ -1517,7 +1810,7 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
   phase_norms<NP, NW>(p, tid, sm, sm);
   __syncthreads();
   if constexpr (COMMIT && !kEarly) {
-    commit_tile<NW, false, RAWK>(pd, sm.pkey(), kr, vnr, gp, wave, lane, s0r);
+    commit_tile<NW, false, RAWK, RVN>(pd, sm.pkey(), sm.rvx, kr, pv, wave, lane, s0r);
     // everything this wave loaded has been consumed: no load is left in
     // flight past the (conditional) write-back
     __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 15));
@@ -1548,9 +1841,9 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
     // the path's entry words came with the gates (row 4); its loads go out
     // now, so that they are not held in registers through phase 1
     pd = decode_pending(ph, lane, sm.graw[4][lane & 15]);
-    issue_pending<NW, RAWK>(P.c, pd, it.h, wave, lane, S0, kr, vnr, gp);
+    issue_pending<NW, RAWK, RVN>(P.c, pd, it.h, wave, lane, S0, kr, pv);
     float* stage = reinterpret_cast<float*>(sm.vrows());  // 8 KiB: the 16 path keys, then the write-back
-    commit_tile<NW, true, RAWK>(pd, stage, kr, vnr, gp, wave, lane, s0r);
+    commit_tile<NW, true, RAWK, RVN>(pd, stage, sm.rvx, kr, pv, wave, lane, s0r);
     __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 15));
     if (pd.last >= 0) {  // uniform over the workgroup (one request)
       __syncthreads();  // every wave has read the staged keys
@@ -1604,17 +1897,18 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
 template <int NP, bool S0VEC>
 __global__ void __launch_bounds__(64 * WavesFor<NP>()) __attribute__((amdgpu_waves_per_eu(4)))
 tree_verify_kernel(const VerifyParams P) {
-  verify_body<NP, S0VEC, false, false>(P);
+  verify_body<NP, S0VEC, false, false, false>(P);
 }
 
 // P must stay this kernel's first (only) argument: out_args<true> reads it
 // back from offset 0 of the kernel-argument segment.
 static_assert(std::is_trivially_copyable<VerifyParams>::value, "VerifyParams is passed by value to the kernels");
-// RAWK: the pending keys are the previous step's raw bf16 rows
-template <int NP, bool RAWK>
+// RAWK: the pending keys are the previous step's raw bf16 rows; RVN: the
+// path's values are recomputed from raw rows
+template <int NP, bool RAWK, bool RVN>
 __global__ void __launch_bounds__(64 * WavesFor<NP>()) __attribute__((amdgpu_waves_per_eu(4)))
 tree_commit_verify_kernel(const VerifyParams P) {
-  verify_body<NP, true, true, RAWK>(P);
+  verify_body<NP, true, true, RAWK, RVN>(P);
 }
 
 static VerifyParams make_params(const dft_verify_args* a) {
@@ -1680,19 +1974,18 @@ int launch_tree_commit_verify(const dft_verify_args* a, const dft_pending_commit
   VerifyParams narrow, wide;
   bool split;
   split_by_size(a, P, narrow, wide, split);
-  const bool raw = c->keys == nullptr;  // the previous step's raw key rows (validated by the caller)
-  if (a->n_nodes > 32) {
-    if (raw)
-      hipLaunchKernelGGL((tree_commit_verify_kernel<64, true>), grid, block64, 0, stream, wide);
-    else
-      hipLaunchKernelGGL((tree_commit_verify_kernel<64, false>), grid, block64, 0, stream, wide);
+  // the previous step's raw key rows, recomputed values (validated by the caller)
+  const int form = (c->keys == nullptr ? 1 : 0) + (c->values == nullptr ? 2 : 0);
+#define DFT_FUSED(np, g, b, prm)                                                                               \
+  switch (form) {                                                                                              \
+    case 0: hipLaunchKernelGGL((tree_commit_verify_kernel<np, false, false>), g, b, 0, stream, prm); break;   \
+    case 1: hipLaunchKernelGGL((tree_commit_verify_kernel<np, true, false>), g, b, 0, stream, prm); break;    \
+    case 2: hipLaunchKernelGGL((tree_commit_verify_kernel<np, false, true>), g, b, 0, stream, prm); break;    \
+    default: hipLaunchKernelGGL((tree_commit_verify_kernel<np, true, true>), g, b, 0, stream, prm); break;    \
   }
-  if (a->n_nodes <= 32 || split) {
-    if (raw)
-      hipLaunchKernelGGL((tree_commit_verify_kernel<32, true>), grid, block, 0, stream, narrow);
-    else
-      hipLaunchKernelGGL((tree_commit_verify_kernel<32, false>), grid, block, 0, stream, narrow);
-  }
+  if (a->n_nodes > 32) DFT_FUSED(64, grid, block64, wide)
+  if (a->n_nodes <= 32 || split) DFT_FUSED(32, grid, block, narrow)
+#undef DFT_FUSED
   return hipGetLastError() == hipSuccess ? DFT_OK : DFT_ERR_LAUNCH;
 }
 

@@ -233,9 +233,11 @@ def _verify_args(y, a, b, A_log, dt_bias, state, *, hk, hv, anc, anc_bits, batch
 
 def tree_commit_verify(y: torch.Tensor, a: torch.Tensor, b: torch.Tensor, A_log: Optional[torch.Tensor],
                        dt_bias: torch.Tensor, state: torch.Tensor, *, hk: int, hv: int,
-                       pending_path: torch.Tensor, pending_keys: Optional[torch.Tensor], pending_values: torch.Tensor,
-                       pending_gains: torch.Tensor, pending_path_len: Optional[torch.Tensor] = None,
+                       pending_path: torch.Tensor, pending_keys: Optional[torch.Tensor],
+                       pending_values: Optional[torch.Tensor], pending_gains: torch.Tensor,
+                       pending_path_len: Optional[torch.Tensor] = None,
                        pending_key_rows: Optional[torch.Tensor] = None,
+                       pending_value_rows: Optional[torch.Tensor] = None, pending_b: Optional[torch.Tensor] = None,
                        prev_cu_seqlens: Optional[torch.Tensor] = None, prev_n_nodes: Optional[int] = None,
                        pending_k_head_div: int = 1, anc: Optional[torch.Tensor] = None,
                        anc_bits: Optional[torch.Tensor] = None, batch: Optional[int] = None,
@@ -255,7 +257,14 @@ def tree_commit_verify(y: torch.Tensor, a: torch.Tensor, b: torch.Tensor, A_log:
     ``pending_key_rows`` may give the previous step's raw bf16 key rows
     [rows, hk, 128], e.g. ``prev_y[:, hk*128:2*hk*128].unflatten(1, (hk, 128))``,
     which the commit normalises itself: the verify then needs no aux_k.
-    Previous rows of request b start at prev_cu_seqlens[b] or
+    Likewise, instead of saved values (pending_values None), the commit can
+    recompute the path's values from the previous step's raw bf16 value rows
+    ``pending_value_rows`` [rows, hv, 128] (``prev_y[:, 2*hk*128:]``) and b
+    gates ``pending_b`` [rows, hv], with the state the slot holds: then the
+    verify needs no aux_v.  That form requires every pending path to be a
+    walk from its tree's root (each entry's ancestors are the entries before
+    it), as an accepted path is, and the slot to hold the state the previous
+    verify read.  Previous rows of request b start at prev_cu_seqlens[b] or
     b * prev_n_nodes.  Returns o.  ``status`` as in ``tree_verify``, plus
     DFT_STATUS_PATH for a pending entry past the previous tree (the entry is
     ignored)."""
@@ -264,18 +273,25 @@ def tree_commit_verify(y: torch.Tensor, a: torch.Tensor, b: torch.Tensor, A_log:
         cu_seqlens=cu_seqlens, scale=scale, neg_exp_A=neg_exp_A, state_indices=state_indices,
         state_slot_stride=state_slot_stride, o=o, o_dtype=o_dtype, aux_k=aux_k, aux_v=aux_v, aux_g=aux_g,
         aux_k_per_khead=aux_k_per_khead, status=status)
-    _device_of(pending_path, pending_keys, pending_key_rows, pending_values, pending_gains, pending_path_len,
-               prev_cu_seqlens, y)
+    _device_of(pending_path, pending_keys, pending_key_rows, pending_values, pending_value_rows, pending_b,
+               pending_gains, pending_path_len, prev_cu_seqlens, y)
     if (pending_keys is None) == (pending_key_rows is None):
         raise ValueError("give either pending_keys or pending_key_rows")
+    if (pending_values is None) == (pending_value_rows is None):
+        raise ValueError("give either pending_values or pending_value_rows")
+    if (pending_value_rows is None) != (pending_b is None):
+        raise ValueError("pending_value_rows and pending_b go together")
     for t, nm, dims in ((pending_keys, "pending_keys", 3), (pending_values, "pending_values", 3),
                         (pending_gains, "pending_gains", 2)):
         if t is not None:
             _check_aux(t, nm, torch.float32, dims=dims)
-    if pending_key_rows is not None:
-        _check_aux(pending_key_rows, "pending_key_rows", torch.bfloat16, dims=3)
-        if pending_key_rows.shape[-1] != 128:
-            raise ValueError("pending_key_rows is [rows, heads, 128]")
+    for t, nm in ((pending_key_rows, "pending_key_rows"), (pending_value_rows, "pending_value_rows")):
+        if t is not None:
+            _check_aux(t, nm, torch.bfloat16, dims=3)
+            if t.shape[-1] != 128:
+                raise ValueError(f"{nm} is [rows, heads, 128]")
+    if pending_b is not None and (pending_b.dim() != 2 or pending_b.stride(1) != 1):
+        raise ValueError("pending_b is [rows, hv] with unit stride along hv")
     saves = [t for t in (pending_keys, pending_values, pending_gains) if t is not None]
     for out in (aux_k, aux_v, aux_g):
         if out is not None and any(out.data_ptr() == t.data_ptr() for t in saves):
@@ -304,7 +320,13 @@ def tree_commit_verify(y: torch.Tensor, a: torch.Tensor, b: torch.Tensor, A_log:
     else:  # [rows, heads, 128]: row stride first
         c.key_rows = pending_key_rows.data_ptr()
         c.kr_row_stride, c.kr_h_stride = pending_key_rows.stride(0), pending_key_rows.stride(1)
-    c.values, c.v_h_stride, c.v_row_stride = pending_values.data_ptr(), *pending_values.stride()[:2]
+    if pending_values is not None:
+        c.values, c.v_h_stride, c.v_row_stride = pending_values.data_ptr(), *pending_values.stride()[:2]
+    else:  # [rows, hv, 128]: row stride first
+        c.value_rows = pending_value_rows.data_ptr()
+        c.vr_row_stride, c.vr_h_stride = pending_value_rows.stride(0), pending_value_rows.stride(1)
+        c.prev_b, c.pb_row_stride = pending_b.data_ptr(), pending_b.stride(0)
+        c.prev_b_dtype = _ftag(pending_b, "pending_b")
     c.gains, c.g_h_stride, c.g_row_stride = pending_gains.data_ptr(), *pending_gains.stride()
     check("dft_tree_commit_verify", load().dft_tree_commit_verify(C.byref(args), C.byref(c), _stream(dev)))
     return o

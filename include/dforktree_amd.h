@@ -301,6 +301,22 @@ typedef struct dft_pending_commit {
    * aligned (strides multiples of 4 elements). */
   const uint16_t* key_rows;
   int64_t kr_h_stride, kr_row_stride;
+  /* DFT_ABI_VERSION 3 as well.  With values NULL the commit recomputes the
+   * path's values instead of reading saves: vn_t = sum_j X_tj W_j over the
+   * path (X = (I + A)^-1 of the path nodes, A and W as the verify forms them,
+   * W from the state the slot holds, which must be the state the previous
+   * verify read).  Needs the previous step's raw bf16 value rows (row r of
+   * v-head h at value_rows + h vr_h_stride + r vr_row_stride) and its b gates
+   * (element (r, h) at prev_b + r pb_row_stride + h, dtype prev_b_dtype);
+   * the gains are still read.  The valid entries must form a root walk of the
+   * previous tree (each entry's ancestors are the valid entries before it),
+   * as an accepted path does; the verify before such a commit need not save
+   * values (aux_v NULL). */
+  const uint16_t* value_rows;
+  int64_t vr_h_stride, vr_row_stride;
+  const void* prev_b;
+  int64_t pb_row_stride;
+  int32_t prev_b_dtype;
 } dft_pending_commit;
 
 DFT_API int dft_tree_commit_verify(const dft_verify_args* verify, const dft_pending_commit* pending, void* stream);

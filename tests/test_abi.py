@@ -99,6 +99,13 @@ def test_validation_rejects_bad_descriptors_without_launching():
     pc.key_rows, pc.kr_row_stride = 16, 6
     assert lib.dft_tree_commit_verify(ctypes.byref(v), ctypes.byref(pc), None) == _lib.DFT_ERR_INVALID  # stride % 4
     pc.keys, pc.key_rows, pc.kr_row_stride = 16, None, 0
+    pc.value_rows = 16
+    assert lib.dft_tree_commit_verify(ctypes.byref(v), ctypes.byref(pc), None) == _lib.DFT_ERR_INVALID  # values twice
+    pc.values = None
+    assert lib.dft_tree_commit_verify(ctypes.byref(v), ctypes.byref(pc), None) == _lib.DFT_ERR_INVALID  # no b gates
+    pc.prev_b, pc.prev_b_dtype = 16, 99
+    assert lib.dft_tree_commit_verify(ctypes.byref(v), ctypes.byref(pc), None) == _lib.DFT_ERR_INVALID  # b dtype
+    pc.values, pc.value_rows, pc.prev_b, pc.prev_b_dtype = 16, None, None, 0
     pc.path_cols = 17
     assert lib.dft_tree_commit_verify(ctypes.byref(v), ctypes.byref(pc), None) == _lib.DFT_ERR_UNSUPPORTED
     pc.path_cols = 0  # the kernel pads from entry path_cols - 1: at least one column

@@ -11,6 +11,11 @@ separate in-place commit followed by the plain verify to fp32 rounding.
 The raw-key form (the commit normalises step 1's bf16 k rows itself, and
 step 1 saves no keys) is checked against the same oracle chain, and
 against the saved-key form within rel-L2 1e-6 on the committed states.
+So is the recomputed-value form (the commit recomputes the path's values
+from step 1's raw bf16 v rows, b gates and the slot's state, and step 1
+saves no values), and against the saved-value form within rel-L2 1e-5 on
+the committed states (a different solve: fp32 products against the
+verify's split-bf16 block inverse).
 """
 import numpy as np
 import pytest
@@ -58,10 +63,12 @@ def _committed_states(batch1, walks):
 
 
 def _run_chain(cuda, batch1, batch2, per_khead, packed, empty=(), shorten=(), path_dtype=torch.int32,
-               raw_keys=False):
+               raw_keys=False, raw_values=False):
     """Step 1 verifies batch1 (saving k, vn, G); step 2 verifies batch2
     through the fused entry, committing step 1's walks first.  raw_keys: step
-    1 saves no keys, and the commit reads step 1's raw bf16 k rows from its y."""
+    1 saves no keys, and the commit reads step 1's raw bf16 k rows from its y.
+    raw_values: step 1 saves no values, and the commit recomputes them from
+    step 1's raw bf16 v rows (from its y) and b gates."""
     from dforktree_amd import ops
     hk, hv, B = batch1.hk, batch1.hv, batch1.batch
     pool = batch1.state.clone().to(cuda)  # [B, hv, V, K]
@@ -82,7 +89,8 @@ def _run_chain(cuda, batch1, batch2, per_khead, packed, empty=(), shorten=(), pa
     ts1 = ops.tree_struct(g1.parent, 4, cu_seqlens=g1.cu_seqlens, n_nodes=batch1.n_max, batch=B, want=("anc_bits",))
     ts2 = ops.tree_struct(g2.parent, 4, cu_seqlens=g2.cu_seqlens, n_nodes=batch2.n_max, batch=B, want=("anc_bits",))
     ops.tree_verify(g1.y, g1.a, g1.b, g1.A_log, g1.dt_bias, st, hk=hk, hv=hv, anc_bits=ts1["anc_bits"],
-                    aux_k=None if raw_keys else k1, aux_v=v1, aux_g=G1, aux_k_per_khead=per_khead, **kw1)
+                    aux_k=None if raw_keys else k1, aux_v=None if raw_values else v1, aux_g=G1,
+                    aux_k_per_khead=per_khead, **kw1)
     idx, lens, walks = _paths(batch1, 5, empty, shorten)
     prev = dict(prev_cu_seqlens=g1.cu_seqlens) if packed else dict(prev_n_nodes=batch1.n_max)
     if raw_keys:  # the k part of step 1's y, [rows, hk, 128]
@@ -90,9 +98,14 @@ def _run_chain(cuda, batch1, batch2, per_khead, packed, empty=(), shorten=(), pa
                     pending_k_head_div=hv // hk)
     else:
         keys = dict(pending_keys=k1, pending_k_head_div=hv // kh)
+    if raw_values:  # the v part of step 1's y, [rows, hv, 128], and its b gates
+        keys.update(pending_values=None, pending_value_rows=g1.y[:, 2 * hk * 128:].unflatten(1, (hv, 128)),
+                    pending_b=g1.b)
+    else:
+        keys.update(pending_values=v1)
     o2 = ops.tree_commit_verify(g2.y, g2.a, g2.b, g2.A_log, g2.dt_bias, st, hk=hk, hv=hv,
                                 anc_bits=ts2["anc_bits"], pending_path=idx.to(path_dtype).to(cuda),
-                                pending_values=v1, pending_gains=G1, pending_path_len=lens.to(cuda), **keys,
+                                pending_gains=G1, pending_path_len=lens.to(cuda), **keys,
                                 aux_k=k2, aux_v=v2, aux_g=G2, aux_k_per_khead=per_khead, **prev, **kw2)
     torch.cuda.synchronize()
     return pool, o2, (k2, v2, G2), walks
@@ -213,6 +226,42 @@ def test_commit_verify_raw_key_rows_bench_shape(cuda):
     empty, shorten = (9,), (33,)
     pool, o2, aux2, walks = _run_chain(cuda, batch1, batch2, per_khead=True, packed=False, empty=empty,
                                        shorten=shorten, raw_keys=True)
+    _check_chain(batch1, batch2, pool, o2, aux2, walks, empty, per_khead=True)
+
+
+@pytest.mark.parametrize("sizes1,sizes2,packed", [([32] * 6, [32] * 6, False),
+                                                   ([40, 9, 64, 17, 33, 1], [12, 64, 30, 1, 50, 20], True)])
+def test_commit_verify_recomputed_values(cuda, sizes1, sizes2, packed):
+    """The commit recomputes the path's values from the previous step's raw
+    bf16 v rows, b gates and the slot's state (both widths; with raw key rows
+    too); the step-1 verify saves no values.  Against the oracle chain, and
+    against the same chain through saved values."""
+    from dforktree_amd import synth
+    announce(f"commit->verify recomputed values packed={packed}")
+    kinds = ["random", "chain", "bushy", "random", "chain", "bushy"]
+    batch1 = synth.make_batch(46, 0, sizes1, hk=2, hv=4, kinds=kinds)
+    batch2 = synth.make_batch(47, 0, sizes2, hk=2, hv=4, kinds=kinds[::-1])
+    empty, shorten = (2,), (5,)
+    for raw_keys in (False, True):
+        pool, o2, aux2, walks = _run_chain(cuda, batch1, batch2, per_khead=True, packed=packed, empty=empty,
+                                           shorten=shorten, raw_keys=raw_keys, raw_values=True)
+        _check_chain(batch1, batch2, pool, o2, aux2, walks, empty, per_khead=True)
+        pool_s, o2_s, _, _ = _run_chain(cuda, batch1, batch2, per_khead=True, packed=packed, empty=empty,
+                                        shorten=shorten, raw_keys=raw_keys)
+        assert rel_l2(np32(pool), np32(pool_s)) <= 1e-5
+        assert rel_l2(np32(o2), np32(o2_s)) <= 1e-4
+
+
+def test_commit_verify_recomputed_values_bench_shape(cuda):
+    """The measured form at its shape: 64 requests of 32-node trees at full
+    width, keys and values both from step 1's y (the verify saves neither)."""
+    from dforktree_amd import synth
+    announce("commit->verify raw keys + recomputed values, bench shape 64 x 32")
+    batch1 = synth.make_batch(48, 0, [32] * 64, hk=16, hv=32, kinds="random")
+    batch2 = synth.make_batch(49, 0, [32] * 64, hk=16, hv=32, kinds="random")
+    empty, shorten = (11,), (40,)
+    pool, o2, aux2, walks = _run_chain(cuda, batch1, batch2, per_khead=True, packed=False, empty=empty,
+                                       shorten=shorten, raw_keys=True, raw_values=True)
     _check_chain(batch1, batch2, pool, o2, aux2, walks, empty, per_khead=True)
 
 

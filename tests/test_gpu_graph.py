@@ -54,6 +54,7 @@ class Step:
         self.pool0 = self.g1.state.clone()                    # [B, hv, V, K]
         self.pool = self.pool0.clone()                        # fused commit -> verify
         self.rpool = self.pool0.clone()                       # the same with raw key rows
+        self.vpool = self.pool0.clone()                       # raw key rows, recomputed values
         self.cpool0 = self.g1.state.clone().unsqueeze(0)      # [L=1, B, hv, V, K], separate commit
         self.cpool = self.cpool0.clone()
         n = 48
@@ -75,6 +76,7 @@ class Step:
             k2=torch.empty(2, rows, 128, **f32), v2=torch.empty(4, rows, 128, **f32), G2=torch.empty(4, rows, **f32),
             o3=torch.empty(rows, 4, 128, device=cuda, dtype=torch.bfloat16),
             v3=torch.empty(4, rows, 128, **f32), G3=torch.empty(4, rows, **f32),
+            o4=torch.empty(rows, 4, 128, device=cuda, dtype=torch.bfloat16), G4=torch.empty(4, rows, **f32),
             y=torch.empty_like(self.cx), iw=torch.empty(*self.cx.shape, 3, device=cuda, dtype=torch.bfloat16),
             mask=torch.empty(mask_bytes, device=cuda, dtype=torch.uint8),
             mind=torch.empty(self.B + 1, device=cuda, dtype=torch.int32),
@@ -84,6 +86,7 @@ class Step:
     def reset(self):
         self.pool.copy_(self.pool0)
         self.rpool.copy_(self.pool0)
+        self.vpool.copy_(self.pool0)
         self.cpool.copy_(self.cpool0)
         self.inv.copy_(self.inv0)
         for t in self.out.values():
@@ -121,6 +124,14 @@ class Step:
                                pending_key_rows=g1.y[:, 256:512].unflatten(1, (2, 128)), pending_values=o["v1"],
                                pending_gains=o["G1"], pending_path_len=self.lens, pending_k_head_div=2, o=o["o3"],
                                aux_v=o["v3"], aux_g=o["G3"], **prev, **self.shape_kw(g2))
+        # and with the path's values recomputed from step 1's raw v rows and b gates (vpool holds the
+        # state step 1 read)
+        ops.tree_commit_verify(g2.y, g2.a, g2.b, g2.A_log, g2.dt_bias, self.vpool.transpose(-1, -2), hk=2, hv=4,
+                               anc_bits=ts2["anc_bits"], pending_path=self.idx, pending_keys=None,
+                               pending_key_rows=g1.y[:, 256:512].unflatten(1, (2, 128)), pending_values=None,
+                               pending_value_rows=g1.y[:, 512:].unflatten(1, (4, 128)), pending_b=g1.b,
+                               pending_gains=o["G1"], pending_path_len=self.lens, pending_k_head_div=2, o=o["o4"],
+                               aux_g=o["G4"], **prev, **self.shape_kw(g2))
         ops.tree_commit(self.cpool, o["k2"][None], o["v2"][None], o["G2"][None], self.idx2, n_nodes=self.N,
                         k_head_div=2, **(dict(cu_seqlens=g2.cu_seqlens) if self.packed else {}))
         ops.block_inverse_(self.inv)
@@ -130,7 +141,8 @@ class Step:
 
     def snapshot(self, ts):
         got = {k: t.clone() for k, t in self.out.items()}
-        got.update(pool=self.pool.clone(), rpool=self.rpool.clone(), cpool=self.cpool.clone(), inv=self.inv.clone())
+        got.update(pool=self.pool.clone(), rpool=self.rpool.clone(), vpool=self.vpool.clone(), cpool=self.cpool.clone(),
+                   inv=self.inv.clone())
         got.update({f"ts_{k}": v.clone() for k, v in ts.items()})
         return got
 
@@ -148,9 +160,10 @@ def _replays(cuda, step):
     torch.cuda.synchronize()
     want = step.snapshot(step.run())
     torch.cuda.synchronize()
-    for name in ("o1", "o2", "o3", "k2", "mask", "pb"):
+    for name in ("o1", "o2", "o3", "o4", "k2", "mask", "pb"):
         assert not torch.equal(want[name], torch.full_like(want[name], SENTINEL[want[name].dtype])), name
     assert not torch.equal(want["pool"], step.pool0) and not torch.equal(want["cpool"], step.cpool0)
+    assert not torch.equal(want["vpool"], step.pool0)
 
     # capture on a side stream after one warm-up there, as torch.cuda.graph requires
     s = torch.cuda.Stream()
