@@ -110,7 +110,7 @@ class Workload:
             self.verify(l)
         self.commit()
 
-    def fused(self, l, raw_keys=True, raw_values=False):
+    def fused(self, l, raw_keys=True, raw_values=True):
         """One layer of the pipelined schedule.  raw_keys: the commit reads the
         previous step's raw k rows from its y and normalises them, so this
         step's verify saves no keys; else it reads the previous step's saved
@@ -193,7 +193,7 @@ class Workload:
                    + HK * N * D * 4)       # normalised k fp32 write (per k-head)
         return B * per_req
 
-    def fused_bytes_per_launch(self, raw_keys=True, raw_values=False):
+    def fused_bytes_per_launch(self, raw_keys=True, raw_values=True):
         """verify bytes + the committed tile written back + the path's saves.
         raw_keys: no keys are saved, and the path's keys are read as raw bf16
         rows (per k-head) instead of saved fp32 ones.  raw_values: no values
@@ -533,10 +533,11 @@ def main():
     torch.cuda.synchronize()
     t_fused_layers = time_graph(lambda: [w.fused(l) for l in range(L)], reps_kernel, args.warmup, args.eager)
     t_fused = t_fused_layers / L
-    t_fused_saved = time_graph(lambda: [w.fused(l, raw_keys=False) for l in range(L)], reps_kernel, args.warmup,
-                               args.eager) / L
-    t_fused_rv = time_graph(lambda: [w.fused(l, raw_values=True) for l in range(L)], reps_kernel, args.warmup,
+    # the same launch reading saved values (raw key rows), and saved keys and values
+    t_fused_sv = time_graph(lambda: [w.fused(l, raw_values=False) for l in range(L)], reps_kernel, args.warmup,
                             args.eager) / L
+    t_fused_saved = time_graph(lambda: [w.fused(l, raw_keys=False, raw_values=False) for l in range(L)], reps_kernel,
+                               args.warmup, args.eager) / L
     t_step = time_graph(w.fused_step, args.steps, args.warmup, args.eager)
     # conv and mask run once per layer in a step: 24 back-to-back launches per replay, as for verify
     w.conv_setup(dev)
@@ -610,19 +611,21 @@ def main():
                    "layers": L, "qk_heads": HK, "v_heads": HV, "dk": D, "dv": D, "tree": "random recursive",
                    "accepted_path": "random walk, length 1-16",
                    "schedule": "pipelined: each layer's launch commits the previous step's path (its keys "
-                               "normalised from the previous step's raw k rows), then verifies",
+                               "normalised from the previous step's raw k rows, its values recomputed from the "
+                               "previous step's raw v rows and b gates), then verifies",
                    "timing": "eager" if args.eager else "hip graph"},
         "roofline": {"kernel": dom, "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "algorithmic_bytes_per_launch": kd["bytes"]},
         "mfma": mfma,
         "commit_verify_us_per_layer": round(t_fused * 1e3, 2),
-        # the same launch with the keys saved by the verify and read back by the next commit
+        # the same launch with the values saved by the verify and read back by the next commit (keys from the
+        # raw rows), and with both keys and values saved
+        "commit_verify_saved_values": {"us_per_layer": round(t_fused_sv * 1e3, 2),
+                                       "hbm_frac": frac(w.fused_bytes_per_launch(raw_values=False), t_fused_sv)},
         "commit_verify_saved_keys": {"us_per_layer": round(t_fused_saved * 1e3, 2),
-                                     "hbm_frac": frac(w.fused_bytes_per_launch(raw_keys=False), t_fused_saved)},
-        # with the path's values recomputed by the commit (the verify saves no values)
-        "commit_verify_recomputed_values": {"us_per_layer": round(t_fused_rv * 1e3, 2),
-                                            "hbm_frac": frac(w.fused_bytes_per_launch(raw_values=True), t_fused_rv)},
+                                     "hbm_frac": frac(w.fused_bytes_per_launch(raw_keys=False, raw_values=False),
+                                                      t_fused_saved)},
         # state bytes the separate kernels need (verify read + commit read and write) per unit time,
         # and the state bytes the pipelined schedule actually moves (one read + one write)
         "state_traffic_hbm_frac": frac(w.state_bytes_per_step(), t_step),

@@ -222,10 +222,6 @@ __device__ __forceinline__ int pkey_at(int p, int c) { return p * kD + ((((c >> 
 // into the q region once Cq/Ck have consumed it, and o is staged in x once the
 // vn tiles have consumed X.  That keeps the workgroup under 80 KiB of LDS, so
 // two of them fit on a CU.
-// LDS of the recomputed path values: four 16 x 16 matrices (row pitch 17),
-// then the 16 key norms of the raw-key form
-constexpr int kRvxNorms = 4 * 16 * 17, kRvx = kRvxNorms + 16;
-
 template <int NP, bool LATE_V>
 struct VRegion {
   uint16_t v[NP * kD];
@@ -252,7 +248,6 @@ struct VerifySmem : VRegion<NP, (NP > 32)> {
   alignas(16) float cO[NP];
   alignas(16) uint64_t anc[NP];
   uint32_t graw[6][64];  // per lane of wave 0: words of a, b, ancestry bits lo / hi, dt_bias, decay
-  alignas(16) float rvx[kRvx];  // the fused commit's recomputed path values: A, its powers, X; key norms
   __device__ float* am() { return amx; }
   __device__ const float* am() const { return amx; }
   __device__ float* x() { return amx + NP * LDA; }
@@ -395,6 +390,10 @@ struct Pending {
   bool bad;        // an entry within the length names a node past the previous tree
   int64_t prow0;   // row of the request's node 0 in the previous step's buffers
 };
+
+// LDS of the recomputed path values: four 16 x 16 matrices (row pitch 17),
+// then the 16 key norms of the raw-key form
+constexpr int kRvxNorms = 4 * 16 * 17, kRvx = kRvxNorms + 16;
 
 // The recompute's slot of path position i, and the position of slot i (the
 // map is its own inverse): positions 4m .. 4m + 3 take slots m, 4 + m, 8 + m,
@@ -1703,6 +1702,9 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
   constexpr int kStateLoads = 8 * TT, kGroupLoads = 2 * TT;   // per lane: whole tile, one k-step group
   const dft_verify_args& p = P.a;
   __shared__ VerifySmem<NP> sm;
+  // the recomputed path values' matrices and key norms: only the forms that
+  // recompute them hold them (4.3 KiB)
+  __shared__ alignas(16) float rvx[RVN ? kRvx : 4];
 
   // (the wave index as a scalar: in a vector register it is held, and at the
   // fused form's register cap spilled, through phase 1)
@@ -1732,7 +1734,7 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
       PathVals<NW, RVN> pv;
       issue_state<true, kEarly, NW>(S0, p.state_v_stride, wave, lane, s0r);
       issue_pending<NW, RAWK, RVN>(P.c, pd, it.h, wave, lane, S0, kr, pv);
-      commit_tile<NW, kEarly, RAWK, RVN>(pd, sm.pkey(), sm.rvx, kr, pv, wave, lane, s0r);
+      commit_tile<NW, kEarly, RAWK, RVN>(pd, sm.pkey(), rvx, kr, pv, wave, lane, s0r);
       __syncthreads();  // every wave has read the staged keys: am + x take the write-back staging
       store_state<NW>(const_cast<float*>(S0), p.state_v_stride, wave, lane, s0r, sm.amx + wave * 512);
       return;
@@ -1810,7 +1812,7 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
   phase_norms<NP, NW>(p, tid, sm, sm);
   __syncthreads();
   if constexpr (COMMIT && !kEarly) {
-    commit_tile<NW, false, RAWK, RVN>(pd, sm.pkey(), sm.rvx, kr, pv, wave, lane, s0r);
+    commit_tile<NW, false, RAWK, RVN>(pd, sm.pkey(), rvx, kr, pv, wave, lane, s0r);
     // everything this wave loaded has been consumed: no load is left in
     // flight past the (conditional) write-back
     __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 15));
@@ -1843,7 +1845,7 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
     pd = decode_pending(ph, lane, sm.graw[4][lane & 15]);
     issue_pending<NW, RAWK, RVN>(P.c, pd, it.h, wave, lane, S0, kr, pv);
     float* stage = reinterpret_cast<float*>(sm.vrows());  // 8 KiB: the 16 path keys, then the write-back
-    commit_tile<NW, true, RAWK, RVN>(pd, stage, sm.rvx, kr, pv, wave, lane, s0r);
+    commit_tile<NW, true, RAWK, RVN>(pd, stage, rvx, kr, pv, wave, lane, s0r);
     __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 15));
     if (pd.last >= 0) {  // uniform over the workgroup (one request)
       __syncthreads();  // every wave has read the staged keys
