@@ -252,17 +252,22 @@ class RaggedWorkload:
         self.cu = torch.tensor([0] + torch.tensor(self.sizes).cumsum(0).tolist(), dtype=torch.int32, device=dev)
         self.anc_bits = ops.tree_struct(parents, 4, cu_seqlens=self.cu, n_nodes=64, batch=self.RB,
                                         want=("anc_bits",))["anc_bits"]
+        # the requests by size class, once per step like the tree structure, and the count of trees of at most
+        # 32 nodes, which the host knows: each kernel of the split launch runs exactly its own requests
+        self.order = ops.size_order(self.cu, 64)
+        self.n_small = sum(1 for n in self.sizes if n <= 32)
         self.o = torch.empty(L, rows, HV, D, device=dev, dtype=torch.bfloat16)
         self.keys = torch.empty(L, HK, rows, D, device=dev)
         self.vals = torch.empty(L, HV, rows, D, device=dev)
         self.gains = torch.empty(L, HV, rows, device=dev)
 
-    def verify(self, l):
+    def verify(self, l, ordered=True):
         from dforktree_amd import ops
         ops.tree_verify(self.y[l], self.a[l], self.b[l], self.A_log, self.dt_bias, self.state[l].transpose(-1, -2),
                         hk=HK, hv=HV, anc_bits=self.anc_bits, batch=self.RB, n_nodes=64, cu_seqlens=self.cu,
                         neg_exp_A=self.neg, o=self.o[l], aux_k=self.keys[l], aux_v=self.vals[l],
-                        aux_g=self.gains[l], aux_k_per_khead=True)
+                        aux_g=self.gains[l], aux_k_per_khead=True, size_order=self.order if ordered else None,
+                        size_order_small=self.n_small if ordered else None)
 
     def bytes_per_launch(self, lo=0, hi=64):
         """Algorithmic bytes of the requests with lo <= nodes <= hi: per
@@ -548,9 +553,12 @@ def main():
     if not args.no_ragged:
         rw = RaggedWorkload(dev)  # both workloads fit together (about 17 GB)
         t_ragged = time_graph(lambda: [rw.verify(l) for l in range(L)], reps_kernel, args.warmup, args.eager) / L
+        t_unord = time_graph(lambda: [rw.verify(l, ordered=False) for l in range(L)], reps_kernel, args.warmup,
+                             args.eager) / L
         ragged = {"workload": "packed ragged batch: 128 requests, trees of 8-64 nodes (chains / bushy / random), "
-                              "verify",
+                              "verify, each kernel of the split launch taking its size class's requests first",
                   "nodes": rw.rows, "us_per_layer": round(t_ragged * 1e3, 2),
+                  "unordered_us_per_layer": round(t_unord * 1e3, 2),
                   "nodes_per_s_per_layer": round(rw.rows / (t_ragged * 1e-3), 1),
                   "hbm_frac": round(rw.bytes_per_launch() / (t_ragged * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
     plugin = None

@@ -13,10 +13,10 @@ LIB_PATH = Path(__file__).resolve().parent / "libdforktree_amd.so"
 
 DFT_OK, DFT_ERR_INVALID, DFT_ERR_UNSUPPORTED, DFT_ERR_LAUNCH = 0, 1, 2, 3
 DFT_F32, DFT_BF16, DFT_F16, DFT_I32, DFT_I64 = 0, 1, 2, 3, 4
-DFT_VERIFY_AUX_K_PER_KHEAD = 1
+DFT_VERIFY_AUX_K_PER_KHEAD, DFT_VERIFY_ORDER_COUNT = 1, 2
 DFT_COMMIT_KV, DFT_COMMIT_CHECK_ANC, DFT_COMMIT_LEN_IS_LAST = 1, 2, 4
-DFT_STATUS_SPAN, DFT_STATUS_PATH = 1, 2
-ABI_VERSION = 3
+DFT_STATUS_SPAN, DFT_STATUS_PATH, DFT_STATUS_ORDER = 1, 2, 4
+ABI_VERSION = 4
 
 i32, i64, f32, vp = C.c_int32, C.c_int64, C.c_float, C.c_void_p
 
@@ -41,6 +41,7 @@ class VerifyArgs(C.Structure):
         ("aux_v", vp), ("aux_v_h_stride", i64), ("aux_v_row_stride", i64),
         ("aux_g", vp), ("aux_g_h_stride", i64), ("aux_g_row_stride", i64),
         ("status", vp),
+        ("size_order", vp), ("size_order_small", i32),
     ]
 
 
@@ -146,8 +147,8 @@ class MaskArgs(C.Structure):
 DFT_BITS_LITTLE, DFT_BITS_BIG = 0, 1
 
 EXPORTS = ("dft_tree_verify", "dft_tree_commit_verify", "dft_tree_conv", "dft_tree_commit", "dft_tree_struct",
-           "dft_anc_pack", "dft_block_inverse", "dft_packbits", "dft_tree_mask_pack", "dft_error_string",
-           "dft_abi_version")
+           "dft_anc_pack", "dft_block_inverse", "dft_packbits", "dft_tree_mask_pack", "dft_size_order",
+           "dft_error_string", "dft_abi_version")
 
 
 class LibraryMissing(RuntimeError):
@@ -180,7 +181,8 @@ def load() -> C.CDLL:
                        ("dft_anc_pack", [C.POINTER(AncPackArgs), vp]),
                        ("dft_packbits", [C.POINTER(PackbitsArgs), vp]),
                        ("dft_tree_mask_pack", [C.POINTER(MaskArgs), vp]),
-                       ("dft_block_inverse", [vp, i32, i32, i64, vp])):
+                       ("dft_block_inverse", [vp, i32, i32, i64, vp]),
+                       ("dft_size_order", [vp, i32, i32, vp, vp])):
         fn = getattr(lib, name)
         fn.argtypes = argt
         fn.restype = C.c_int

@@ -8,6 +8,7 @@ namespace dft {
 int launch_tree_verify(const dft_verify_args* a, hipStream_t stream);
 int launch_tree_commit_verify(const dft_verify_args* a, const dft_pending_commit* c, hipStream_t stream);
 int launch_block_inverse(float* x, int n_mats, int n, int64_t mat_stride, hipStream_t stream);
+int launch_size_order(const int32_t* cu_seqlens, int batch, int n_nodes, int32_t* order, hipStream_t stream);
 int launch_tree_conv(const dft_conv_args* a, hipStream_t stream);
 int launch_tree_commit(const dft_commit_args* a, hipStream_t stream);
 int launch_tree_struct(const dft_tree_args* a, hipStream_t stream);
@@ -45,6 +46,11 @@ int verify_status(const dft_verify_args* a) {
   if (a->state_indices && !index_tag(a->state_indices_dtype)) return DFT_ERR_INVALID;
   // q/k/v rows are copied as 16-byte pieces
   if (!aligned16(a->y) || a->y_row_stride % 8 != 0) return DFT_ERR_INVALID;
+  // size-order records: 16-byte records of a packed batch
+  if (a->size_order && (!a->cu_seqlens || !aligned16(a->size_order))) return DFT_ERR_INVALID;
+  if ((a->flags & DFT_VERIFY_ORDER_COUNT) &&
+      (!a->size_order || a->size_order_small < 0 || a->size_order_small > a->batch))
+    return DFT_ERR_INVALID;
   // one workgroup per (request, v-head): 4 waves for trees of up to 32 nodes, 8 beyond
   if ((int64_t)a->batch * a->hv > max_blocks(a->n_nodes > 32 ? 512 : 256)) return DFT_ERR_UNSUPPORTED;
   return DFT_OK;
@@ -94,6 +100,12 @@ int dft_tree_commit_verify(const dft_verify_args* a, const dft_pending_commit* c
       a->state_slot_stride % 4)
     return DFT_ERR_UNSUPPORTED;
   return dft::launch_tree_commit_verify(a, c, static_cast<hipStream_t>(stream));
+}
+
+int dft_size_order(const int32_t* cu_seqlens, int32_t batch, int32_t n_nodes, int32_t* order, void* stream) {
+  if (batch < 0 || n_nodes < 1 || n_nodes > 64 || !cu_seqlens || !order) return DFT_ERR_INVALID;
+  if (!aligned16(order)) return DFT_ERR_INVALID;  // 16-byte records
+  return dft::launch_size_order(cu_seqlens, batch, n_nodes, order, static_cast<hipStream_t>(stream));
 }
 
 int dft_block_inverse(float* x, int32_t n_mats, int32_t n, int64_t mat_stride, void* stream) {

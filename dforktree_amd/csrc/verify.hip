@@ -144,6 +144,10 @@ struct VerifyParams {
   int o_stage;   // o is bf16 with 16-byte aligned head rows: written through LDS
   int n_lo, n_hi;  // packed launches split by tree size: this kernel takes the
                    // requests with n_lo <= nodes <= n_hi (the others exit at once)
+  int cls;         // with a.size_order: this kernel's size class (0: at most 32
+                   // nodes, 1: more), its requests read from the order records; -1: none
+  int order_small; // the caller's count of class-0 requests (the grids are sized
+                   // from it), -1 when unknown (both grids cover every request)
 };
 
 // The output fields a workgroup needs only at the end of its life (the key
@@ -987,11 +991,12 @@ struct Item {
   const float* S0;   // the head's state tile (k stride 1 on the vector paths)
 };
 
-// block id -> (request, v-head); the R v-heads sharing a k-head get ids 8
-// apart so that they land on the same XCD (shared q/k rows in its L2)
-__device__ __forceinline__ void item_heads(const dft_verify_args& p, int id, Item& it) {
+// block id -> (request, v-head) over nb requests (the batch, or a size
+// class's count); the R v-heads sharing a k-head get ids 8 apart so that
+// they land on the same XCD (shared q/k rows in its L2)
+__device__ __forceinline__ void item_heads(const dft_verify_args& p, int id, int nb, Item& it) {
   const int R = p.hv / p.hk;
-  const int pairs = p.batch * p.hk;
+  const int pairs = nb * p.hk;
   const int full = (pairs / 8) * 8 * R;
   int pair, rr;
   if (id < full) {
@@ -1009,14 +1014,43 @@ __device__ __forceinline__ void item_heads(const dft_verify_args& p, int id, Ite
   it.h = it.hk * R + rr;
 }
 
+// With the caller's class count hs, each kernel's grid covers hs (class 0)
+// or batch - hs (class 1) requests.  If hs disagrees with the records, the
+// class whose grid is short leaves requests out; the other kernel's first
+// thread marks them DFT_STATUS_ORDER (its grid is the longer one, so it
+// exists).  No other block writes those status words.
+__device__ __forceinline__ void order_misses(const dft_verify_args& p, int cls, int hs) {
+  if (!p.status) return;
+  const int4* ord = reinterpret_cast<const int4*>(p.size_order);
+  const int4 hd = ord[0];
+  if (cls == 0)  // class 1 launched batch - hs blocks' worth of requests: records hd.y past them are missed
+    for (int q = p.batch - hs; q < hd.y; ++q) p.status[ord[p.batch - q].x] = DFT_STATUS_ORDER;
+  else  // class 0 launched hs requests' worth
+    for (int q = hs; q < hd.x; ++q) p.status[ord[1 + q].x] = DFT_STATUS_ORDER;
+}
+
 // rows, node count and state tile of a request (loads the index arrays).
 // A row span that is negative or exceeds n_nodes is cut to [0, n_nodes] and
 // flagged.  Returns false when the request belongs to the other kernel of a
 // launch split by tree size (its node count outside [n_lo, n_hi]).
+//
+// With size-order records (cls >= 0) the block's request index q counts the
+// kernel's own class: record q from the front (class 0) or from the back
+// (class 1), read with the class counts in one pair of independent loads;
+// q past the class's count exits (those blocks come last in the grid).
 template <int NP>
-__device__ __forceinline__ bool item_rows(const dft_verify_args& p, Item& it, int n_lo, int n_hi) {
+__device__ __forceinline__ bool item_rows(const dft_verify_args& p, Item& it, int n_lo, int n_hi, int cls) {
   int span;
-  if (p.cu_seqlens) {
+  if (cls >= 0) {
+    const int4* ord = reinterpret_cast<const int4*>(p.size_order);
+    const int q = it.b;
+    const int4 hd = ord[0];
+    const int4 e = ord[1 + (cls == 0 ? q : p.batch - 1 - q)];
+    if (q >= (cls == 0 ? hd.x : hd.y)) return false;
+    it.b = e.x;
+    it.row0 = e.y;
+    span = e.z;
+  } else if (p.cu_seqlens) {
     it.row0 = p.cu_seqlens[it.b];
     span = p.cu_seqlens[it.b + 1] - p.cu_seqlens[it.b];
   } else {
@@ -1712,8 +1746,10 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
   const int n16 = lane & 15, g4 = lane >> 4;
 
   Item it;
-  item_heads(p, blockIdx.x, it);
-  if (!item_rows<NP>(p, it, P.n_lo, P.n_hi)) return;
+  if (P.cls >= 0 && P.order_small >= 0 && blockIdx.x == 0 && tid == 0) order_misses(p, P.cls, P.order_small);
+  item_heads(p, blockIdx.x, P.cls < 0 || P.order_small < 0 ? p.batch : P.cls == 0 ? P.order_small
+                                                                                 : p.batch - P.order_small, it);
+  if (!item_rows<NP>(p, it, P.n_lo, P.n_hi, P.cls)) return;
   // Thread 0 of the request's head-0 workgroup writes its status word (the
   // condition is evaluated where it is written: held from here, it would
   // cost the fused kernel a register through the state stream).
@@ -1928,6 +1964,8 @@ static VerifyParams make_params(const dft_verify_args* a) {
               (a->o_h_stride % 8) == 0;
   P.n_lo = INT_MIN;
   P.n_hi = INT_MAX;
+  P.cls = -1;
+  P.order_small = -1;
   return P;
 }
 
@@ -1936,7 +1974,9 @@ static VerifyParams make_params(const dft_verify_args* a) {
 // requests of 33-64 nodes and the 32-wide kernel (four per CU) the rest, each
 // exiting at once on the other's requests.  The sizes stay on the device.
 // The 64-wide kernel goes first: the reverse order measured 0.4% slower on
-// 128 requests of 8-64 nodes.
+// 128 requests of 8-64 nodes.  With size-order records each kernel takes its
+// own class's requests from the front of its grid, and its exiting blocks
+// come last.
 static void split_by_size(const dft_verify_args* a, const VerifyParams& P, VerifyParams& narrow, VerifyParams& wide,
                           bool& split) {
   narrow = wide = P;
@@ -1944,26 +1984,93 @@ static void split_by_size(const dft_verify_args* a, const VerifyParams& P, Verif
   if (split) {
     narrow.n_hi = 32;
     wide.n_lo = 33;
+    if (a->size_order) {
+      narrow.cls = 0;
+      wide.cls = 1;
+      if (a->flags & DFT_VERIFY_ORDER_COUNT) narrow.order_small = wide.order_small = a->size_order_small;
+    }
   }
+}
+
+// the grids of a launch: one block per (request, v-head) of the kernel's
+// requests (a size class's count when the caller gave it)
+static void split_grids(const dft_verify_args* a, const VerifyParams& wide, bool split, dim3& g_narrow, dim3& g_wide) {
+  unsigned nn = (unsigned)a->batch, nw = (unsigned)a->batch;
+  if (split && wide.order_small >= 0) {
+    nn = (unsigned)wide.order_small;
+    nw = (unsigned)(a->batch - wide.order_small);
+  }
+  g_narrow = dim3(nn * (unsigned)a->hv);
+  g_wide = dim3(nw * (unsigned)a->hv);
+}
+
+// Requests by size class (dft_size_order): one workgroup, chunks of 1024
+// requests; per chunk each wave counts its classes by ballot, and the block
+// adds the counts of the waves before it.  Class 0 (at most 32 nodes) fills
+// records 0, 1, .. and class 1 records batch - 1, batch - 2, .., both in
+// request order.
+__global__ void __launch_bounds__(1024) size_order_kernel(const int32_t* cu, int batch, int n_nodes, int4* order) {
+  __shared__ int counts[16][2];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  int done_small = 0, done_large = 0;
+  for (int c0 = 0; c0 < batch; c0 += 1024) {
+    const int i = c0 + tid;
+    const bool in = i < batch;
+    const int row0 = in ? cu[i] : 0;
+    const int span = in ? cu[i + 1] - row0 : 0;
+    const int n = span < 0 ? 0 : (span > n_nodes ? n_nodes : span);
+    const bool small = in && n <= 32, large = in && n > 32;
+    const uint64_t bs = __ballot(small), bl = __ballot(large);
+    const uint64_t below = (1ull << lane) - 1ull;
+    if (lane == 0) {
+      counts[wave][0] = __popcll(bs);
+      counts[wave][1] = __popcll(bl);
+    }
+    __syncthreads();
+    int off_s = 0, off_l = 0, tot_s = 0, tot_l = 0;
+#pragma unroll
+    for (int w = 0; w < 16; ++w) {
+      const int cs = counts[w][0], cl = counts[w][1];
+      off_s += w < wave ? cs : 0;
+      off_l += w < wave ? cl : 0;
+      tot_s += cs;
+      tot_l += cl;
+    }
+    const int4 rec = make_int4(i, row0, span, 0);
+    if (small) order[1 + done_small + off_s + __popcll(bs & below)] = rec;
+    if (large) order[batch - (done_large + off_l + __popcll(bl & below))] = rec;
+    done_small += tot_s;
+    done_large += tot_l;
+    __syncthreads();  // counts is rewritten by the next chunk
+  }
+  if (tid == 0) order[0] = make_int4(done_small, done_large, 0, 0);
+}
+
+int launch_size_order(const int32_t* cu_seqlens, int batch, int n_nodes, int32_t* order, hipStream_t stream) {
+  hipLaunchKernelGGL(size_order_kernel, dim3(1), dim3(1024), 0, stream, cu_seqlens, batch, n_nodes,
+                     reinterpret_cast<int4*>(order));
+  return hipGetLastError() == hipSuccess ? DFT_OK : DFT_ERR_LAUNCH;
 }
 
 int launch_tree_verify(const dft_verify_args* a, hipStream_t stream) {
   const VerifyParams P = make_params(a);
-  const dim3 grid((unsigned)(a->batch * a->hv)), block(64 * WavesFor<32>()), block64(64 * WavesFor<64>());
+  const dim3 block(64 * WavesFor<32>()), block64(64 * WavesFor<64>());
   VerifyParams narrow, wide;
   bool split;
   split_by_size(a, P, narrow, wide, split);
-  if (a->n_nodes > 32) {
+  dim3 g_narrow, g_wide;
+  split_grids(a, wide, split, g_narrow, g_wide);
+  if (a->n_nodes > 32 && g_wide.x > 0) {
     if (P.s0_vec)
-      hipLaunchKernelGGL((tree_verify_kernel<64, true>), grid, block64, 0, stream, wide);
+      hipLaunchKernelGGL((tree_verify_kernel<64, true>), g_wide, block64, 0, stream, wide);
     else
-      hipLaunchKernelGGL((tree_verify_kernel<64, false>), grid, block64, 0, stream, wide);
+      hipLaunchKernelGGL((tree_verify_kernel<64, false>), g_wide, block64, 0, stream, wide);
   }
-  if (a->n_nodes <= 32 || split) {
+  if ((a->n_nodes <= 32 || split) && g_narrow.x > 0) {
     if (P.s0_vec)
-      hipLaunchKernelGGL((tree_verify_kernel<32, true>), grid, block, 0, stream, narrow);
+      hipLaunchKernelGGL((tree_verify_kernel<32, true>), g_narrow, block, 0, stream, narrow);
     else
-      hipLaunchKernelGGL((tree_verify_kernel<32, false>), grid, block, 0, stream, narrow);
+      hipLaunchKernelGGL((tree_verify_kernel<32, false>), g_narrow, block, 0, stream, narrow);
   }
   return hipGetLastError() == hipSuccess ? DFT_OK : DFT_ERR_LAUNCH;
 }
@@ -1972,10 +2079,12 @@ int launch_tree_verify(const dft_verify_args* a, hipStream_t stream) {
 int launch_tree_commit_verify(const dft_verify_args* a, const dft_pending_commit* c, hipStream_t stream) {
   VerifyParams P = make_params(a);
   P.c = *c;
-  const dim3 grid((unsigned)(a->batch * a->hv)), block(64 * WavesFor<32>()), block64(64 * WavesFor<64>());
+  const dim3 block(64 * WavesFor<32>()), block64(64 * WavesFor<64>());
   VerifyParams narrow, wide;
   bool split;
   split_by_size(a, P, narrow, wide, split);
+  dim3 g_narrow, g_wide;
+  split_grids(a, wide, split, g_narrow, g_wide);
   // the previous step's raw key rows, recomputed values (validated by the caller)
   const int form = (c->keys == nullptr ? 1 : 0) + (c->values == nullptr ? 2 : 0);
 #define DFT_FUSED(np, g, b, prm)                                                                               \
@@ -1985,8 +2094,8 @@ int launch_tree_commit_verify(const dft_verify_args* a, const dft_pending_commit
     case 2: hipLaunchKernelGGL((tree_commit_verify_kernel<np, false, true>), g, b, 0, stream, prm); break;    \
     default: hipLaunchKernelGGL((tree_commit_verify_kernel<np, true, true>), g, b, 0, stream, prm); break;    \
   }
-  if (a->n_nodes > 32) DFT_FUSED(64, grid, block64, wide)
-  if (a->n_nodes <= 32 || split) DFT_FUSED(32, grid, block, narrow)
+  if (a->n_nodes > 32 && g_wide.x > 0) DFT_FUSED(64, g_wide, block64, wide)
+  if ((a->n_nodes <= 32 || split) && g_narrow.x > 0) DFT_FUSED(32, g_narrow, block, narrow)
 #undef DFT_FUSED
   return hipGetLastError() == hipSuccess ? DFT_OK : DFT_ERR_LAUNCH;
 }

@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define DFT_ABI_VERSION 3
+#define DFT_ABI_VERSION 4
 
 #if defined(__GNUC__)
 #define DFT_API __attribute__((visibility("default")))
@@ -69,7 +69,10 @@ enum dft_request_status {
   DFT_STATUS_SPAN = 1,
   /* a path entry (within its length) or a commit end names a node at or past
    * the size of its tree: that entry (or end) was ignored */
-  DFT_STATUS_PATH = 2
+  DFT_STATUS_PATH = 2,
+  /* DFT_VERIFY_ORDER_COUNT gave fewer requests of the request's size class
+   * than size_order holds: the request was not processed */
+  DFT_STATUS_ORDER = 4
 };
 
 /* ---------------------------------------------------------------------------
@@ -78,7 +81,8 @@ enum dft_request_status {
  * row0(b) = cu_seqlens[b] if cu_seqlens else b*n_nodes.
  * ------------------------------------------------------------------------- */
 enum dft_verify_flags {
-  DFT_VERIFY_AUX_K_PER_KHEAD = 1 /* aux_k holds one row set per k-head */
+  DFT_VERIFY_AUX_K_PER_KHEAD = 1, /* aux_k holds one row set per k-head */
+  DFT_VERIFY_ORDER_COUNT = 2      /* size_order_small holds size_order's count of requests of at most 32 nodes */
 };
 
 typedef struct dft_verify_args {
@@ -144,9 +148,36 @@ typedef struct dft_verify_args {
   /* optional [batch] dft_request_status bits (DFT_STATUS_SPAN; with
    * dft_tree_commit_verify also DFT_STATUS_PATH for the pending path) */
   int32_t* status;
+
+  /* DFT_ABI_VERSION 4 (appended).  Optional: the packed batch's requests
+   * ordered by size class, as dft_size_order writes them from the same
+   * cu_seqlens and n_nodes.  A packed launch split by tree size (n_nodes >
+   * 32) then gives each of its two kernels its own requests first, read from
+   * the records: the workgroups past a class's count exit at the end of the
+   * grid instead of among the work.  With DFT_VERIFY_ORDER_COUNT in flags,
+   * size_order_small is the records' count of requests of at most 32 nodes,
+   * known to the caller, and each kernel launches exactly its class's
+   * workgroups: none exits.  A count below the records' marks the requests it
+   * leaves out DFT_STATUS_ORDER (not processed); one above them leaves the
+   * other kernel's extra workgroups to exit.  Ignored by unsplit launches;
+   * size_order must not be written while the launch runs. */
+  const int32_t* size_order;
+  int32_t size_order_small;
 } dft_verify_args;
 
 DFT_API int dft_tree_verify(const dft_verify_args* args, void* stream);
+
+/* Requests of a packed batch by size class, for dft_verify_args.size_order:
+ * order[0..3] = {n_small, n_large, 0, 0}, then batch records of 4 int32
+ * {request, cu_seqlens[request], span, 0}: the requests of at most 32 nodes
+ * (the span clamped to [0, n_nodes]) from record 0 up in request order, the
+ * others from record batch - 1 down in request order.  order holds
+ * 4 * (batch + 1) int32; one workgroup, no allocation.  No counterpart in the
+ * reference (its launches are per tree size, tree_kernels.py:193-208): for
+ * callers of packed ragged batches, once per step and shared by all layers.
+ * DFT_ERR_INVALID for batch < 0, n_nodes outside 1..64 or a null pointer. */
+DFT_API int dft_size_order(const int32_t* cu_seqlens, int32_t batch, int32_t n_nodes, int32_t* order,
+                           void* stream);
 
 /* ---------------------------------------------------------------------------
  * Tree-parent causal conv1d: y[n,c] = act(sum_j w[c,j] xt[cidx[n,j]][c] + bias[c])

@@ -29,7 +29,7 @@ def test_library_exports_every_declared_symbol():
     out = subprocess.run(["nm", "-D", "--defined-only", str(_lib.LIB_PATH)], capture_output=True, text=True).stdout
     exported = {l.split()[-1] for l in out.splitlines() if " T " in l}
     assert exported == set(names), "only the C ABI is exported"
-    assert lib.dft_abi_version() == _lib.ABI_VERSION == 3
+    assert lib.dft_abi_version() == _lib.ABI_VERSION == 4
 
 
 @pytest.fixture(scope="module")
@@ -59,8 +59,9 @@ def c_layouts(tmp_path_factory):
 def test_ctypes_structs_match_c_layout(c_layouts):
     from dforktree_amd import _lib
     layout, structs = c_layouts
-    # the status words were appended: every earlier field kept its offset
-    assert _lib.VerifyArgs._fields_[-1][0] == "status" and _lib.CommitArgs._fields_[-1][0] == "status"
+    # the status words, then the size-order records, were appended: every earlier field kept its offset
+    assert [f for f, _ in _lib.VerifyArgs._fields_[-3:]] == ["status", "size_order", "size_order_small"]
+    assert _lib.CommitArgs._fields_[-1][0] == "status"
     for cname, py in structs.items():
         assert ctypes.sizeof(py) == layout[f"{cname}.__size__"], cname
         for f, _ in py._fields_:
@@ -84,11 +85,24 @@ def test_validation_rejects_bad_descriptors_without_launching():
     v.batch = 0
     assert lib.dft_tree_verify(ctypes.byref(v), None) == _lib.DFT_OK                # empty batch: no-op
     v.batch, v.n_nodes = 1, 32
+    assert lib.dft_size_order(None, 1, 64, 16, None) == _lib.DFT_ERR_INVALID        # no cu_seqlens
+    assert lib.dft_size_order(16, 1, 65, 16, None) == _lib.DFT_ERR_INVALID          # > 64 nodes
+    assert lib.dft_size_order(16, -1, 64, 16, None) == _lib.DFT_ERR_INVALID         # batch
+    assert lib.dft_size_order(16, 1, 64, 8, None) == _lib.DFT_ERR_INVALID           # records: 16 B
     pc = _lib.PendingArgs()
     pc.path_cols, pc.k_head_div, pc.prev_n_nodes, pc.path_dtype = 16, 1, 32, _lib.DFT_I32
     assert lib.dft_tree_commit_verify(ctypes.byref(v), None, None) == _lib.DFT_ERR_INVALID  # null pointers
     v.y = v.a = v.b = v.A_log = v.dt_bias = v.state = v.o = v.anc_bits = 16
     v.y_row_stride, v.state_k_stride, v.state_v_stride = 8, 1, 128
+    v.size_order = 16
+    assert lib.dft_tree_verify(ctypes.byref(v), None) == _lib.DFT_ERR_INVALID       # size order, not packed
+    v.cu_seqlens, v.size_order = 16, 8
+    assert lib.dft_tree_verify(ctypes.byref(v), None) == _lib.DFT_ERR_INVALID       # records: 16 B
+    v.size_order, v.flags = None, _lib.DFT_VERIFY_ORDER_COUNT
+    assert lib.dft_tree_verify(ctypes.byref(v), None) == _lib.DFT_ERR_INVALID       # a count without records
+    v.size_order, v.size_order_small = 16, 2
+    assert lib.dft_tree_verify(ctypes.byref(v), None) == _lib.DFT_ERR_INVALID       # count > batch
+    v.cu_seqlens, v.size_order, v.size_order_small, v.flags = None, None, 0, 0
     assert lib.dft_tree_commit_verify(ctypes.byref(v), None, None) == _lib.DFT_ERR_INVALID  # no pending
     assert lib.dft_tree_commit_verify(ctypes.byref(v), ctypes.byref(pc), None) == _lib.DFT_ERR_INVALID
     pc.path = pc.keys = pc.values = pc.gains = 16

@@ -63,12 +63,13 @@ def _committed_states(batch1, walks):
 
 
 def _run_chain(cuda, batch1, batch2, per_khead, packed, empty=(), shorten=(), path_dtype=torch.int32,
-               raw_keys=False, raw_values=False):
+               raw_keys=False, raw_values=False, ordered=False):
     """Step 1 verifies batch1 (saving k, vn, G); step 2 verifies batch2
     through the fused entry, committing step 1's walks first.  raw_keys: step
     1 saves no keys, and the commit reads step 1's raw bf16 k rows from its y.
     raw_values: step 1 saves no values, and the commit recomputes them from
-    step 1's raw bf16 v rows (from its y) and b gates."""
+    step 1's raw bf16 v rows (from its y) and b gates.  ordered: step 2's
+    fused launch reads size-order records of its packed batch."""
     from dforktree_amd import ops
     hk, hv, B = batch1.hk, batch1.hv, batch1.batch
     pool = batch1.state.clone().to(cuda)  # [B, hv, V, K]
@@ -86,6 +87,8 @@ def _run_chain(cuda, batch1, batch2, per_khead, packed, empty=(), shorten=(), pa
     kw2 = dict(batch=B, n_nodes=batch2.n_max)
     if packed:
         kw1["cu_seqlens"], kw2["cu_seqlens"] = g1.cu_seqlens, g2.cu_seqlens
+        if ordered:
+            kw2["size_order"] = ops.size_order(g2.cu_seqlens, batch2.n_max)
     ts1 = ops.tree_struct(g1.parent, 4, cu_seqlens=g1.cu_seqlens, n_nodes=batch1.n_max, batch=B, want=("anc_bits",))
     ts2 = ops.tree_struct(g2.parent, 4, cu_seqlens=g2.cu_seqlens, n_nodes=batch2.n_max, batch=B, want=("anc_bits",))
     ops.tree_verify(g1.y, g1.a, g1.b, g1.A_log, g1.dt_bias, st, hk=hk, hv=hv, anc_bits=ts1["anc_bits"],
@@ -162,6 +165,25 @@ def test_commit_verify_packed_ragged_per_khead(cuda, path_dtype):
     _check_chain(batch1, batch2, pool, o2, aux2, walks, empty, per_khead=True)
 
 
+def test_commit_verify_size_order(cuda):
+    """Packed trees on both sides of 32 nodes in both steps, recomputed
+    values and raw keys: the fused launch reading size-order records commits
+    and verifies bit for bit as the launch without them."""
+    from dforktree_amd import synth
+    announce("commit->verify with size-order records")
+    sizes1, kinds = [40, 9, 64, 17, 33, 1, 50, 20], ["random", "chain", "bushy", "random"] * 2
+    sizes2 = [12, 64, 30, 1, 50, 20, 33, 64]
+    batch1 = synth.make_batch(52, 0, sizes1, hk=2, hv=4, kinds=kinds)
+    batch2 = synth.make_batch(53, 0, sizes2, hk=2, hv=4, kinds=kinds)
+    runs = [_run_chain(cuda, batch1, batch2, per_khead=True, packed=True, empty=(3,), shorten=(6,), raw_keys=True,
+                       raw_values=True, ordered=ordered) for ordered in (False, True)]
+    (pa, oa, auxa, walks), (pb, ob, auxb, _) = runs
+    assert torch.equal(pa, pb) and torch.equal(oa.view(torch.int16), ob.view(torch.int16))
+    for x, z in zip(auxa, auxb):
+        assert torch.equal(x, z)
+    _check_chain(batch1, batch2, pb, ob, auxb, walks, (3,), per_khead=True)
+
+
 def test_commit_verify_bench_shape(cuda):
     """The measured shape: 64 requests of 32-node random trees at full width
     (2048 items, two generations of resident workgroups, so freed slots take
@@ -229,18 +251,22 @@ def test_commit_verify_raw_key_rows_bench_shape(cuda):
     _check_chain(batch1, batch2, pool, o2, aux2, walks, empty, per_khead=True)
 
 
-@pytest.mark.parametrize("sizes1,sizes2,packed", [([32] * 6, [32] * 6, False),
-                                                   ([40, 9, 64, 17, 33, 1], [12, 64, 30, 1, 50, 20], True)])
-def test_commit_verify_recomputed_values(cuda, sizes1, sizes2, packed):
+@pytest.mark.parametrize("sizes1,sizes2,packed,b_dtype", [
+    ([32] * 6, [32] * 6, False, torch.float32),
+    ([32] * 6, [32] * 6, False, torch.bfloat16),
+    ([40, 9, 64, 17, 33, 1], [12, 64, 30, 1, 50, 20], True, torch.float16)])
+def test_commit_verify_recomputed_values(cuda, sizes1, sizes2, packed, b_dtype):
     """The commit recomputes the path's values from the previous step's raw
-    bf16 v rows, b gates and the slot's state (both widths; with raw key rows
-    too); the step-1 verify saves no values.  Against the oracle chain, and
-    against the same chain through saved values."""
+    bf16 v rows, b gates (fp32, bf16 or fp16, as the verify reads them) and
+    the slot's state (both widths; with raw key rows too); the step-1 verify
+    saves no values.  Against the oracle chain, and against the same chain
+    through saved values."""
     from dforktree_amd import synth
-    announce(f"commit->verify recomputed values packed={packed}")
+    announce(f"commit->verify recomputed values packed={packed} b {b_dtype}")
     kinds = ["random", "chain", "bushy", "random", "chain", "bushy"]
     batch1 = synth.make_batch(46, 0, sizes1, hk=2, hv=4, kinds=kinds)
     batch2 = synth.make_batch(47, 0, sizes2, hk=2, hv=4, kinds=kinds[::-1])
+    batch1.b, batch2.b = batch1.b.to(b_dtype), batch2.b.to(b_dtype)  # the oracle reads the same rounded gates
     empty, shorten = (2,), (5,)
     for raw_keys in (False, True):
         pool, o2, aux2, walks = _run_chain(cuda, batch1, batch2, per_khead=True, packed=packed, empty=empty,

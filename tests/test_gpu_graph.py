@@ -43,6 +43,7 @@ class Step:
         b1 = synth.make_batch(seed, 0, sizes, hk=2, hv=4, kinds=kinds[:len(sizes)])
         b2 = synth.make_batch(seed + 1, 0, sizes, hk=2, hv=4, kinds=kinds[::-1][:len(sizes)])
         self.packed, self.B, self.N, self.hk, self.hv = packed, b1.batch, b1.n_max, 2, 4
+        self.sizes = list(sizes)
         self.g1, self.g2 = b1.to(cuda), b2.to(cuda)
         rows = self.g1.y.shape[0]
         gen = torch.Generator().manual_seed(seed + 2)
@@ -81,6 +82,8 @@ class Step:
             mask=torch.empty(mask_bytes, device=cuda, dtype=torch.uint8),
             mind=torch.empty(self.B + 1, device=cuda, dtype=torch.int32),
             pb=torch.empty((self.bits.numel() + 7) // 8, device=cuda, dtype=torch.uint8),
+            so1=torch.empty(self.B + 1, 4, device=cuda, dtype=torch.int32),
+            so2=torch.empty(self.B + 1, 4, device=cuda, dtype=torch.int32),
         )
 
     def reset(self):
@@ -92,10 +95,12 @@ class Step:
         for t in self.out.values():
             t.fill_(SENTINEL[t.dtype])
 
-    def shape_kw(self, g):
+    def shape_kw(self, g, order=None):
         kw = dict(batch=self.B, n_nodes=self.N)
         if self.packed:
             kw["cu_seqlens"] = g.cu_seqlens
+            if order is not None:  # the packed step's size-order records (written by run) and class count
+                kw.update(size_order=order, size_order_small=sum(1 for n in self.sizes if n <= 32))
         return kw
 
     def run(self):
@@ -110,14 +115,18 @@ class Step:
         if not self.packed:
             cidx = ts1["cidx"].view(self.B, self.N, 4)
             ops.tree_conv(self.cx, self.cs, self.cw, None, cidx, y=o["y"], iw=o["iw"])
+        else:
+            ops.size_order(g1.cu_seqlens, self.N, out=o["so1"])
+            ops.size_order(g2.cu_seqlens, self.N, out=o["so2"])
         st = self.pool.transpose(-1, -2)
         ops.tree_verify(g1.y, g1.a, g1.b, g1.A_log, g1.dt_bias, st, hk=2, hv=4, anc_bits=ts1["anc_bits"],
-                        o=o["o1"], aux_k=o["k1"], aux_v=o["v1"], aux_g=o["G1"], **self.shape_kw(g1))
+                        o=o["o1"], aux_k=o["k1"], aux_v=o["v1"], aux_g=o["G1"], **self.shape_kw(g1, o["so1"]))
         prev = dict(prev_cu_seqlens=g1.cu_seqlens) if self.packed else dict(prev_n_nodes=self.N)
         ops.tree_commit_verify(g2.y, g2.a, g2.b, g2.A_log, g2.dt_bias, st, hk=2, hv=4, anc_bits=ts2["anc_bits"],
                                pending_path=self.idx, pending_keys=o["k1"], pending_values=o["v1"],
                                pending_gains=o["G1"], pending_path_len=self.lens, o=o["o2"], aux_k=o["k2"],
-                               aux_v=o["v2"], aux_g=o["G2"], aux_k_per_khead=True, **prev, **self.shape_kw(g2))
+                               aux_v=o["v2"], aux_g=o["G2"], aux_k_per_khead=True, **prev,
+                               **self.shape_kw(g2, o["so2"]))
         # the fused entry again, its keys normalised from step 1's raw k rows
         ops.tree_commit_verify(g2.y, g2.a, g2.b, g2.A_log, g2.dt_bias, self.rpool.transpose(-1, -2), hk=2, hv=4,
                                anc_bits=ts2["anc_bits"], pending_path=self.idx, pending_keys=None,
@@ -131,7 +140,7 @@ class Step:
                                pending_key_rows=g1.y[:, 256:512].unflatten(1, (2, 128)), pending_values=None,
                                pending_value_rows=g1.y[:, 512:].unflatten(1, (4, 128)), pending_b=g1.b,
                                pending_gains=o["G1"], pending_path_len=self.lens, pending_k_head_div=2, o=o["o4"],
-                               aux_g=o["G4"], **prev, **self.shape_kw(g2))
+                               aux_g=o["G4"], **prev, **self.shape_kw(g2, o["so2"]))
         ops.tree_commit(self.cpool, o["k2"][None], o["v2"][None], o["G2"][None], self.idx2, n_nodes=self.N,
                         k_head_div=2, **(dict(cu_seqlens=g2.cu_seqlens) if self.packed else {}))
         ops.block_inverse_(self.inv)

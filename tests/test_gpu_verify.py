@@ -142,6 +142,90 @@ def test_verify_split_order_empty_requests_and_slots(cuda):
     check_against_oracle(batch, o, aux_k, aux_v, aux_g)
 
 
+def size_order_records(cu, n_nodes):
+    """The records dft_size_order writes, restated on the host: the counts,
+    then (request, first row, span, 0) for the requests of at most 32 nodes
+    (span clamped to [0, n_nodes]) from the front and the others from the
+    back, each class in request order."""
+    B = len(cu) - 1
+    n = [min(max(cu[r + 1] - cu[r], 0), n_nodes) for r in range(B)]
+    small = [r for r in range(B) if n[r] <= 32]
+    large = [r for r in range(B) if n[r] > 32]
+    recs = [None] * B
+    for j, r in enumerate(small):
+        recs[j] = [r, cu[r], cu[r + 1] - cu[r], 0]
+    for j, r in enumerate(large):
+        recs[B - 1 - j] = [r, cu[r], cu[r + 1] - cu[r], 0]
+    return [[len(small), len(large), 0, 0]] + recs
+
+
+def test_verify_size_order(cuda):
+    """1100 packed requests of 0-64 nodes (two chunks of the ordering
+    workgroup) launched at n_nodes 60, so that those past 60 are cut
+    (DFT_STATUS_SPAN): the records equal the host restatement, and the split
+    launch that reads them writes o, the saves and the status words bit for
+    bit as the launch without them, also with the class count given on the
+    host (each kernel launching exactly its class's blocks).  A count 3 too
+    small or too large leaves 3 requests of one class unprocessed: exactly
+    those get DFT_STATUS_ORDER and keep their outputs unwritten, and every
+    other request is written as before."""
+    from dforktree_amd import ops, synth
+    announce("verify with size-order records, 1100 requests")
+    g = torch.Generator().manual_seed(17)
+    B, hk, hv = 1100, 1, 1
+    sizes = torch.randint(0, 65, (B,), generator=g).tolist()
+    rows = sum(sizes)
+    cu = [0]
+    for n in sizes:
+        cu.append(cu[-1] + n)
+    y = torch.randn(rows, 2 * hk * 128 + hv * 128, generator=g).to(torch.bfloat16).to(cuda)
+    a, b = torch.randn(rows, hv, generator=g).to(cuda), torch.randn(rows, hv, generator=g).to(cuda)
+    parents = torch.cat([synth.tree_parents(n, "random", g) for n in sizes if n]).to(cuda)
+    cu_d = torch.tensor(cu, dtype=torch.int32, device=cuda)
+    state = (torch.randn(B, hv, 128, 128, generator=g) * 0.02).to(cuda)
+    A_log, dt_bias = torch.full((hv,), -0.69, device=cuda), torch.zeros(hv, device=cuda)
+    bits = ops.tree_struct(parents, 4, cu_seqlens=cu_d, n_nodes=64, batch=B, want=("anc_bits",))["anc_bits"]
+    order = ops.size_order(cu_d, 60)
+    torch.cuda.synchronize()
+    assert order.cpu().tolist() == size_order_records(cu, 60)
+    recs = size_order_records(cu, 60)
+    n_small = recs[0][0]
+
+    def run(so=None, small=None):
+        aux = [torch.full((hv, rows, 128), -3.0, device=cuda), torch.full((hv, rows, 128), -3.0, device=cuda),
+               torch.full((hv, rows), -3.0, device=cuda)]
+        status = torch.full((B,), -7, device=cuda, dtype=torch.int32)
+        o = torch.full((rows, hv, 128), -3.0, device=cuda, dtype=torch.bfloat16)
+        ops.tree_verify(y, a, b, A_log, dt_bias, state.transpose(-1, -2), hk=hk, hv=hv, anc_bits=bits,
+                        cu_seqlens=cu_d, n_nodes=60, batch=B, o=o, aux_k=aux[0], aux_v=aux[1], aux_g=aux[2],
+                        status=status, size_order=so, size_order_small=small)
+        torch.cuda.synchronize()
+        return [o.view(torch.int16), *(t.view(torch.int32) for t in aux), status]
+
+    def rows_of(reqs):
+        m = torch.zeros(rows, dtype=torch.bool, device=cuda)
+        for r in reqs:
+            m[cu[r]:cu[r + 1]] = True
+        return m
+
+    want = run()
+    assert want[-1].cpu().tolist() == [1 if n > 60 else 0 for n in sizes]  # DFT_STATUS_SPAN: the cut ones
+    for small in (None, n_small):
+        for x, z in zip(want, run(order, small)):
+            assert torch.equal(x, z)
+    # a count 3 short misses class 0's last 3 records; 3 over misses class 1's last 3
+    for small, missed in ((n_small - 3, [recs[1 + q][0] for q in range(n_small - 3, n_small)]),
+                          (n_small + 3, [recs[B - q][0] for q in range(B - n_small - 3, B - n_small)])):
+        got = run(order, small)
+        st = got[-1].cpu().tolist()
+        assert sorted(r for r in range(B) if st[r] == 4) == sorted(missed)
+        keep = ~rows_of(missed)
+        assert torch.equal(want[0][keep], got[0][keep])  # o [rows, hv, dv]
+        for x, z in zip(want[1:4], got[1:4]):            # saves [hv, rows, ...]
+            assert torch.equal(x[:, keep], z[:, keep])
+        assert (got[0][~keep] == torch.tensor(-3.0, dtype=torch.bfloat16).view(torch.int16)).all()
+
+
 def test_verify_split_beyond_ordered_batch(cuda):
     """300 requests (more than the split launch orders): the kernels take
     their requests by block id, skipping the other kernel's."""
