@@ -252,10 +252,9 @@ class RaggedWorkload:
         self.cu = torch.tensor([0] + torch.tensor(self.sizes).cumsum(0).tolist(), dtype=torch.int32, device=dev)
         self.anc_bits = ops.tree_struct(parents, 4, cu_seqlens=self.cu, n_nodes=64, batch=self.RB,
                                         want=("anc_bits",))["anc_bits"]
-        # the requests by size class, once per step like the tree structure, and the count of trees of at most
-        # 32 nodes, which the host knows: each kernel of the split launch runs exactly its own requests
+        # the requests by size class, once per step like the tree structure: each kernel of the split launch
+        # takes its own requests first
         self.order = ops.size_order(self.cu, 64)
-        self.n_small = sum(1 for n in self.sizes if n <= 32)
         self.o = torch.empty(L, rows, HV, D, device=dev, dtype=torch.bfloat16)
         self.keys = torch.empty(L, HK, rows, D, device=dev)
         self.vals = torch.empty(L, HV, rows, D, device=dev)
@@ -266,8 +265,7 @@ class RaggedWorkload:
         ops.tree_verify(self.y[l], self.a[l], self.b[l], self.A_log, self.dt_bias, self.state[l].transpose(-1, -2),
                         hk=HK, hv=HV, anc_bits=self.anc_bits, batch=self.RB, n_nodes=64, cu_seqlens=self.cu,
                         neg_exp_A=self.neg, o=self.o[l], aux_k=self.keys[l], aux_v=self.vals[l],
-                        aux_g=self.gains[l], aux_k_per_khead=True, size_order=self.order if ordered else None,
-                        size_order_small=self.n_small if ordered else None)
+                        aux_g=self.gains[l], aux_k_per_khead=True, size_order=self.order if ordered else None)
 
     def bytes_per_launch(self, lo=0, hi=64):
         """Algorithmic bytes of the requests with lo <= nodes <= hi: per

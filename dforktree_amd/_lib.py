@@ -13,9 +13,9 @@ LIB_PATH = Path(__file__).resolve().parent / "libdforktree_amd.so"
 
 DFT_OK, DFT_ERR_INVALID, DFT_ERR_UNSUPPORTED, DFT_ERR_LAUNCH = 0, 1, 2, 3
 DFT_F32, DFT_BF16, DFT_F16, DFT_I32, DFT_I64 = 0, 1, 2, 3, 4
-DFT_VERIFY_AUX_K_PER_KHEAD, DFT_VERIFY_ORDER_COUNT = 1, 2
+DFT_VERIFY_AUX_K_PER_KHEAD = 1
 DFT_COMMIT_KV, DFT_COMMIT_CHECK_ANC, DFT_COMMIT_LEN_IS_LAST = 1, 2, 4
-DFT_STATUS_SPAN, DFT_STATUS_PATH, DFT_STATUS_ORDER = 1, 2, 4
+DFT_STATUS_SPAN, DFT_STATUS_PATH = 1, 2
 ABI_VERSION = 4
 
 i32, i64, f32, vp = C.c_int32, C.c_int64, C.c_float, C.c_void_p
@@ -41,7 +41,7 @@ class VerifyArgs(C.Structure):
         ("aux_v", vp), ("aux_v_h_stride", i64), ("aux_v_row_stride", i64),
         ("aux_g", vp), ("aux_g_h_stride", i64), ("aux_g_row_stride", i64),
         ("status", vp),
-        ("size_order", vp), ("size_order_small", i32),
+        ("size_order", vp),
     ]
 
 

@@ -48,9 +48,6 @@ int verify_status(const dft_verify_args* a) {
   if (!aligned16(a->y) || a->y_row_stride % 8 != 0) return DFT_ERR_INVALID;
   // size-order records: 16-byte records of a packed batch
   if (a->size_order && (!a->cu_seqlens || !aligned16(a->size_order))) return DFT_ERR_INVALID;
-  if ((a->flags & DFT_VERIFY_ORDER_COUNT) &&
-      (!a->size_order || a->size_order_small < 0 || a->size_order_small > a->batch))
-    return DFT_ERR_INVALID;
   // one workgroup per (request, v-head): 4 waves for trees of up to 32 nodes, 8 beyond
   if ((int64_t)a->batch * a->hv > max_blocks(a->n_nodes > 32 ? 512 : 256)) return DFT_ERR_UNSUPPORTED;
   return DFT_OK;

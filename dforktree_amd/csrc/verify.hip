@@ -146,8 +146,6 @@ struct VerifyParams {
                    // requests with n_lo <= nodes <= n_hi (the others exit at once)
   int cls;         // with a.size_order: this kernel's size class (0: at most 32
                    // nodes, 1: more), its requests read from the order records; -1: none
-  int order_small; // the caller's count of class-0 requests (the grids are sized
-                   // from it), -1 when unknown (both grids cover every request)
 };
 
 // The output fields a workgroup needs only at the end of its life (the key
@@ -991,12 +989,11 @@ struct Item {
   const float* S0;   // the head's state tile (k stride 1 on the vector paths)
 };
 
-// block id -> (request, v-head) over nb requests (the batch, or a size
-// class's count); the R v-heads sharing a k-head get ids 8 apart so that
-// they land on the same XCD (shared q/k rows in its L2)
-__device__ __forceinline__ void item_heads(const dft_verify_args& p, int id, int nb, Item& it) {
+// block id -> (request, v-head); the R v-heads sharing a k-head get ids 8
+// apart so that they land on the same XCD (shared q/k rows in its L2)
+__device__ __forceinline__ void item_heads(const dft_verify_args& p, int id, Item& it) {
   const int R = p.hv / p.hk;
-  const int pairs = nb * p.hk;
+  const int pairs = p.batch * p.hk;
   const int full = (pairs / 8) * 8 * R;
   int pair, rr;
   if (id < full) {
@@ -1012,21 +1009,6 @@ __device__ __forceinline__ void item_heads(const dft_verify_args& p, int id, int
   it.hk = pair - it.b * p.hk;
   it.rr = rr;
   it.h = it.hk * R + rr;
-}
-
-// With the caller's class count hs, each kernel's grid covers hs (class 0)
-// or batch - hs (class 1) requests.  If hs disagrees with the records, the
-// class whose grid is short leaves requests out; the other kernel's first
-// thread marks them DFT_STATUS_ORDER (its grid is the longer one, so it
-// exists).  No other block writes those status words.
-__device__ __forceinline__ void order_misses(const dft_verify_args& p, int cls, int hs) {
-  if (!p.status) return;
-  const int4* ord = reinterpret_cast<const int4*>(p.size_order);
-  const int4 hd = ord[0];
-  if (cls == 0)  // class 1 launched batch - hs blocks' worth of requests: records hd.y past them are missed
-    for (int q = p.batch - hs; q < hd.y; ++q) p.status[ord[p.batch - q].x] = DFT_STATUS_ORDER;
-  else  // class 0 launched hs requests' worth
-    for (int q = hs; q < hd.x; ++q) p.status[ord[1 + q].x] = DFT_STATUS_ORDER;
 }
 
 // rows, node count and state tile of a request (loads the index arrays).
@@ -1746,9 +1728,7 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
   const int n16 = lane & 15, g4 = lane >> 4;
 
   Item it;
-  if (P.cls >= 0 && P.order_small >= 0 && blockIdx.x == 0 && tid == 0) order_misses(p, P.cls, P.order_small);
-  item_heads(p, blockIdx.x, P.cls < 0 || P.order_small < 0 ? p.batch : P.cls == 0 ? P.order_small
-                                                                                 : p.batch - P.order_small, it);
+  item_heads(p, blockIdx.x, it);
   if (!item_rows<NP>(p, it, P.n_lo, P.n_hi, P.cls)) return;
   // Thread 0 of the request's head-0 workgroup writes its status word (the
   // condition is evaluated where it is written: held from here, it would
@@ -1965,7 +1945,6 @@ static VerifyParams make_params(const dft_verify_args* a) {
   P.n_lo = INT_MIN;
   P.n_hi = INT_MAX;
   P.cls = -1;
-  P.order_small = -1;
   return P;
 }
 
@@ -1987,21 +1966,8 @@ static void split_by_size(const dft_verify_args* a, const VerifyParams& P, Verif
     if (a->size_order) {
       narrow.cls = 0;
       wide.cls = 1;
-      if (a->flags & DFT_VERIFY_ORDER_COUNT) narrow.order_small = wide.order_small = a->size_order_small;
     }
   }
-}
-
-// the grids of a launch: one block per (request, v-head) of the kernel's
-// requests (a size class's count when the caller gave it)
-static void split_grids(const dft_verify_args* a, const VerifyParams& wide, bool split, dim3& g_narrow, dim3& g_wide) {
-  unsigned nn = (unsigned)a->batch, nw = (unsigned)a->batch;
-  if (split && wide.order_small >= 0) {
-    nn = (unsigned)wide.order_small;
-    nw = (unsigned)(a->batch - wide.order_small);
-  }
-  g_narrow = dim3(nn * (unsigned)a->hv);
-  g_wide = dim3(nw * (unsigned)a->hv);
 }
 
 // Requests by size class (dft_size_order): one workgroup, chunks of 1024
@@ -2054,23 +2020,21 @@ int launch_size_order(const int32_t* cu_seqlens, int batch, int n_nodes, int32_t
 
 int launch_tree_verify(const dft_verify_args* a, hipStream_t stream) {
   const VerifyParams P = make_params(a);
-  const dim3 block(64 * WavesFor<32>()), block64(64 * WavesFor<64>());
+  const dim3 grid((unsigned)(a->batch * a->hv)), block(64 * WavesFor<32>()), block64(64 * WavesFor<64>());
   VerifyParams narrow, wide;
   bool split;
   split_by_size(a, P, narrow, wide, split);
-  dim3 g_narrow, g_wide;
-  split_grids(a, wide, split, g_narrow, g_wide);
-  if (a->n_nodes > 32 && g_wide.x > 0) {
+  if (a->n_nodes > 32) {
     if (P.s0_vec)
-      hipLaunchKernelGGL((tree_verify_kernel<64, true>), g_wide, block64, 0, stream, wide);
+      hipLaunchKernelGGL((tree_verify_kernel<64, true>), grid, block64, 0, stream, wide);
     else
-      hipLaunchKernelGGL((tree_verify_kernel<64, false>), g_wide, block64, 0, stream, wide);
+      hipLaunchKernelGGL((tree_verify_kernel<64, false>), grid, block64, 0, stream, wide);
   }
-  if ((a->n_nodes <= 32 || split) && g_narrow.x > 0) {
+  if (a->n_nodes <= 32 || split) {
     if (P.s0_vec)
-      hipLaunchKernelGGL((tree_verify_kernel<32, true>), g_narrow, block, 0, stream, narrow);
+      hipLaunchKernelGGL((tree_verify_kernel<32, true>), grid, block, 0, stream, narrow);
     else
-      hipLaunchKernelGGL((tree_verify_kernel<32, false>), g_narrow, block, 0, stream, narrow);
+      hipLaunchKernelGGL((tree_verify_kernel<32, false>), grid, block, 0, stream, narrow);
   }
   return hipGetLastError() == hipSuccess ? DFT_OK : DFT_ERR_LAUNCH;
 }
@@ -2079,12 +2043,10 @@ int launch_tree_verify(const dft_verify_args* a, hipStream_t stream) {
 int launch_tree_commit_verify(const dft_verify_args* a, const dft_pending_commit* c, hipStream_t stream) {
   VerifyParams P = make_params(a);
   P.c = *c;
-  const dim3 block(64 * WavesFor<32>()), block64(64 * WavesFor<64>());
+  const dim3 grid((unsigned)(a->batch * a->hv)), block(64 * WavesFor<32>()), block64(64 * WavesFor<64>());
   VerifyParams narrow, wide;
   bool split;
   split_by_size(a, P, narrow, wide, split);
-  dim3 g_narrow, g_wide;
-  split_grids(a, wide, split, g_narrow, g_wide);
   // the previous step's raw key rows, recomputed values (validated by the caller)
   const int form = (c->keys == nullptr ? 1 : 0) + (c->values == nullptr ? 2 : 0);
 #define DFT_FUSED(np, g, b, prm)                                                                               \
@@ -2094,8 +2056,8 @@ int launch_tree_commit_verify(const dft_verify_args* a, const dft_pending_commit
     case 2: hipLaunchKernelGGL((tree_commit_verify_kernel<np, false, true>), g, b, 0, stream, prm); break;    \
     default: hipLaunchKernelGGL((tree_commit_verify_kernel<np, true, true>), g, b, 0, stream, prm); break;    \
   }
-  if (a->n_nodes > 32 && g_wide.x > 0) DFT_FUSED(64, g_wide, block64, wide)
-  if ((a->n_nodes <= 32 || split) && g_narrow.x > 0) DFT_FUSED(32, g_narrow, block, narrow)
+  if (a->n_nodes > 32) DFT_FUSED(64, grid, block64, wide)
+  if (a->n_nodes <= 32 || split) DFT_FUSED(32, grid, block, narrow)
 #undef DFT_FUSED
   return hipGetLastError() == hipSuccess ? DFT_OK : DFT_ERR_LAUNCH;
 }

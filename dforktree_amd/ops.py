@@ -87,7 +87,7 @@ def tree_verify(y: torch.Tensor, a: torch.Tensor, b: torch.Tensor, A_log: Option
                 o_dtype: Optional[torch.dtype] = None, aux_k: Optional[torch.Tensor] = None,
                 aux_v: Optional[torch.Tensor] = None, aux_g: Optional[torch.Tensor] = None,
                 aux_k_per_khead: bool = False, status: Optional[torch.Tensor] = None,
-                size_order: Optional[torch.Tensor] = None, size_order_small: Optional[int] = None) -> torch.Tensor:
+                size_order: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Fused tree verify of every (request, v-head).
 
     y [rows, 2*hk*128 + hv*128] bf16 with channel stride 1; a, b [rows, hv];
@@ -102,16 +102,12 @@ def tree_verify(y: torch.Tensor, a: torch.Tensor, b: torch.Tensor, A_log: Option
     ``size_order``: the records ``size_order(cu_seqlens, n_nodes)`` wrote for
     this packed batch (once per step, shared by every layer); a launch split
     by tree size then runs each class's requests first in its kernel.
-    ``size_order_small``: the number of requests of at most 32 nodes (span
-    clamped to n_nodes), when the caller knows it on the host: each kernel
-    then launches exactly its class's blocks.  Requests a too small count
-    leaves out are not processed and get DFT_STATUS_ORDER.
     """
     args, o, dev, _keep = _verify_args(
         y, a, b, A_log, dt_bias, state, hk=hk, hv=hv, anc=anc, anc_bits=anc_bits, batch=batch, n_nodes=n_nodes,
         cu_seqlens=cu_seqlens, scale=scale, neg_exp_A=neg_exp_A, state_indices=state_indices,
         state_slot_stride=state_slot_stride, o=o, o_dtype=o_dtype, aux_k=aux_k, aux_v=aux_v, aux_g=aux_g,
-        aux_k_per_khead=aux_k_per_khead, status=status, size_order=size_order, size_order_small=size_order_small)
+        aux_k_per_khead=aux_k_per_khead, status=status, size_order=size_order)
     check("dft_tree_verify", load().dft_tree_verify(C.byref(args), _stream(dev)))
     return o
 
@@ -156,7 +152,7 @@ def _status_ptr(status, batch, dev):
 
 def _verify_args(y, a, b, A_log, dt_bias, state, *, hk, hv, anc, anc_bits, batch, n_nodes, cu_seqlens, scale,
                  neg_exp_A, state_indices, state_slot_stride, o, o_dtype, aux_k, aux_v, aux_g, aux_k_per_khead,
-                 status=None, size_order=None, size_order_small=None):
+                 status=None, size_order=None):
     """Validate the verify operands and fill the C descriptor; returns
     (args, o, device, tensors that must outlive the launch call)."""
     dev = _device_of(y, a, b, A_log, dt_bias, state, anc, anc_bits, cu_seqlens, neg_exp_A,
@@ -269,13 +265,6 @@ def _verify_args(y, a, b, A_log, dt_bias, state, *, hk, hv, anc, anc_bits, batch
             raise ValueError("size_order goes with a packed batch (cu_seqlens)")
         _check_size_order(size_order, batch, dev)
         args.size_order = size_order.data_ptr()
-    if size_order_small is not None:
-        if size_order is None:
-            raise ValueError("size_order_small goes with size_order")
-        if not 0 <= size_order_small <= batch:
-            raise ValueError(f"size_order_small must lie in [0, {batch}]")
-        args.flags |= _lib.DFT_VERIFY_ORDER_COUNT
-        args.size_order_small = size_order_small
     return args, o, dev, (y, cu_seqlens, anc, anc_bits, si)
 
 
@@ -296,8 +285,7 @@ def tree_commit_verify(y: torch.Tensor, a: torch.Tensor, b: torch.Tensor, A_log:
                        aux_k: Optional[torch.Tensor] = None, aux_v: Optional[torch.Tensor] = None,
                        aux_g: Optional[torch.Tensor] = None, aux_k_per_khead: bool = False,
                        status: Optional[torch.Tensor] = None,
-                       size_order: Optional[torch.Tensor] = None,
-                       size_order_small: Optional[int] = None) -> torch.Tensor:
+                       size_order: Optional[torch.Tensor] = None) -> torch.Tensor:
     """``tree_verify`` with the previous step's accepted path committed into
     each request's state slot on the way in (one read of the state, one
     write back).  The pending_* tensors are the previous step's saves
@@ -315,14 +303,14 @@ def tree_commit_verify(y: torch.Tensor, a: torch.Tensor, b: torch.Tensor, A_log:
     walk from its tree's root (each entry's ancestors are the entries before
     it), as an accepted path is, and the slot to hold the state the previous
     verify read.  Previous rows of request b start at prev_cu_seqlens[b] or
-    b * prev_n_nodes.  Returns o.  ``status``, ``size_order`` and
-    ``size_order_small`` as in ``tree_verify``; status adds DFT_STATUS_PATH for a pending entry past the
+    b * prev_n_nodes.  Returns o.  ``status`` and ``size_order`` as in
+    ``tree_verify``; status adds DFT_STATUS_PATH for a pending entry past the
     previous tree (the entry is ignored)."""
     args, o, dev, _keep = _verify_args(
         y, a, b, A_log, dt_bias, state, hk=hk, hv=hv, anc=anc, anc_bits=anc_bits, batch=batch, n_nodes=n_nodes,
         cu_seqlens=cu_seqlens, scale=scale, neg_exp_A=neg_exp_A, state_indices=state_indices,
         state_slot_stride=state_slot_stride, o=o, o_dtype=o_dtype, aux_k=aux_k, aux_v=aux_v, aux_g=aux_g,
-        aux_k_per_khead=aux_k_per_khead, status=status, size_order=size_order, size_order_small=size_order_small)
+        aux_k_per_khead=aux_k_per_khead, status=status, size_order=size_order)
     _device_of(pending_path, pending_keys, pending_key_rows, pending_values, pending_value_rows, pending_b,
                pending_gains, pending_path_len, prev_cu_seqlens, y)
     if (pending_keys is None) == (pending_key_rows is None):

@@ -60,7 +60,7 @@ def test_ctypes_structs_match_c_layout(c_layouts):
     from dforktree_amd import _lib
     layout, structs = c_layouts
     # the status words, then the size-order records, were appended: every earlier field kept its offset
-    assert [f for f, _ in _lib.VerifyArgs._fields_[-3:]] == ["status", "size_order", "size_order_small"]
+    assert [f for f, _ in _lib.VerifyArgs._fields_[-2:]] == ["status", "size_order"]
     assert _lib.CommitArgs._fields_[-1][0] == "status"
     for cname, py in structs.items():
         assert ctypes.sizeof(py) == layout[f"{cname}.__size__"], cname
@@ -98,11 +98,7 @@ def test_validation_rejects_bad_descriptors_without_launching():
     assert lib.dft_tree_verify(ctypes.byref(v), None) == _lib.DFT_ERR_INVALID       # size order, not packed
     v.cu_seqlens, v.size_order = 16, 8
     assert lib.dft_tree_verify(ctypes.byref(v), None) == _lib.DFT_ERR_INVALID       # records: 16 B
-    v.size_order, v.flags = None, _lib.DFT_VERIFY_ORDER_COUNT
-    assert lib.dft_tree_verify(ctypes.byref(v), None) == _lib.DFT_ERR_INVALID       # a count without records
-    v.size_order, v.size_order_small = 16, 2
-    assert lib.dft_tree_verify(ctypes.byref(v), None) == _lib.DFT_ERR_INVALID       # count > batch
-    v.cu_seqlens, v.size_order, v.size_order_small, v.flags = None, None, 0, 0
+    v.cu_seqlens, v.size_order = None, None
     assert lib.dft_tree_commit_verify(ctypes.byref(v), None, None) == _lib.DFT_ERR_INVALID  # no pending
     assert lib.dft_tree_commit_verify(ctypes.byref(v), ctypes.byref(pc), None) == _lib.DFT_ERR_INVALID
     pc.path = pc.keys = pc.values = pc.gains = 16

@@ -43,7 +43,6 @@ class Step:
         b1 = synth.make_batch(seed, 0, sizes, hk=2, hv=4, kinds=kinds[:len(sizes)])
         b2 = synth.make_batch(seed + 1, 0, sizes, hk=2, hv=4, kinds=kinds[::-1][:len(sizes)])
         self.packed, self.B, self.N, self.hk, self.hv = packed, b1.batch, b1.n_max, 2, 4
-        self.sizes = list(sizes)
         self.g1, self.g2 = b1.to(cuda), b2.to(cuda)
         rows = self.g1.y.shape[0]
         gen = torch.Generator().manual_seed(seed + 2)
@@ -99,8 +98,8 @@ class Step:
         kw = dict(batch=self.B, n_nodes=self.N)
         if self.packed:
             kw["cu_seqlens"] = g.cu_seqlens
-            if order is not None:  # the packed step's size-order records (written by run) and class count
-                kw.update(size_order=order, size_order_small=sum(1 for n in self.sizes if n <= 32))
+            if order is not None:  # the packed step's size-order records (written by run)
+                kw["size_order"] = order
         return kw
 
     def run(self):
