@@ -1844,6 +1844,14 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
   if constexpr (!kEarly) phase_saves<NP, COMMIT, NW>(P, it, tid, sm, sm);
   const int mtn = (it.n + 15) >> 4;  // uniform over the workgroup
   phase_gram_diag<NP, NW>(tid, sm, sm, mtn);
+  if constexpr (kEarly && RVN) {
+    // The recompute forms hold few registers for the path (raw rows, 10 per
+    // lane): their loads go out here, once the diagonal solves (a 32-float
+    // column per lane) are done, and stream in under the rest of phase 1
+    // (65.4 -> 65.0 us at batch 64; issued before the solves they spilled).
+    pd = decode_pending(ph, lane, sm.graw[4][lane & 15]);
+    issue_pending<NW, RAWK, RVN>(P.c, pd, it.h, wave, lane, S0, kr, pv);
+  }
   if constexpr (kSplit) issue_state_group<false, false, NW>(S0, p.state_v_stride, wave, lane, 2, s0r);
   __syncthreads();
 #pragma unroll
@@ -1856,10 +1864,13 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
   phase_pq<NP, NW>(tid, sm, sm, mtn);
   phase_split_x<NP, NW>(tid, sm, mtn);
   if constexpr (kEarly) {
-    // the path's entry words came with the gates (row 4); its loads go out
-    // now, so that they are not held in registers through phase 1
-    pd = decode_pending(ph, lane, sm.graw[4][lane & 15]);
-    issue_pending<NW, RAWK, RVN>(P.c, pd, it.h, wave, lane, S0, kr, pv);
+    // the path's entry words came with the gates (row 4); the saved-value
+    // forms' loads go out now, so that they are not held in registers through
+    // phase 1
+    if constexpr (!RVN) {
+      pd = decode_pending(ph, lane, sm.graw[4][lane & 15]);
+      issue_pending<NW, RAWK, RVN>(P.c, pd, it.h, wave, lane, S0, kr, pv);
+    }
     float* stage = reinterpret_cast<float*>(sm.vrows());  // 8 KiB: the 16 path keys, then the write-back
     commit_tile<NW, true, RAWK, RVN>(pd, stage, rvx, kr, pv, wave, lane, s0r);
     __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 15));
