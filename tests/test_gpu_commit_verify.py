@@ -336,6 +336,50 @@ def test_commit_verify_equals_commit_then_verify(cuda):
         assert rel_l2(np32(x), np32(y)) <= 1e-6
 
 
+def test_commit_verify_recomputed_values_slots_int64_vhead_keys(cuda):
+    """The recomputed-value form with keys saved per v-head (k_head_div 1),
+    int64 path entries and state indices [2, -1, 1, 3] over a pool of 5
+    slots: against the same launch with saved values (committed states within
+    rel-L2 1e-5, o within 1e-4).  The slotless request verifies on slot 0 and
+    commits nothing, so slots 0 and 4 keep their bits (no committing request
+    owns slot 0, which the slotless one reads)."""
+    from dforktree_amd import ops, synth
+    announce("commit->verify recomputed values: v-head keys, int64 paths, slots")
+    B, N, hk, hv = 4, 32, 2, 4
+    b1 = synth.make_batch(54, 0, [N] * B, hk=hk, hv=hv, kinds=["random", "chain", "bushy", "random"])
+    b2 = synth.make_batch(55, 0, [N] * B, hk=hk, hv=hv)
+    g1, g2 = b1.to(cuda), b2.to(cuda)
+    rows = B * N
+    slots = torch.tensor([2, -1, 1, 3], dtype=torch.int32, device=cuda)
+    pool0 = (torch.randn(5, hv, 128, 128, generator=torch.Generator().manual_seed(56)) * 0.02).to(cuda)
+    k1 = torch.zeros(hv, rows, 128, device=cuda)
+    v1 = torch.zeros(hv, rows, 128, device=cuda)
+    G1 = torch.zeros(hv, rows, device=cuda)
+    ts1 = ops.tree_struct(g1.parent, 4, batch=B, n_nodes=N, want=("anc_bits",))["anc_bits"]
+    ts2 = ops.tree_struct(g2.parent, 4, batch=B, n_nodes=N, want=("anc_bits",))["anc_bits"]
+    ops.tree_verify(g1.y, g1.a, g1.b, g1.A_log, g1.dt_bias, pool0.transpose(-1, -2), hk=hk, hv=hv, anc_bits=ts1,
+                    batch=B, n_nodes=N, state_indices=slots, aux_k=k1, aux_v=v1, aux_g=G1)
+    idx, lens, _ = _paths(b1, 57)
+    idx_d, lens_d = idx.to(torch.int64).to(cuda), lens.to(cuda)
+    common = dict(hk=hk, hv=hv, anc_bits=ts2, batch=B, n_nodes=N, state_indices=slots, pending_path=idx_d,
+                  pending_keys=k1, pending_gains=G1, pending_path_len=lens_d, prev_n_nodes=N, pending_k_head_div=1)
+    pools, outs = [], []
+    for recompute in (False, True):
+        pool = pool0.clone()
+        vals = (dict(pending_values=None, pending_value_rows=g1.y[:, 2 * hk * 128:].unflatten(1, (hv, 128)),
+                     pending_b=g1.b) if recompute else dict(pending_values=v1))
+        outs.append(ops.tree_commit_verify(g2.y, g2.a, g2.b, g2.A_log, g2.dt_bias, pool.transpose(-1, -2), **vals,
+                                           **common))
+        pools.append(pool)
+    torch.cuda.synchronize()
+    for s_ in (0, 4):
+        assert np.array_equal(np32(pools[1][s_]), np32(pool0[s_])), f"slot {s_} was written"
+    for s_ in (1, 2, 3):
+        assert not np.array_equal(np32(pools[1][s_]), np32(pool0[s_])), f"slot {s_} was not committed"
+    assert rel_l2(np32(pools[1]), np32(pools[0])) <= 1e-5
+    assert rel_l2(np32(outs[1]), np32(outs[0])) <= 1e-4
+
+
 def test_commit_verify_negative_slot_commits_nothing(cuda):
     """State indices [2, -1, 1] over a pool of 4 slots, every request with a
     pending path: the request without a slot verifies on slot 0 (as the plain
