@@ -401,6 +401,40 @@ def plugin_lines(dev, reps, warmup, eager):
     return lines
 
 
+def copy_rate(dev, reps=20):
+    """Achievable HBM rate on this GPU: GB/s (bytes read + bytes written) of
+    the streaming copy kernel built beside the library
+    (dforktree_amd/calib/stream_copy.hip: 16-byte non-temporal loads and
+    stores) over a 1 GiB buffer, four times the memory-side cache, timed as
+    a HIP graph of back-to-back copies like the layers.  torch's copy_ of the
+    same buffers is reported beside it.  None if the copy library is absent."""
+    import ctypes
+    import torch
+    path = ROOT / "dforktree_amd" / "libdft_stream_copy.so"
+    if not path.exists():
+        return None
+    lib = ctypes.CDLL(str(path))
+    lib.dft_calib_stream_copy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p]
+    nbytes = 1 << 30
+    src = torch.ones(nbytes // 4, device=dev)
+    dst = torch.empty_like(src)
+
+    def kernel_copy():
+        rc = lib.dft_calib_stream_copy(src.data_ptr(), dst.data_ptr(), nbytes,
+                                       ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+        if rc != 0:
+            raise RuntimeError(f"dft_calib_stream_copy returned {rc}")
+
+    ms = time_graph(kernel_copy, reps, 3)
+    if not torch.equal(dst[::4096], src[::4096]):
+        raise RuntimeError("stream copy produced a wrong result")
+    ms_torch = time_graph(lambda: dst.copy_(src), reps, 3)
+    del src, dst
+    return {"kernel": "stream_copy_kernel (16-byte non-temporal load + store per thread)", "bytes": 2 * nbytes,
+            "achieved": round(2 * nbytes / (ms * 1e-3) / 1e9, 1),
+            "torch_copy": round(2 * nbytes / (ms_torch * 1e-3) / 1e9, 1), "unit": "GB/s"}
+
+
 def time_graph(fn, reps, warmup, eager=False):
     """ms per call of fn (a sequence of launches), HIP events on the current stream."""
     import torch
@@ -573,6 +607,9 @@ def main():
         torch.cuda.synchronize()
         del src, dst
 
+    torch.cuda.empty_cache()
+    copy = copy_rate(dev)
+
     vb, cb, fb = w.verify_bytes_per_launch(), w.commit_bytes_per_launch(), w.fused_bytes_per_launch()
     kernels = {"tree_commit_verify_kernel": dict(ms=t_fused, bytes=fb, per_step=L)}
     dom = max(kernels, key=lambda k: kernels[k]["ms"] * kernels[k]["per_step"])
@@ -622,7 +659,9 @@ def main():
                    "timing": "eager" if args.eager else "hip graph"},
         "roofline": {"kernel": dom, "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "algorithmic_bytes_per_launch": kd["bytes"]},
+                     "algorithmic_bytes_per_launch": kd["bytes"],
+                     # what a streaming copy reaches on this GPU, and the kernel's rate against it
+                     "copy": copy, "frac_of_copy": round(achieved / copy["achieved"], 4) if copy else None},
         "mfma": mfma,
         "commit_verify_us_per_layer": round(t_fused * 1e3, 2),
         # the same launch with the values saved by the verify and read back by the next commit (keys from the

@@ -4,6 +4,9 @@
 
 Every csrc/*.hip is compiled to an object with hipcc (in parallel) and linked
 into one shared library that exports the C ABI of include/dforktree_amd.h.
+calib/stream_copy.hip, the streaming copy that bench.py times as the
+achievable-bandwidth reference, goes into a library of its own
+(dforktree_amd/libdft_stream_copy.so), outside the C ABI.
 Packed-fp32 instruction selection is disabled for all device code.
 """
 from __future__ import annotations
@@ -19,6 +22,8 @@ CSRC = PKG / "csrc"
 INCLUDE = PKG.parent / "include"
 BUILD = PKG / "_build"
 LIB = PKG / "libdforktree_amd.so"
+CALIB_SRC = PKG / "calib" / "stream_copy.hip"
+CALIB_LIB = PKG / "libdft_stream_copy.so"
 ARCH = os.environ.get("DFT_OFFLOAD_ARCH", "gfx950")
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
@@ -60,6 +65,11 @@ def build(verbose: bool = False) -> Path:
     if rc != 0:
         raise RuntimeError(f"link failed ({rc}):\n{out}")
     os.replace(tmp, LIB)
+    tmp = CALIB_LIB.with_suffix(".so.tmp")
+    rc, out = _run([HIPCC, *COMMON, "-shared", str(CALIB_SRC), "-o", str(tmp)])
+    if rc != 0:
+        raise RuntimeError(f"hipcc failed ({rc}) on {CALIB_SRC}:\n{out}")
+    os.replace(tmp, CALIB_LIB)
     return LIB
 
 

@@ -211,3 +211,19 @@ def test_python_layer_refuses_cpu_tensors():
     x = torch.zeros(4, 4)
     with pytest.raises(ValueError, match="GPU tensors"):
         ops.block_inverse_(x)
+
+
+def test_stream_copy_library_is_outside_the_c_abi():
+    """The bench's copy calibration kernel lives in its own library, exports
+    one symbol and rejects bad arguments before any launch."""
+    from dforktree_amd import build
+    assert build.CALIB_LIB.exists()
+    out = subprocess.run(["nm", "-D", "--defined-only", str(build.CALIB_LIB)], capture_output=True, text=True).stdout
+    assert {l.split()[-1] for l in out.splitlines() if " T " in l} == {"dft_calib_stream_copy"}
+    lib = ctypes.CDLL(str(build.CALIB_LIB))
+    f = lib.dft_calib_stream_copy
+    f.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p]
+    assert f(None, ctypes.c_void_p(16), 16, None) == 1
+    assert f(ctypes.c_void_p(16), ctypes.c_void_p(32), 24, None) == 1   # not a multiple of 16
+    assert f(ctypes.c_void_p(16), ctypes.c_void_p(40), 16, None) == 1   # misaligned destination
+    assert f(ctypes.c_void_p(16), ctypes.c_void_p(32), 0, None) == 1
