@@ -545,6 +545,59 @@ __device__ __forceinline__ void issue_pending(const dft_pending_commit& c, const
   }
 }
 
+// (32-wide recompute form with raw key rows) The path's raw k and v rows
+// copied into LDS ahead of the state tile, so that they do not queue behind
+// it: key slot s (position rvn_slot(s)) at row s of praw, value position p
+// at row 16 + p, both in the q/k row layout; the gains (lanes 0-15) and the
+// b-gate words (lanes 16-31) at rvx[0 .. 31], which the recompute claims only
+// after path_from_lds has read them.
+template <int NW>
+__device__ __forceinline__ void issue_path_dma(const dft_pending_commit& c, const Pending& pd, int h, int wave,
+                                               int lane, const float* dummy, uint16_t* praw, float* rvx) {
+  static_assert(NW == 4, "one key and one value copy per wave");
+  const bool any = pd.last >= 0;
+  const int cp = lane & 15, s = 4 * wave + (lane >> 4);
+  const int krow = __shfl(pd.ent, rvn_slot(s));
+  const int vrow = __shfl(pd.ent, s);
+  const uint16_t* kb = any ? c.key_rows + (int64_t)(h / c.k_head_div) * c.kr_h_stride + pd.prow0 * c.kr_row_stride
+                           : reinterpret_cast<const uint16_t*>(dummy);
+  const uint16_t* vb = any ? c.value_rows + (int64_t)h * c.vr_h_stride + pd.prow0 * c.vr_row_stride
+                           : reinterpret_cast<const uint16_t*>(dummy);
+  const int64_t ks = any ? c.kr_row_stride : 0, vs = any ? c.vr_row_stride : 0;
+  const int ck = 8 * ((cp ^ s) & 15);  // the chunk that lands at chunk position cp of row s
+  lds_dma16(kb + krow * ks + ck, praw + 4 * wave * kD);
+  lds_dma16(vb + vrow * vs + ck, praw + (16 + 4 * wave) * kD);
+  if (wave == 0 && lane < 32) {
+    const void* src;
+    if (lane < 16) {
+      src = any ? static_cast<const void*>(c.gains + (int64_t)h * c.g_h_stride + (pd.prow0 + pd.ent) * c.g_row_stride)
+                : static_cast<const void*>(dummy);
+    } else {
+      uint32_t sh;
+      src = any ? static_cast<const void*>(word_of(c.prev_b, (pd.prow0 + pd.ent) * c.pb_row_stride + h,
+                                                   c.prev_b_dtype, sh))
+                : static_cast<const void*>(dummy);
+    }
+    lds_dma4(src, rvx);
+  }
+}
+// The keys, gains and b gates issue_pending would have loaded, read from
+// those copies (the values are read where W is formed: path_values<VLDS>).
+template <int NW>
+__device__ __forceinline__ void path_from_lds(const dft_pending_commit& c, const Pending& pd, int h, int wave,
+                                              int lane, const uint16_t* praw, const float* rvx,
+                                              PathKeys<NW, true>& pk, PathVals<NW, true>& pv) {
+  const int n16 = lane & 15, g4 = lane >> 4;
+  const int rs = rvn_slot(4 * (wave & 3) + g4);
+#pragma unroll
+  for (int m = 0; m < 2; ++m) pk.raw[m] = *reinterpret_cast<const uint2*>(&praw[qkv_at(rs, 4 * n16 + 64 * m)]);
+  pv.gl = rvx[n16];
+  const bool any = pd.last >= 0;
+  uint32_t sh = 0;
+  if (any) (void)word_of(c.prev_b, (pd.prow0 + pd.ent) * c.pb_row_stride + h, c.prev_b_dtype, sh);
+  pv.bl = word_to_f(__float_as_uint(rvx[16 + n16]), any ? sh : 0u, any ? c.prev_b_dtype : (int)DFT_F32);
+}
+
 // Whole-line state loads (the 32-wide fused form).  In the MFMA layout
 // (s0r[t][j] = S0[k = 16j + 4g + e][v = CW w + 16t + n]) one load covers 64
 // bytes of each of 16 rows, and a line's two halves come from two
@@ -699,7 +752,9 @@ __device__ __forceinline__ void mat16_store(float* D, f32x4 acc, int n16, int g4
 //    position p from slot rvn_slot(p).
 // Every thread arrives here (one barrier, skipped by the whole workgroup
 // when nothing is pending).
-template <int NW, bool RAWK>
+// VLDS: the raw value rows are in LDS (rows 16 + position of the key
+// staging, issue_path_dma) rather than in pv.vr.
+template <int NW, bool RAWK, bool VLDS = false>
 __device__ __forceinline__ void path_values(const Pending& pd, const float* pkey, float* rvx,
                                             const PathVals<NW, true>& pv, int wave, int lane,
                                             const f32x4 (&s0r)[Waves<NW>::TT][8], float (&vnr)[4][Waves<NW>::TT]) {
@@ -823,7 +878,11 @@ __device__ __forceinline__ void path_values(const Pending& pd, const float* pkey
     const float ep = __expf(__shfl(pv.gl, ip)) * (RAWK ? rvx[kRvxNorms + p] : 1.f);
     const bool ok = (pd.vmask >> ip) & 1u;
 #pragma unroll
-    for (int t = 0; t < TT; ++t) w[t][e] = ok ? bp * (bf16_bits_to_f32(vr[e][t]) - ep * w[t][e]) : 0.f;
+    for (int t = 0; t < TT; ++t) {
+      const uint16_t vb = VLDS ? reinterpret_cast<const uint16_t*>(pkey)[qkv_at(16 + ip, Waves<NW>::CW * wave + 16 * t + n16)]
+                               : vr[e][t];
+      w[t][e] = ok ? bp * (bf16_bits_to_f32(vb) - ep * w[t][e]) : 0.f;
+    }
   }
   __syncthreads();  // X complete
   f32x4 vn[TT];
@@ -849,7 +908,7 @@ __device__ __forceinline__ void path_values(const Pending& pd, const float* pkey
 // whole lines, and is turned into the MFMA layout after the keys are staged:
 // they were loaded after it, so it has landed, and their registers are free
 // by then.
-template <int NW, bool LINES, bool RAWK, bool RVN>
+template <int NW, bool LINES, bool RAWK, bool RVN, bool VLDS = false>
 __device__ __forceinline__ void commit_tile(const Pending& pd, float* pkey, float* rvx, const PathKeys<NW, RAWK>& kr,
                                             const PathVals<NW, RVN>& pv, int wave, int lane,
                                             f32x4 (&s0r)[Waves<NW>::TT][8]) {
@@ -871,7 +930,7 @@ __device__ __forceinline__ void commit_tile(const Pending& pd, float* pkey, floa
 #pragma unroll
         for (int j = 0; j < 8; ++j) asm volatile("" : "+v"(s0r[t][j]));
     __builtin_amdgcn_sched_barrier(0);
-    path_values<NW, RAWK>(pd, pkey, rvx, pv, wave, lane, s0r, vnr);
+    path_values<NW, RAWK, VLDS>(pd, pkey, rvx, pv, wave, lane, s0r, vnr);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int s = 0; s < 4; ++s) gp[s] = __shfl(pv.gl, 4 * s + g4);
@@ -1704,7 +1763,7 @@ __device__ __forceinline__ void fused_status(const Item& it, int lane, uint32_t 
 
 // The body of the one-head-per-workgroup kernels (COMMIT: the fused commit ->
 // verify form).
-template <int NP, bool S0VEC, bool COMMIT, bool RAWK, bool RVN>
+template <int NP, bool S0VEC, bool COMMIT, bool RAWK, bool RVN, bool PDMA = false>
 __device__ __forceinline__ void verify_body(const VerifyParams& P) {
   constexpr int MT = NP / 16;
   constexpr int NW = WavesFor<NP>();
@@ -1714,6 +1773,10 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
   // write-back in the v region, whose rows it copies in afterwards.
   constexpr bool kEarly = COMMIT && !VerifySmem<NP>::kLateV;
   constexpr int kPlanes = (VerifySmem<NP>::kLateV || kEarly) ? 2 : 3;  // the late forms copy v rows later
+  // PDMA: the path's raw rows are copied into LDS ahead of the state tile
+  // (16-byte aligned key and value rows; issue_path_dma)
+  constexpr bool kPathDma = PDMA;
+  static_assert(!PDMA || (kEarly && RVN && RAWK), "the path copies serve the 32-wide recompute form");
   constexpr int kQkvDma = kPlanes * (NP / (4 * NW));          // row copies per wave
   constexpr int kStateLoads = 8 * TT, kGroupLoads = 2 * TT;   // per lane: whole tile, one k-step group
   const dft_verify_args& p = P.a;
@@ -1774,6 +1837,10 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
   PathVals<NW, RVN> pv;
   uint32_t pword = 0;
   if constexpr (COMMIT && !kEarly) pword = *path_word(P.c, it.b, lane);
+  if constexpr (kPathDma) {
+    pword = *path_word(P.c, it.b, lane);
+    asm volatile("" ::: "memory");
+  }
   if (wave == 0) issue_gates(p, it, lane, S0, sm.graw, COMMIT ? path_word(P.c, it.b, lane) : nullptr);
   if (p.anc_f32) dense_ancestry<NP, NW>(p, it, wave, lane, sm);
   issue_rows<NP, 0, kPlanes, NW>(p, it, wave, lane, S0, sm);
@@ -1781,6 +1848,9 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
     pd = decode_pending(ph, lane, pword);
     issue_pending<NW, RAWK, RVN>(P.c, pd, it.h, wave, lane, S0, kr, pv);
   }
+  if constexpr (kPathDma)
+    issue_path_dma<NW>(P.c, decode_pending(ph, lane, pword), it.h, wave, lane, S0,
+                       reinterpret_cast<uint16_t*>(sm.vrows()), rvx);
   asm volatile("" ::: "memory");
 
   f32x4 s0r[TT][8];
@@ -1850,7 +1920,7 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
     // column per lane) are done, and stream in under the rest of phase 1
     // (65.4 -> 65.0 us at batch 64; issued before the solves they spilled).
     pd = decode_pending(ph, lane, sm.graw[4][lane & 15]);
-    issue_pending<NW, RAWK, RVN>(P.c, pd, it.h, wave, lane, S0, kr, pv);
+    if constexpr (!kPathDma) issue_pending<NW, RAWK, RVN>(P.c, pd, it.h, wave, lane, S0, kr, pv);
   }
   if constexpr (kSplit) issue_state_group<false, false, NW>(S0, p.state_v_stride, wave, lane, 2, s0r);
   __syncthreads();
@@ -1872,7 +1942,9 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
       issue_pending<NW, RAWK, RVN>(P.c, pd, it.h, wave, lane, S0, kr, pv);
     }
     float* stage = reinterpret_cast<float*>(sm.vrows());  // 8 KiB: the 16 path keys, then the write-back
-    commit_tile<NW, true, RAWK, RVN>(pd, stage, rvx, kr, pv, wave, lane, s0r);
+    if constexpr (kPathDma)
+      path_from_lds<NW>(P.c, pd, it.h, wave, lane, reinterpret_cast<const uint16_t*>(stage), rvx, kr, pv);
+    commit_tile<NW, true, RAWK, RVN, kPathDma>(pd, stage, rvx, kr, pv, wave, lane, s0r);
     __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 15));
     if (pd.last >= 0) {  // uniform over the workgroup (one request)
       __syncthreads();  // every wave has read the staged keys
@@ -1933,11 +2005,12 @@ tree_verify_kernel(const VerifyParams P) {
 // back from offset 0 of the kernel-argument segment.
 static_assert(std::is_trivially_copyable<VerifyParams>::value, "VerifyParams is passed by value to the kernels");
 // RAWK: the pending keys are the previous step's raw bf16 rows; RVN: the
-// path's values are recomputed from raw rows
-template <int NP, bool RAWK, bool RVN>
+// path's values are recomputed from raw rows; PDMA: (32-wide, both raw)
+// those rows are copied into LDS ahead of the state tile
+template <int NP, bool RAWK, bool RVN, bool PDMA = false>
 __global__ void __launch_bounds__(64 * WavesFor<NP>()) __attribute__((amdgpu_waves_per_eu(4)))
 tree_commit_verify_kernel(const VerifyParams P) {
-  verify_body<NP, true, true, RAWK, RVN>(P);
+  verify_body<NP, true, true, RAWK, RVN, PDMA>(P);
 }
 
 static VerifyParams make_params(const dft_verify_args* a) {
@@ -2060,6 +2133,11 @@ int launch_tree_commit_verify(const dft_verify_args* a, const dft_pending_commit
   split_by_size(a, P, narrow, wide, split);
   // the previous step's raw key rows, recomputed values (validated by the caller)
   const int form = (c->keys == nullptr ? 1 : 0) + (c->values == nullptr ? 2 : 0);
+  // both as raw rows whose 16-byte pieces are aligned: the 32-wide kernel
+  // copies them into LDS ahead of the state tile
+  const auto al16 = [](const void* q) { return reinterpret_cast<uintptr_t>(q) % 16 == 0; };
+  const bool pdma = form == 3 && al16(c->key_rows) && al16(c->value_rows) && c->kr_h_stride % 8 == 0 &&
+                    c->kr_row_stride % 8 == 0 && c->vr_h_stride % 8 == 0 && c->vr_row_stride % 8 == 0;
 #define DFT_FUSED(np, g, b, prm)                                                                               \
   switch (form) {                                                                                              \
     case 0: hipLaunchKernelGGL((tree_commit_verify_kernel<np, false, false>), g, b, 0, stream, prm); break;   \
@@ -2068,7 +2146,12 @@ int launch_tree_commit_verify(const dft_verify_args* a, const dft_pending_commit
     default: hipLaunchKernelGGL((tree_commit_verify_kernel<np, true, true>), g, b, 0, stream, prm); break;    \
   }
   if (a->n_nodes > 32) DFT_FUSED(64, grid, block64, wide)
-  if (a->n_nodes <= 32 || split) DFT_FUSED(32, grid, block, narrow)
+  if (a->n_nodes <= 32 || split) {
+    if (pdma)
+      hipLaunchKernelGGL((tree_commit_verify_kernel<32, true, true, true>), grid, block, 0, stream, narrow);
+    else
+      DFT_FUSED(32, grid, block, narrow)
+  }
 #undef DFT_FUSED
   return hipGetLastError() == hipSuccess ? DFT_OK : DFT_ERR_LAUNCH;
 }

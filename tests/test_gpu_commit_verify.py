@@ -63,13 +63,15 @@ def _committed_states(batch1, walks):
 
 
 def _run_chain(cuda, batch1, batch2, per_khead, packed, empty=(), shorten=(), path_dtype=torch.int32,
-               raw_keys=False, raw_values=False, ordered=False):
+               raw_keys=False, raw_values=False, ordered=False, row_pad=0):
     """Step 1 verifies batch1 (saving k, vn, G); step 2 verifies batch2
     through the fused entry, committing step 1's walks first.  raw_keys: step
     1 saves no keys, and the commit reads step 1's raw bf16 k rows from its y.
     raw_values: step 1 saves no values, and the commit recomputes them from
     step 1's raw bf16 v rows (from its y) and b gates.  ordered: step 2's
-    fused launch reads size-order records of its packed batch."""
+    fused launch reads size-order records of its packed batch.  row_pad: the
+    raw rows come from a copy of step 1's y whose rows are row_pad elements
+    longer (not 16-byte multiples for row_pad = 4)."""
     from dforktree_amd import ops
     hk, hv, B = batch1.hk, batch1.hv, batch1.batch
     pool = batch1.state.clone().to(cuda)  # [B, hv, V, K]
@@ -96,13 +98,17 @@ def _run_chain(cuda, batch1, batch2, per_khead, packed, empty=(), shorten=(), pa
                     aux_k_per_khead=per_khead, **kw1)
     idx, lens, walks = _paths(batch1, 5, empty, shorten)
     prev = dict(prev_cu_seqlens=g1.cu_seqlens) if packed else dict(prev_n_nodes=batch1.n_max)
+    y1 = g1.y
+    if row_pad:
+        y1 = torch.empty(rows1, y1.shape[1] + row_pad, dtype=y1.dtype, device=cuda)[:, :y1.shape[1]]
+        y1.copy_(g1.y)
     if raw_keys:  # the k part of step 1's y, [rows, hk, 128]
-        keys = dict(pending_keys=None, pending_key_rows=g1.y[:, hk * 128:2 * hk * 128].unflatten(1, (hk, 128)),
+        keys = dict(pending_keys=None, pending_key_rows=y1[:, hk * 128:2 * hk * 128].unflatten(1, (hk, 128)),
                     pending_k_head_div=hv // hk)
     else:
         keys = dict(pending_keys=k1, pending_k_head_div=hv // kh)
     if raw_values:  # the v part of step 1's y, [rows, hv, 128], and its b gates
-        keys.update(pending_values=None, pending_value_rows=g1.y[:, 2 * hk * 128:].unflatten(1, (hv, 128)),
+        keys.update(pending_values=None, pending_value_rows=y1[:, 2 * hk * 128:].unflatten(1, (hv, 128)),
                     pending_b=g1.b)
     else:
         keys.update(pending_values=v1)
@@ -276,6 +282,29 @@ def test_commit_verify_recomputed_values(cuda, sizes1, sizes2, packed, b_dtype):
                                         shorten=shorten, raw_keys=raw_keys)
         assert rel_l2(np32(pool), np32(pool_s)) <= 1e-5
         assert rel_l2(np32(o2), np32(o2_s)) <= 1e-4
+
+
+@pytest.mark.parametrize("packed", [False, True])
+def test_commit_verify_recomputed_values_unaligned_rows(cuda, packed):
+    """Raw k and v rows whose row stride is not a multiple of 16 bytes take the
+    32-wide kernel that loads them into registers; aligned rows take the one
+    that copies them into LDS ahead of the state tile.  Both read the same
+    values: bit-identical states, outputs and saves, and the oracle chain."""
+    from dforktree_amd import synth
+    announce(f"commit->verify recomputed values, aligned vs padded rows packed={packed}")
+    sizes1, sizes2 = ([32, 7, 19, 1, 32, 25], [32, 12, 32, 4, 17, 30]) if packed else ([32] * 6, [32] * 6)
+    kinds = ["random", "chain", "bushy", "random", "chain", "bushy"]
+    batch1 = synth.make_batch(50, 0, sizes1, hk=2, hv=4, kinds=kinds)
+    batch2 = synth.make_batch(51, 0, sizes2, hk=2, hv=4, kinds=kinds[::-1])
+    empty, shorten = (3,), (5,)
+    runs = [_run_chain(cuda, batch1, batch2, per_khead=True, packed=packed, empty=empty, shorten=shorten,
+                       raw_keys=True, raw_values=True, row_pad=pad) for pad in (0, 4)]
+    (pool_a, o_a, aux_a, walks), (pool_p, o_p, aux_p, _) = runs
+    _check_chain(batch1, batch2, pool_p, o_p, aux_p, walks, empty, per_khead=True)
+    assert torch.equal(pool_a, pool_p)
+    assert torch.equal(o_a, o_p)
+    for a, b in zip(aux_a, aux_p):
+        assert torch.equal(a, b)
 
 
 def test_commit_verify_recomputed_values_bench_shape(cuda):
