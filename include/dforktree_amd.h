@@ -333,7 +333,11 @@ typedef struct dft_pending_commit {
    * the gains are still read.  The valid entries must form a root walk of the
    * previous tree (each entry's ancestors are the valid entries before it),
    * as an accepted path does; the verify before such a commit need not save
-   * values (aux_v NULL). */
+   * values (aux_v NULL).  With both key_rows and value_rows 16-byte aligned
+   * (base, and strides multiples of 8 elements, as slices of a y row are),
+   * trees of up to 32 nodes take a kernel that copies the path's rows into
+   * LDS ahead of the state tile (about 1% faster at batch 64); the results
+   * are the same bits either way. */
   const uint16_t* value_rows;
   int64_t vr_h_stride, vr_row_stride;
   const void* prev_b;
