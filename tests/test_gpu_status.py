@@ -82,10 +82,13 @@ def test_status_is_optional_and_uniform_batches_report_zero(cuda):
     assert status.tolist() == [0, 0, 0] and torch.equal(o1, o2)
 
 
-def test_commit_verify_reports_a_path_entry_past_the_tree(cuda):
+@pytest.mark.parametrize("raw", [False, True])
+def test_commit_verify_reports_a_path_entry_past_the_tree(cuda, raw):
     """The fused entry: request 1's pending path names node 40 of a 32-node
     tree (ignored: the commit equals the one without it), request 2's next
-    tree is longer than n_nodes."""
+    tree is longer than n_nodes.  raw: the commit reads step 1's raw k and v
+    rows and recomputes the values (the kernel that copies the path's rows
+    into LDS ahead of the state tile)."""
     from dforktree_amd import ops, synth
     announce("commit->verify status")
     hk, hv, B = 2, 4, 4
@@ -110,9 +113,15 @@ def test_commit_verify_reports_a_path_entry_past_the_tree(cuda):
     idx[1, len(walks[1])] = 40  # past the 32-node tree: ignored, flagged
     ts2 = ops.tree_struct(g2.parent, 4, cu_seqlens=g2.cu_seqlens, n_nodes=40, batch=B, want=("anc_bits",))
     status = torch.full((B,), -5, device=cuda, dtype=torch.int32)
+    if raw:
+        rows = dict(pending_keys=None, pending_key_rows=g1.y[:, hk * 128:2 * hk * 128].unflatten(1, (hk, 128)),
+                    pending_k_head_div=hv // hk, pending_values=None,
+                    pending_value_rows=g1.y[:, 2 * hk * 128:].unflatten(1, (hv, 128)), pending_b=g1.b)
+    else:
+        rows = dict(pending_keys=k1, pending_values=v1)
     ops.tree_commit_verify(g2.y, g2.a, g2.b, g2.A_log, g2.dt_bias, st, hk=hk, hv=hv, anc_bits=ts2["anc_bits"],
                            cu_seqlens=g2.cu_seqlens, n_nodes=32, batch=B, pending_path=idx.to(cuda),
-                           pending_keys=k1, pending_values=v1, pending_gains=G1, prev_n_nodes=32, status=status)
+                           pending_gains=G1, prev_n_nodes=32, status=status, **rows)
     torch.cuda.synchronize()
     assert status.tolist() == [0, PATH, SPAN, 0]
     ref1 = oracle_verify(b1)
