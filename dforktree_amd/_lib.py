@@ -15,8 +15,8 @@ DFT_OK, DFT_ERR_INVALID, DFT_ERR_UNSUPPORTED, DFT_ERR_LAUNCH = 0, 1, 2, 3
 DFT_F32, DFT_BF16, DFT_F16, DFT_I32, DFT_I64 = 0, 1, 2, 3, 4
 DFT_VERIFY_AUX_K_PER_KHEAD = 1
 DFT_COMMIT_KV, DFT_COMMIT_CHECK_ANC, DFT_COMMIT_LEN_IS_LAST = 1, 2, 4
-DFT_STATUS_SPAN, DFT_STATUS_PATH = 1, 2
-ABI_VERSION = 4
+DFT_STATUS_SPAN, DFT_STATUS_PATH, DFT_STATUS_WALK = 1, 2, 4
+ABI_VERSION = 5
 
 i32, i64, f32, vp = C.c_int32, C.c_int64, C.c_float, C.c_void_p
 
@@ -57,6 +57,7 @@ class PendingArgs(C.Structure):
         ("key_rows", vp), ("kr_h_stride", i64), ("kr_row_stride", i64),
         ("value_rows", vp), ("vr_h_stride", i64), ("vr_row_stride", i64),
         ("prev_b", vp), ("pb_row_stride", i64), ("prev_b_dtype", i32),
+        ("prev_anc_bits", vp),
     ]
 
 

@@ -6,7 +6,9 @@ Every csrc/*.hip is compiled to an object with hipcc (in parallel) and linked
 into one shared library that exports the C ABI of include/dforktree_amd.h.
 calib/stream_copy.hip, the streaming copy that bench.py times as the
 achievable-bandwidth reference, goes into a library of its own
-(dforktree_amd/libdft_stream_copy.so), outside the C ABI.
+(dforktree_amd/libdft_stream_copy.so, ``build_calibration``), outside the C
+ABI; a failure there is reported as a warning and leaves the product
+library in place.
 Packed-fp32 instruction selection is disabled for all device code.
 """
 from __future__ import annotations
@@ -65,12 +67,22 @@ def build(verbose: bool = False) -> Path:
     if rc != 0:
         raise RuntimeError(f"link failed ({rc}):\n{out}")
     os.replace(tmp, LIB)
+    try:
+        build_calibration()
+    except RuntimeError as e:  # a bench-only artefact: the product library is built
+        print(f"warning: {e}", file=sys.stderr)
+    return LIB
+
+
+def build_calibration() -> Path:
+    """Compile the streaming-copy library that bench.py times as the
+    achievable-bandwidth reference (outside the C ABI); returns its path."""
     tmp = CALIB_LIB.with_suffix(".so.tmp")
     rc, out = _run([HIPCC, *COMMON, "-shared", str(CALIB_SRC), "-o", str(tmp)])
     if rc != 0:
         raise RuntimeError(f"hipcc failed ({rc}) on {CALIB_SRC}:\n{out}")
     os.replace(tmp, CALIB_LIB)
-    return LIB
+    return CALIB_LIB
 
 
 if __name__ == "__main__":

@@ -28,14 +28,23 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 constexpr int64_t max_blocks(int threads) { return (int64_t)0xffffffffll / threads; }
 
 // Checks shared by the verify entry points: DFT_OK to launch, DFT_ERR_* to
-// refuse, or -1 when there is nothing to do.
-int verify_status(const dft_verify_args* a) {
+// refuse, or -1 when there is nothing to do.  commit_only: a launch of the
+// fused entry with n_nodes 0, which commits the pending paths and verifies
+// nothing, so it reads no rows, gates, ancestry or outputs.
+int verify_status(const dft_verify_args* a, bool commit_only = false) {
   if (!a) return DFT_ERR_INVALID;
   if (a->batch < 0 || a->n_nodes < 0 || a->hk <= 0 || a->hv <= 0 || a->hv % a->hk != 0) return DFT_ERR_INVALID;
   if (a->dk != 128 || a->dv != 128) return DFT_ERR_UNSUPPORTED;
   if (a->n_nodes > 64) return DFT_ERR_UNSUPPORTED;
-  if (a->batch == 0 || a->n_nodes == 0) return -1;
-  if (!a->y || !a->a || !a->b || !a->state || !a->o) return DFT_ERR_INVALID;
+  if (a->batch == 0 || (a->n_nodes == 0 && !commit_only)) return -1;
+  if (!a->state) return DFT_ERR_INVALID;
+  if (a->state_indices && !index_tag(a->state_indices_dtype)) return DFT_ERR_INVALID;
+  // size-order records: 16-byte records of a packed batch
+  if (a->size_order && (!a->cu_seqlens || !aligned16(a->size_order))) return DFT_ERR_INVALID;
+  // one workgroup per (request, v-head): 4 waves for trees of up to 32 nodes, 8 beyond
+  if ((int64_t)a->batch * a->hv > max_blocks(a->n_nodes > 32 ? 512 : 256)) return DFT_ERR_UNSUPPORTED;
+  if (a->n_nodes == 0) return DFT_OK;
+  if (!a->y || !a->a || !a->b || !a->o) return DFT_ERR_INVALID;
   if (!a->neg_exp_A && !a->A_log) return DFT_ERR_INVALID;
   if (!a->dt_bias) return DFT_ERR_INVALID;
   if ((a->anc_f32 == nullptr) == (a->anc_bits == nullptr)) return DFT_ERR_INVALID;
@@ -43,13 +52,8 @@ int verify_status(const dft_verify_args* a) {
       (a->A_log && !float_tag(a->A_log_dtype)))
     return DFT_ERR_INVALID;
   if (a->o_dtype != DFT_F32 && a->o_dtype != DFT_BF16 && a->o_dtype != DFT_F16) return DFT_ERR_INVALID;
-  if (a->state_indices && !index_tag(a->state_indices_dtype)) return DFT_ERR_INVALID;
   // q/k/v rows are copied as 16-byte pieces
   if (!aligned16(a->y) || a->y_row_stride % 8 != 0) return DFT_ERR_INVALID;
-  // size-order records: 16-byte records of a packed batch
-  if (a->size_order && (!a->cu_seqlens || !aligned16(a->size_order))) return DFT_ERR_INVALID;
-  // one workgroup per (request, v-head): 4 waves for trees of up to 32 nodes, 8 beyond
-  if ((int64_t)a->batch * a->hv > max_blocks(a->n_nodes > 32 ? 512 : 256)) return DFT_ERR_UNSUPPORTED;
   return DFT_OK;
 }
 
@@ -76,7 +80,8 @@ int dft_tree_verify(const dft_verify_args* a, void* stream) {
 }
 
 int dft_tree_commit_verify(const dft_verify_args* a, const dft_pending_commit* c, void* stream) {
-  const int st = verify_status(a);
+  // n_nodes 0 (every request's tree empty) still commits the pending paths
+  const int st = verify_status(a, /*commit_only=*/true);
   if (st != DFT_OK) return st < 0 ? DFT_OK : st;
   if (!c) return DFT_ERR_INVALID;
   if (c->path_cols < 1) return DFT_ERR_INVALID;  // the kernels read entry path_cols - 1 for padding lanes

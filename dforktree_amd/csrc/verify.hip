@@ -134,6 +134,24 @@ __device__ __forceinline__ void lds_dma16_nt_untracked(const void* g, void* lds)
 __device__ __forceinline__ void lds_dma4(const void* g, void* lds) {
   __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)lds, 4, 0, 0);
 }
+// a 4-byte copy the backend's wait analysis does not see (as
+// lds_dma16_nt_untracked); the caller makes sure it has landed before the
+// destination is read
+__device__ __forceinline__ void lds_dma4_untracked(const void* g, void* lds) {
+  const uint32_t base =
+      __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)lds);
+  uint32_t keep;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %2\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dword %1, off\n\t"
+      "s_mov_b32 m0, %0\n\t"
+      "s_nop 0"
+      : "=&s"(keep)
+      : "v"(g), "s"(base)
+      : "memory");
+}
 
 struct VerifyParams {
   dft_verify_args a;
@@ -454,6 +472,45 @@ __device__ __forceinline__ Pending decode_pending(const PendingHead& ph, int lan
   const int u = __shfl(e, pd.last < 0 ? 0 : pd.last);
   pd.ent = ok ? e : (pd.last < 0 ? 0 : u);
   return pd;
+}
+
+// The ancestry rows of the pending entries for the walk check
+// (c.prev_anc_bits): wave 0's lanes 16-31 copy the low words and lanes 32-47
+// the high words of the row of entry lane % 16 into walk[16 .. 47] (row 4
+// of the gate words, whose lanes 16-47 nothing else reads).  With nothing
+// pending the source is `dummy` (valid memory, never checked).  UNTRACKED:
+// the copy is hidden from the backend's wait analysis (issued late, it
+// would make every LDS read after it wait for the whole state tile); the
+// caller's later loads, which return in order behind it, cover it.
+template <bool UNTRACKED>
+__device__ __forceinline__ void issue_walk_dma(const dft_pending_commit& c, const Pending& pd, int wave, int lane,
+                                               const void* dummy, uint32_t* walk) {
+  if (!c.prev_anc_bits || wave != 0 || lane < 16 || lane >= 48) return;
+  const uint32_t* src = pd.last >= 0 ? reinterpret_cast<const uint32_t*>(c.prev_anc_bits + pd.prow0 + pd.ent) + (lane >> 5)
+                                     : static_cast<const uint32_t*>(dummy);
+  if constexpr (UNTRACKED) lds_dma4_untracked(src, walk);
+  else lds_dma4(src, walk);
+}
+
+// Whether the valid pending entries, in path order, walk down from the
+// previous tree's root (uniform): lane c < 16 checks that its entry's
+// ancestors-or-self in that tree are exactly the valid entries 0 .. c and
+// that none of them repeats, which makes entry c the child of the valid
+// entry before it.  The recomputed values and the closed-form commit both
+// assume this (fc1_fused.py:41 checks path ancestry on the device).
+__device__ __forceinline__ bool pending_walk_ok(const Pending& pd, int lane, const uint32_t* walk, int bound) {
+  const int c = lane & 15, e = pd.ent;
+  const bool valid = (pd.vmask >> c) & 1u;
+  uint64_t m = (valid && e < 64) ? (1ull << e) : 0ull;  // entries past 63 cannot be rows of a tree here
+#pragma unroll
+  for (int o = 1; o < 16; o <<= 1) {  // inclusive OR over positions 0 .. c
+    const uint32_t lo = __shfl_up((uint32_t)m, o, 16), hi = __shfl_up((uint32_t)(m >> 32), o, 16);
+    if (c >= o) m |= ((uint64_t)hi << 32) | lo;
+  }
+  const uint64_t anc = (((uint64_t)walk[32 + c] << 32) | walk[16 + c]) & mask_upto(e) & mask_below(bound);
+  const int cnt = __popc(pd.vmask & ((2u << c) - 1u));
+  const bool ok = !valid || (e < 64 && __popcll(m) == cnt && anc == m);
+  return (__ballot(!ok) & 0xffffull) == 0;
 }
 
 // Two 16-byte pieces of the path keys per thread (path slot 4w + g, columns
@@ -907,15 +964,22 @@ __device__ __forceinline__ void path_values(const Pending& pd, const float* pkey
 // (the staging is followed by a barrier).  LINES: the tile was loaded as
 // whole lines, and is turned into the MFMA layout after the keys are staged:
 // they were loaded after it, so it has landed, and their registers are free
-// by then.
+// by then.  walk: the entries' ancestry rows (issue_walk_dma, landed before
+// the keys the staging waits for), or null for no walk check; a path that
+// fails it is dropped here (pd then says nothing is pending, and the caller
+// writes nothing back).
 template <int NW, bool LINES, bool RAWK, bool RVN, bool VLDS = false>
-__device__ __forceinline__ void commit_tile(const Pending& pd, float* pkey, float* rvx, const PathKeys<NW, RAWK>& kr,
+__device__ __forceinline__ void commit_tile(Pending& pd, float* pkey, float* rvx, const PathKeys<NW, RAWK>& kr,
                                             const PathVals<NW, RVN>& pv, int wave, int lane,
-                                            f32x4 (&s0r)[Waves<NW>::TT][8]) {
+                                            f32x4 (&s0r)[Waves<NW>::TT][8], const uint32_t* walk, int bound) {
   constexpr int TT = Waves<NW>::TT;
   const int n16 = lane & 15, g4 = lane >> 4;
   stage_pending_keys<NW, RAWK, RVN>(pkey, rvx, kr, wave, lane);
   __syncthreads();
+  if (walk && !pending_walk_ok(pd, lane, walk, bound)) {  // uniform
+    pd.last = -1;
+    pd.vmask = 0;
+  }
   if constexpr (LINES) state_to_mfma<NW>(s0r, lane);
   float gp[4], vnr[4][TT];
   if constexpr (RVN) {
@@ -1079,24 +1143,33 @@ __device__ __forceinline__ void item_heads(const dft_verify_args& p, int id, Ite
 // kernel's own class: record q from the front (class 0) or from the back
 // (class 1), read with the class counts in one pair of independent loads;
 // q past the class's count exits (those blocks come last in the grid).
+// Records whose header names another n_nodes or batch than the launch's are
+// ignored (block q then takes request q, as without records).
 template <int NP>
 __device__ __forceinline__ bool item_rows(const dft_verify_args& p, Item& it, int n_lo, int n_hi, int cls) {
   int span;
+  bool rec = false;
   if (cls >= 0) {
     const int4* ord = reinterpret_cast<const int4*>(p.size_order);
     const int q = it.b;
     const int4 hd = ord[0];
     const int4 e = ord[1 + (cls == 0 ? q : p.batch - 1 - q)];
-    if (q >= (cls == 0 ? hd.x : hd.y)) return false;
-    it.b = e.x;
-    it.row0 = e.y;
-    span = e.z;
-  } else if (p.cu_seqlens) {
-    it.row0 = p.cu_seqlens[it.b];
-    span = p.cu_seqlens[it.b + 1] - p.cu_seqlens[it.b];
-  } else {
-    it.row0 = (int64_t)it.b * p.n_nodes;
-    span = p.n_nodes;
+    rec = hd.z == p.n_nodes && hd.w == p.batch;  // uniform
+    if (rec) {
+      if (q >= (cls == 0 ? hd.x : hd.y)) return false;
+      it.b = e.x;
+      it.row0 = e.y;
+      span = e.z;
+    }
+  }
+  if (!rec) {
+    if (p.cu_seqlens) {
+      it.row0 = p.cu_seqlens[it.b];
+      span = p.cu_seqlens[it.b + 1] - p.cu_seqlens[it.b];
+    } else {
+      it.row0 = (int64_t)it.b * p.n_nodes;
+      span = p.n_nodes;
+    }
   }
   it.span_bad = span < 0 || span > p.n_nodes;
   it.n = span < 0 ? 0 : (span > p.n_nodes ? p.n_nodes : span);
@@ -1741,10 +1814,12 @@ __device__ __forceinline__ void phase_stores(const VerifyParams& P, const Item& 
 
 // The fused kernel's status word (wave 0 of the request's head-0
 // workgroup), written at the end of the workgroup from this lane's pending
-// path entry word (still in gate row 4 of LDS there) and the arguments
-// re-read from the kernel-argument segment.  Evaluated early and held
-// through the state stream, the flags cost the kernel a spilled register.
-__device__ __forceinline__ void fused_status(const Item& it, int lane, uint32_t path_word) {
+// path entry word (still in gate row 4 of LDS there), the entries' ancestry
+// rows (walk, where issue_walk_dma copied them; nothing is read from it when
+// nothing was pending) and the arguments re-read from the kernel-argument
+// segment.  Evaluated early and held through the state stream, the flags
+// cost the kernel a spilled register.
+__device__ __forceinline__ void fused_status(const Item& it, int lane, uint32_t path_word, const uint32_t* walk) {
   typedef const __attribute__((address_space(4))) VerifyParams* KParams;
   KParams kp = (KParams)__builtin_amdgcn_kernarg_segment_ptr();
   asm volatile("" : "+s"(kp));
@@ -1758,7 +1833,10 @@ __device__ __forceinline__ void fused_status(const Item& it, int lane, uint32_t 
   // no slot of its own: nothing is committed, as in the commit itself
   if (kp->a.state_indices && ld_i(kp->a.state_indices, b, kp->a.state_indices_dtype) < 0) ph.len = 0;
   const Pending pd = decode_pending(ph, lane, path_word);
-  if (lane == 0) status[b] = (span < 0 || span > nn ? DFT_STATUS_SPAN : 0) | (pd.bad ? DFT_STATUS_PATH : 0);
+  const bool walk_bad = kp->c.prev_anc_bits && pd.last >= 0 && !pending_walk_ok(pd, lane, walk, ph.bound);
+  if (lane == 0)
+    status[b] = (span < 0 || span > nn ? DFT_STATUS_SPAN : 0) | (pd.bad ? DFT_STATUS_PATH : 0) |
+                (walk_bad ? DFT_STATUS_WALK : 0);
 }
 
 // The body of the one-head-per-workgroup kernels (COMMIT: the fused commit ->
@@ -1805,17 +1883,23 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
     if (it.no_slot) ph.len = 0;  // no slot of its own: nothing is committed
     if (it.n == 0) {  // nothing to verify this step: the commit alone
       const uint32_t word = *path_word(P.c, it.b, lane);
-      const Pending pd = decode_pending(ph, lane, word);
-      if (it.h == 0 && wave == 0) fused_status(it, lane, word);
-      if (pd.last < 0) return;
-      f32x4 s0r[TT][8];
-      PathKeys<NW, RAWK> kr;
-      PathVals<NW, RVN> pv;
-      issue_state<true, kEarly, NW>(S0, p.state_v_stride, wave, lane, s0r);
-      issue_pending<NW, RAWK, RVN>(P.c, pd, it.h, wave, lane, S0, kr, pv);
-      commit_tile<NW, kEarly, RAWK, RVN>(pd, sm.pkey(), rvx, kr, pv, wave, lane, s0r);
-      __syncthreads();  // every wave has read the staged keys: am + x take the write-back staging
-      store_state<NW>(const_cast<float*>(S0), p.state_v_stride, wave, lane, s0r, sm.amx + wave * 512);
+      Pending pd = decode_pending(ph, lane, word);
+      uint32_t* walk = sm.graw[4];
+      if (pd.last >= 0) {  // uniform (one request)
+        f32x4 s0r[TT][8];
+        PathKeys<NW, RAWK> kr;
+        PathVals<NW, RVN> pv;
+        // (the ancestry rows go first: the keys the commit waits for land behind them)
+        issue_walk_dma<false>(P.c, pd, wave, lane, S0, walk);
+        issue_state<true, kEarly, NW>(S0, p.state_v_stride, wave, lane, s0r);
+        issue_pending<NW, RAWK, RVN>(P.c, pd, it.h, wave, lane, S0, kr, pv);
+        commit_tile<NW, kEarly, RAWK, RVN>(pd, sm.pkey(), rvx, kr, pv, wave, lane, s0r,
+                                           P.c.prev_anc_bits ? walk : nullptr, ph.bound);
+        __syncthreads();  // every wave has read the staged keys: am + x take the write-back staging
+        if (pd.last >= 0)  // uniform: a path that is not a walk was dropped
+          store_state<NW>(const_cast<float*>(S0), p.state_v_stride, wave, lane, s0r, sm.amx + wave * 512);
+      }
+      if (it.h == 0 && wave == 0) fused_status(it, lane, word, walk);
       return;
     }
   }
@@ -1847,10 +1931,13 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
   if constexpr (COMMIT && !kEarly) {
     pd = decode_pending(ph, lane, pword);
     issue_pending<NW, RAWK, RVN>(P.c, pd, it.h, wave, lane, S0, kr, pv);
+    issue_walk_dma<false>(P.c, pd, wave, lane, S0, sm.graw[4]);  // (lands before the state, as the gates)
   }
-  if constexpr (kPathDma)
-    issue_path_dma<NW>(P.c, decode_pending(ph, lane, pword), it.h, wave, lane, S0,
-                       reinterpret_cast<uint16_t*>(sm.vrows()), rvx);
+  if constexpr (kPathDma) {
+    const Pending pd0 = decode_pending(ph, lane, pword);
+    issue_path_dma<NW>(P.c, pd0, it.h, wave, lane, S0, reinterpret_cast<uint16_t*>(sm.vrows()), rvx);
+    issue_walk_dma<false>(P.c, pd0, wave, lane, S0, sm.graw[4]);
+  }
   asm volatile("" ::: "memory");
 
   f32x4 s0r[TT][8];
@@ -1898,7 +1985,8 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
   phase_norms<NP, NW>(p, tid, sm, sm);
   __syncthreads();
   if constexpr (COMMIT && !kEarly) {
-    commit_tile<NW, false, RAWK, RVN>(pd, sm.pkey(), rvx, kr, pv, wave, lane, s0r);
+    commit_tile<NW, false, RAWK, RVN>(pd, sm.pkey(), rvx, kr, pv, wave, lane, s0r,
+                                      P.c.prev_anc_bits ? sm.graw[4] : nullptr, ph.bound);
     // everything this wave loaded has been consumed: no load is left in
     // flight past the (conditional) write-back
     __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 15));
@@ -1920,7 +2008,10 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
     // column per lane) are done, and stream in under the rest of phase 1
     // (65.4 -> 65.0 us at batch 64; issued before the solves they spilled).
     pd = decode_pending(ph, lane, sm.graw[4][lane & 15]);
-    if constexpr (!kPathDma) issue_pending<NW, RAWK, RVN>(P.c, pd, it.h, wave, lane, S0, kr, pv);
+    if constexpr (!kPathDma) {
+      issue_walk_dma<true>(P.c, pd, wave, lane, S0, sm.graw[4]);  // ahead of the path loads that cover it
+      issue_pending<NW, RAWK, RVN>(P.c, pd, it.h, wave, lane, S0, kr, pv);
+    }
   }
   if constexpr (kSplit) issue_state_group<false, false, NW>(S0, p.state_v_stride, wave, lane, 2, s0r);
   __syncthreads();
@@ -1939,12 +2030,14 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
     // phase 1
     if constexpr (!RVN) {
       pd = decode_pending(ph, lane, sm.graw[4][lane & 15]);
+      issue_walk_dma<true>(P.c, pd, wave, lane, S0, sm.graw[4]);
       issue_pending<NW, RAWK, RVN>(P.c, pd, it.h, wave, lane, S0, kr, pv);
     }
     float* stage = reinterpret_cast<float*>(sm.vrows());  // 8 KiB: the 16 path keys, then the write-back
     if constexpr (kPathDma)
       path_from_lds<NW>(P.c, pd, it.h, wave, lane, reinterpret_cast<const uint16_t*>(stage), rvx, kr, pv);
-    commit_tile<NW, true, RAWK, RVN, kPathDma>(pd, stage, rvx, kr, pv, wave, lane, s0r);
+    commit_tile<NW, true, RAWK, RVN, kPathDma>(pd, stage, rvx, kr, pv, wave, lane, s0r,
+                                               P.c.prev_anc_bits ? sm.graw[4] : nullptr, ph.bound);
     __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 15));
     if (pd.last >= 0) {  // uniform over the workgroup (one request)
       __syncthreads();  // every wave has read the staged keys
@@ -1989,7 +2082,7 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
     phase_stores<NP, COMMIT, NW>(P, it, tid_s, sm);
   }
   if constexpr (COMMIT)
-    if (it.h == 0 && wave == 0) fused_status(it, lane, sm.graw[4][lane & 15]);
+    if (it.h == 0 && wave == 0) fused_status(it, lane, sm.graw[4][lane & 15], sm.graw[4]);
 }
 
 // Both widths run at 4 waves per SIMD (at most 128 registers): the 32-wide
@@ -2058,7 +2151,7 @@ static void split_by_size(const dft_verify_args* a, const VerifyParams& P, Verif
 // requests; per chunk each wave counts its classes by ballot, and the block
 // adds the counts of the waves before it.  Class 0 (at most 32 nodes) fills
 // records 0, 1, .. and class 1 records batch - 1, batch - 2, .., both in
-// request order.
+// request order; the header holds the two counts, n_nodes and batch.
 __global__ void __launch_bounds__(1024) size_order_kernel(const int32_t* cu, int batch, int n_nodes, int4* order) {
   __shared__ int counts[16][2];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -2093,7 +2186,7 @@ __global__ void __launch_bounds__(1024) size_order_kernel(const int32_t* cu, int
     done_large += tot_l;
     __syncthreads();  // counts is rewritten by the next chunk
   }
-  if (tid == 0) order[0] = make_int4(done_small, done_large, 0, 0);
+  if (tid == 0) order[0] = make_int4(done_small, done_large, n_nodes, batch);
 }
 
 int launch_size_order(const int32_t* cu_seqlens, int batch, int n_nodes, int32_t* order, hipStream_t stream) {

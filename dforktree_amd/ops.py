@@ -14,6 +14,7 @@ fc1_branch64.py:13).
 from __future__ import annotations
 
 import ctypes as C
+import weakref
 from typing import Optional
 
 import torch
@@ -112,15 +113,26 @@ def tree_verify(y: torch.Tensor, a: torch.Tensor, b: torch.Tensor, A_log: Option
     return o
 
 
+# Which cu_seqlens each size-order record tensor was written from (host-side
+# bookkeeping: id of the records -> (weak reference to them, the cu_seqlens
+# tensor's data pointer and version counter, n_nodes, batch)).  A verify
+# given records of other cu_seqlens would take the wrong rows; the device
+# only sees the header's n_nodes and batch.
+_SIZE_ORDER_SOURCE = {}
+
+
 def size_order(cu_seqlens: torch.Tensor, n_nodes: int, out: Optional[torch.Tensor] = None) -> torch.Tensor:
     """The packed batch's requests by size class (``dft_size_order``):
     int32 [batch + 1, 4], row 0 = (requests of at most 32 nodes, the others,
-    0, 0), then one (request, first row, span, 0) record per request, the
-    small ones from the front and the others from the back.  Pass it as
-    ``size_order`` to every verify of the step.  ``out`` (int32, contiguous,
-    16-byte aligned, at least [batch + 1, 4]) avoids the allocation."""
+    n_nodes, batch), then one (request, first row, span, 0) record per
+    request, the small ones from the front and the others from the back.
+    Pass it as ``size_order`` to every verify of the step; the verify refuses
+    records written from another cu_seqlens tensor or before an in-place
+    change of it.  ``out`` (int32, contiguous, 16-byte aligned, at least
+    [batch + 1, 4]) avoids the allocation."""
     if cu_seqlens.dtype != torch.int32:
         raise TypeError("cu_seqlens must be int32")
+    source = (cu_seqlens.data_ptr(), cu_seqlens._version)
     cu_seqlens = cu_seqlens.contiguous()
     batch = cu_seqlens.numel() - 1
     dev = cu_seqlens.device
@@ -129,7 +141,26 @@ def size_order(cu_seqlens: torch.Tensor, n_nodes: int, out: Optional[torch.Tenso
     _check_size_order(out, batch, dev)
     check("dft_size_order", load().dft_size_order(cu_seqlens.data_ptr(), batch, int(n_nodes), out.data_ptr(),
                                                   _stream(dev)))
+    for k in [k for k, v in _SIZE_ORDER_SOURCE.items() if v[0]() is None]:
+        del _SIZE_ORDER_SOURCE[k]
+    _SIZE_ORDER_SOURCE[id(out)] = (weakref.ref(out), *source, int(n_nodes), batch)
     return out
+
+
+def _check_size_order_source(t, cu_seqlens, n_nodes, batch):
+    """Refuse records that ``size_order`` wrote for another batch.  Records
+    written by other means are not known here (the device then checks the
+    header's n_nodes and batch only)."""
+    ent = _SIZE_ORDER_SOURCE.get(id(t))
+    if ent is None or ent[0]() is not t:
+        return
+    _, ptr, ver, nn, b = ent
+    if (nn, b) != (int(n_nodes), batch):
+        raise ValueError(f"size_order was written for n_nodes={nn}, batch={b}; this launch has "
+                         f"n_nodes={n_nodes}, batch={batch}")
+    if (ptr, ver) != (cu_seqlens.data_ptr(), cu_seqlens._version):
+        raise ValueError("size_order was written from another cu_seqlens (or before it was changed in place): "
+                         "call size_order(cu_seqlens, n_nodes) again for this batch")
 
 
 def _check_size_order(t, batch, dev):
@@ -170,6 +201,7 @@ def _verify_args(y, a, b, A_log, dt_bias, state, *, hk, hv, anc, anc_bits, batch
         # view would stay misaligned under .contiguous())
         pitch = -(-y.shape[1] // 8) * 8
         y = torch.empty(rows, pitch, device=y.device, dtype=y.dtype)[:, :y.shape[1]].copy_(y)
+    cu_given = cu_seqlens
     if cu_seqlens is not None:
         if batch is None:
             batch = cu_seqlens.numel() - 1
@@ -264,6 +296,7 @@ def _verify_args(y, a, b, A_log, dt_bias, state, *, hk, hv, anc, anc_bits, batch
         if cu_seqlens is None:
             raise ValueError("size_order goes with a packed batch (cu_seqlens)")
         _check_size_order(size_order, batch, dev)
+        _check_size_order_source(size_order, cu_given, n_nodes, batch)
         args.size_order = size_order.data_ptr()
     return args, o, dev, (y, cu_seqlens, anc, anc_bits, si)
 
@@ -285,7 +318,8 @@ def tree_commit_verify(y: torch.Tensor, a: torch.Tensor, b: torch.Tensor, A_log:
                        aux_k: Optional[torch.Tensor] = None, aux_v: Optional[torch.Tensor] = None,
                        aux_g: Optional[torch.Tensor] = None, aux_k_per_khead: bool = False,
                        status: Optional[torch.Tensor] = None,
-                       size_order: Optional[torch.Tensor] = None) -> torch.Tensor:
+                       size_order: Optional[torch.Tensor] = None,
+                       pending_anc_bits: Optional[torch.Tensor] = None) -> torch.Tensor:
     """``tree_verify`` with the previous step's accepted path committed into
     each request's state slot on the way in (one read of the state, one
     write back).  The pending_* tensors are the previous step's saves
@@ -305,7 +339,12 @@ def tree_commit_verify(y: torch.Tensor, a: torch.Tensor, b: torch.Tensor, A_log:
     verify read.  Previous rows of request b start at prev_cu_seqlens[b] or
     b * prev_n_nodes.  Returns o.  ``status`` and ``size_order`` as in
     ``tree_verify``; status adds DFT_STATUS_PATH for a pending entry past the
-    previous tree (the entry is ignored)."""
+    previous tree (the entry is ignored).  ``pending_anc_bits``: the previous
+    step's ancestry rows (``tree_struct(..., want=("anc_bits",))`` of that
+    step); with them a path whose valid entries are not a walk down from the
+    root is not committed, and its request gets DFT_STATUS_WALK.
+    With ``n_nodes=0`` (every request's tree empty) the launch only commits
+    the pending paths: the flush of requests that leave the batch."""
     args, o, dev, _keep = _verify_args(
         y, a, b, A_log, dt_bias, state, hk=hk, hv=hv, anc=anc, anc_bits=anc_bits, batch=batch, n_nodes=n_nodes,
         cu_seqlens=cu_seqlens, scale=scale, neg_exp_A=neg_exp_A, state_indices=state_indices,
@@ -366,6 +405,13 @@ def tree_commit_verify(y: torch.Tensor, a: torch.Tensor, b: torch.Tensor, A_log:
         c.prev_b, c.pb_row_stride = pending_b.data_ptr(), pending_b.stride(0)
         c.prev_b_dtype = _ftag(pending_b, "pending_b")
     c.gains, c.g_h_stride, c.g_row_stride = pending_gains.data_ptr(), *pending_gains.stride()
+    if pending_anc_bits is not None:
+        if pending_anc_bits.dtype != torch.int64:
+            raise TypeError("pending_anc_bits must be int64 (uint64 bit masks)")
+        if pending_anc_bits.device != dev:
+            raise ValueError(f"pending_anc_bits is on {pending_anc_bits.device}, the inputs on {dev}")
+        pending_anc_bits = pending_anc_bits.contiguous()
+        c.prev_anc_bits = pending_anc_bits.data_ptr()
     check("dft_tree_commit_verify", load().dft_tree_commit_verify(C.byref(args), C.byref(c), _stream(dev)))
     return o
 

@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define DFT_ABI_VERSION 4
+#define DFT_ABI_VERSION 5
 
 #if defined(__GNUC__)
 #define DFT_API __attribute__((visibility("default")))
@@ -69,7 +69,14 @@ enum dft_request_status {
   DFT_STATUS_SPAN = 1,
   /* a path entry (within its length) or a commit end names a node at or past
    * the size of its tree: that entry (or end) was ignored */
-  DFT_STATUS_PATH = 2
+  DFT_STATUS_PATH = 2,
+  /* (dft_tree_commit_verify with prev_anc_bits) the valid pending entries,
+   * in order, are not a walk down from the previous tree's root: some
+   * entry's ancestors-or-self are not exactly the valid entries up to it
+   * (an ancestor missing or out of order, a non-ancestor, a repeat).  The
+   * path was not committed: the slot keeps its state, and the verify ran on
+   * it. */
+  DFT_STATUS_WALK = 4
 };
 
 /* ---------------------------------------------------------------------------
@@ -159,13 +166,17 @@ typedef struct dft_verify_args {
 DFT_API int dft_tree_verify(const dft_verify_args* args, void* stream);
 
 /* Requests of a packed batch by size class, for dft_verify_args.size_order:
- * order[0..3] = {n_small, n_large, 0, 0}, then batch records of 4 int32
+ * order[0..3] = {n_small, n_large, n_nodes, batch}, then batch records of 4 int32
  * {request, cu_seqlens[request], span, 0}: the requests of at most 32 nodes
  * (the span clamped to [0, n_nodes]) from record 0 up in request order, the
  * others from record batch - 1 down in request order.  order holds
  * 4 * (batch + 1) int32; one workgroup, no allocation.  No counterpart in the
  * reference (its launches are per tree size, tree_kernels.py:193-208): for
  * callers of packed ragged batches, once per step and shared by all layers.
+ * A launch whose n_nodes or batch differs from the header's ignores the
+ * records (each kernel then takes the requests in block order, as without
+ * them); records written from other cu_seqlens of the same n_nodes and
+ * batch are not detected here.
  * DFT_ERR_INVALID for batch < 0, n_nodes outside 1..64 or a null pointer. */
 DFT_API int dft_size_order(const int32_t* cu_seqlens, int32_t batch, int32_t n_nodes, int32_t* order,
                            void* stream);
@@ -285,7 +296,11 @@ DFT_API int dft_tree_commit(const dft_commit_args* args, void* stream);
  * keys, values and gains), written back to the slot, and then used as S0 of
  * the verify that `verify` describes (same fields as dft_tree_verify; the
  * state must have k stride 1 and 16-byte aligned rows).  Requests without a
- * valid entry verify on S unchanged and write nothing back.
+ * valid entry verify on S unchanged and write nothing back.  A request with
+ * no rows this step (span 0, or n_nodes 0 for the whole launch) only
+ * commits: that is how a request leaving the batch (eviction, end of
+ * sequence) flushes its pending path when no saves exist.  With n_nodes 0
+ * the y, a, b, gate, ancestry and o fields are not read and may be NULL.
  * No counterpart in the reference: it fuses the commit that follows one
  * verify step into the next step's verify, so the state is read once per
  * layer and step instead of twice.  The previous step's keys / values / gains
@@ -343,6 +358,16 @@ typedef struct dft_pending_commit {
   const void* prev_b;
   int64_t pb_row_stride;
   int32_t prev_b_dtype;
+  /* DFT_ABI_VERSION 5 (appended).  Optional: the previous step's ancestry
+   * rows (row r of the previous step's buffers, bit j = node j of its tree
+   * is an ancestor-or-self, as dft_tree_struct writes them).  With them every
+   * request's valid pending entries are checked to be a walk down from the
+   * root (entry c's ancestors-or-self are exactly the valid entries 0..c, no
+   * repeats), as fc1_fused.py:41 checks ancestry on the device; a request
+   * that fails commits nothing and gets DFT_STATUS_WALK.  NULL: no check (a
+   * non-walk path is then committed as given, which is wrong for a state
+   * that persists). */
+  const uint64_t* prev_anc_bits;
 } dft_pending_commit;
 
 DFT_API int dft_tree_commit_verify(const dft_verify_args* verify, const dft_pending_commit* pending, void* stream);

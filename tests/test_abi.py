@@ -29,7 +29,7 @@ def test_library_exports_every_declared_symbol():
     out = subprocess.run(["nm", "-D", "--defined-only", str(_lib.LIB_PATH)], capture_output=True, text=True).stdout
     exported = {l.split()[-1] for l in out.splitlines() if " T " in l}
     assert exported == set(names), "only the C ABI is exported"
-    assert lib.dft_abi_version() == _lib.ABI_VERSION == 4
+    assert lib.dft_abi_version() == _lib.ABI_VERSION == 5
 
 
 @pytest.fixture(scope="module")
@@ -62,6 +62,9 @@ def test_ctypes_structs_match_c_layout(c_layouts):
     # the status words, then the size-order records, were appended: every earlier field kept its offset
     assert [f for f, _ in _lib.VerifyArgs._fields_[-2:]] == ["status", "size_order"]
     assert _lib.CommitArgs._fields_[-1][0] == "status"
+    # ABI 5 appended the previous step's ancestry rows (the walk check) to the pending commit
+    assert _lib.PendingArgs._fields_[-1][0] == "prev_anc_bits"
+    assert _lib.PendingArgs._fields_[-4][0] == "prev_b"
     for cname, py in structs.items():
         assert ctypes.sizeof(py) == layout[f"{cname}.__size__"], cname
         for f, _ in py._fields_:
@@ -124,6 +127,18 @@ def test_validation_rejects_bad_descriptors_without_launching():
     assert lib.dft_tree_commit_verify(ctypes.byref(v), ctypes.byref(pc), None) == _lib.DFT_ERR_UNSUPPORTED
     v.batch = 0
     assert lib.dft_tree_commit_verify(ctypes.byref(v), ctypes.byref(pc), None) == _lib.DFT_OK  # empty: no-op
+    # n_nodes 0 with requests: the fused entry still commits (it needs the state and the pending path, not the
+    # rows), the plain verify has nothing to do
+    v.batch, v.n_nodes, v.state_k_stride, v.state_v_stride = 1, 0, 1, 128
+    v.y = v.a = v.b = v.o = v.anc_bits = None
+    assert lib.dft_tree_verify(ctypes.byref(v), None) == _lib.DFT_OK
+    v.state = None
+    assert lib.dft_tree_commit_verify(ctypes.byref(v), ctypes.byref(pc), None) == _lib.DFT_ERR_INVALID  # no state
+    v.state = 16
+    pc.path = None
+    assert lib.dft_tree_commit_verify(ctypes.byref(v), ctypes.byref(pc), None) == _lib.DFT_ERR_INVALID  # no path
+    pc.path, v.state_k_stride, v.state_v_stride = 16, 128, 1
+    assert lib.dft_tree_commit_verify(ctypes.byref(v), ctypes.byref(pc), None) == _lib.DFT_ERR_UNSUPPORTED
     c = _lib.CommitArgs()
     c.n_layers, c.batch, c.hv, c.dk, c.dv, c.n_nodes, c.path_cols, c.n_ends, c.k_head_div = 1, 1, 4, 128, 128, 32, 16, 3, 1
     assert lib.dft_tree_commit(ctypes.byref(c), None) == _lib.DFT_ERR_INVALID       # n_ends

@@ -144,7 +144,7 @@ def test_verify_split_order_empty_requests_and_slots(cuda):
 
 def size_order_records(cu, n_nodes):
     """The records dft_size_order writes, restated on the host: the counts,
-    then (request, first row, span, 0) for the requests of at most 32 nodes
+    n_nodes and batch, then (request, first row, span, 0) for the requests of at most 32 nodes
     (span clamped to [0, n_nodes]) from the front and the others from the
     back, each class in request order."""
     B = len(cu) - 1
@@ -156,7 +156,7 @@ def size_order_records(cu, n_nodes):
         recs[j] = [r, cu[r], cu[r + 1] - cu[r], 0]
     for j, r in enumerate(large):
         recs[B - 1 - j] = [r, cu[r], cu[r + 1] - cu[r], 0]
-    return [[len(small), len(large), 0, 0]] + recs
+    return [[len(small), len(large), n_nodes, B]] + recs
 
 
 def test_verify_size_order(cuda):
