@@ -348,13 +348,33 @@ __device__ __forceinline__ void lds_f32x8_split(const float* row, int c0, float 
 }
 
 // Forward substitution on one 16x16 unit-lower block: x <- (I + A_bb)^-1 e_j.
-template <int LDA>
+// Step m reads row m of at (A's column m) from column m + 1 on; the rows are
+// 16-byte aligned (LDA and base multiples of 4), so a step's values come as
+// whole 16-byte reads (from the chunk holding column m + 1), issued kAhead
+// steps before their use.  Read element by element, each step's values came
+// as 4- and 8-byte reads, each followed by a wait: at batch 1 the block took
+// about 1.2 us of a workgroup's 10.  kAhead: rows in flight (the fused
+// kernels, which hold their whole state tile here, take 1: more spilled).
+template <int LDA, int kAhead>
 __device__ __forceinline__ void solve_block16(float (&x)[16], const float* at, int base) {
+  static_assert(LDA % 4 == 0, "16-byte aligned rows");
+  f32x4 rows[kAhead][4];
+  auto fetch = [&](int m, f32x4 (&r)[4]) {
+    const f32x4* row = reinterpret_cast<const f32x4*>(at + (base + m) * LDA + base);
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+      if (4 * c + 3 > m) r[c] = row[c];  // the chunks holding columns m + 1 .. 15
+  };
+#pragma unroll
+  for (int m = 0; m < kAhead; ++m) fetch(m, rows[m]);
 #pragma unroll
   for (int m = 0; m < 15; ++m) {
+    f32x4 (&r)[4] = rows[m % kAhead];
     const float xm = x[m];
 #pragma unroll
-    for (int i = m + 1; i < 16; ++i) x[i] -= at[(base + m) * LDA + base + i] * xm;
+    for (int i = m + 1; i < 16; ++i) x[i] -= r[i >> 2][i & 3] * xm;
+    if (m + kAhead < 15) fetch(m + kAhead, r);
+    __builtin_amdgcn_sched_barrier(0);  // (no read is hoisted further ahead)
   }
 }
 
@@ -1186,23 +1206,24 @@ __device__ __forceinline__ bool item_rows(const dft_verify_args& p, Item& it, in
 }
 
 // Wave 0's lane i fetches node i's gate words and ancestry bits into graw
-// (rows past the tree repeat the last node).  The words are whole aligned
-// 32-bit words, decoded later, so nothing waits on them before the state is
-// issued.  `alt` replaces every source when the request has no rows.
+// (rows past the tree repeat the last node; the request has rows).  The
+// words are whole aligned 32-bit words, decoded later, so nothing waits on
+// them before the state is issued.  No address depends on the state slot:
+// at batch 1 the copies then go out while the slot index is still loading.
 //
 // Row 4 carries dt_bias (a per-head word, read from lane kDtLane) on every
 // lane unless `path` is given: then lanes 0-15 fetch the words of the
 // pending path entries instead (the fused commit reads them from there).
 constexpr int kDtLane = 63;
-__device__ __forceinline__ void issue_gates(const dft_verify_args& p, const Item& it, int lane, const void* alt,
+__device__ __forceinline__ void issue_gates(const dft_verify_args& p, const Item& it, int lane,
                                             uint32_t (*graw)[64], const void* path = nullptr) {
   uint32_t sh;
   const int64_t gi = it.row0 + (lane < it.n ? lane : it.n - 1);
-  const bool ok = it.n > 0;
-  lds_dma4(ok ? word_of(p.a, gi * p.a_row_stride + it.h, p.a_dtype, sh) : alt, graw[0]);
-  lds_dma4(ok ? word_of(p.b, gi * p.b_row_stride + it.h, p.b_dtype, sh) : alt, graw[1]);
-  const uint32_t* bits = (ok && p.anc_bits) ? reinterpret_cast<const uint32_t*>(p.anc_bits + gi)
-                                            : static_cast<const uint32_t*>(alt);
+  lds_dma4(word_of(p.a, gi * p.a_row_stride + it.h, p.a_dtype, sh), graw[0]);
+  lds_dma4(word_of(p.b, gi * p.b_row_stride + it.h, p.b_dtype, sh), graw[1]);
+  // (dense ancestry: the words are not read, any valid source will do)
+  const uint32_t* bits = p.anc_bits ? reinterpret_cast<const uint32_t*>(p.anc_bits + gi)
+                                    : static_cast<const uint32_t*>(p.y);
   lds_dma4(bits, graw[2]);
   lds_dma4(bits + 1, graw[3]);
   const uint32_t* dt = word_of(p.dt_bias, it.h, p.dt_bias_dtype, sh);
@@ -1254,10 +1275,9 @@ __device__ __forceinline__ void dense_ancestry(const dft_verify_args& p, const I
 }
 
 // q/k/v rows -> LDS: one 1 KiB copy fills 4 swizzled rows (NP/(4 NW) per wave
-// and plane).  Planes M0 .. M1-1 of (q, k, v).
+// and plane).  Planes M0 .. M1-1 of (q, k, v).  The request has rows.
 template <int NP, int M0, int M1, int NW, class RW>
-__device__ __forceinline__ void issue_rows(const dft_verify_args& p, const Item& it, int wave, int lane,
-                                           const void* alt, RW& rw) {
+__device__ __forceinline__ void issue_rows(const dft_verify_args& p, const Item& it, int wave, int lane, RW& rw) {
   const int KD = p.hk * kD;
   const int64_t ys = p.y_row_stride;
   const uint16_t* ybase = reinterpret_cast<const uint16_t*>(p.y) + it.row0 * ys;
@@ -1275,7 +1295,7 @@ __device__ __forceinline__ void issue_rows(const dft_verify_args& p, const Item&
       // q and k rows are read again by the k-head's other v-heads (same XCD,
       // same L2); each v row is read once.  Non-temporal v copies measured
       // 1.2% faster at batch 64; non-temporal q/k copies gained nothing.
-      const void* src = it.n > 0 ? static_cast<const void*>(srcs[m] + goff) : alt;
+      const void* src = srcs[m] + goff;
       if (m == 2 && M0 == 2)  // the late v rows, copied alone while Ck computes
         lds_dma16_nt_untracked(src, dsts[m] + 4 * blk * kD);
       else if (m == 2)
@@ -1346,15 +1366,18 @@ __device__ __forceinline__ void phase_norms(const dft_verify_args& p, int tid, c
 
 // The saves for the commit: normalised keys (once per k-head when saved per
 // k-head) and G.  Needs the norms and G; reads the k rows.
-template <int NP, bool LATE, int NW, class RW, class WK>
+// CS: the workgroups of a column split share the saves, each writing key
+// columns col0 .. col0 + 128 / CS - 1 (the first one writes G).
+template <int NP, bool LATE, int NW, class RW, class WK, int CS = 1>
 __device__ __forceinline__ void phase_saves(const VerifyParams& P, const Item& it, int tid, const RW& rw,
-                                            const WK& wk) {
+                                            const WK& wk, int col0 = 0) {
+  constexpr int KQ = 32 / CS;  // 4-column pieces of a key row per workgroup
   const OutArgs p = out_args<LATE>(P);
   const bool per_khead = (p.flags & DFT_VERIFY_AUX_K_PER_KHEAD) != 0;
   if (p.aux_k && (!per_khead || it.rr == 0)) {
     float* dk = p.aux_k + (int64_t)(per_khead ? it.hk : it.h) * p.aux_k_h_stride + it.row0 * p.aux_k_row_stride;
-    for (int c = tid; c < it.n * 32; c += Waves<NW>::NT) {
-      const int i = c >> 5, d = (c & 31) * 4;
+    for (int c = tid; c < it.n * KQ; c += Waves<NW>::NT) {
+      const int i = c / KQ, d = col0 + (c % KQ) * 4;
       const uint2 u = *reinterpret_cast<const uint2*>(&rw.k[qkv_at(i, d)]);
       const float r = wk.rk[i];
       const f32x4 val = {__uint_as_float(u.x << 16) * r, __uint_as_float(u.x & 0xffff0000u) * r,
@@ -1368,7 +1391,7 @@ __device__ __forceinline__ void phase_saves(const VerifyParams& P, const Item& i
       }
     }
   }
-  if (p.aux_g && tid < it.n)
+  if (p.aux_g && col0 == 0 && tid < it.n)
     p.aux_g[(int64_t)it.h * p.aux_g_h_stride + (it.row0 + tid) * p.aux_g_row_stride] = wk.G[tid];
 }
 
@@ -1412,8 +1435,9 @@ __device__ __forceinline__ void a_tile(const RW& rw, WK& wk, int ti, int tj, int
   *reinterpret_cast<f32x4*>(&wk.am()[j * LDA + i0]) = out;
 }
 
-// mtn: 16-row tiles that hold nodes (the rest are padding and are skipped)
-template <int NP, int NW, class RW, class WK>
+// mtn: 16-row tiles that hold nodes (the rest are padding and are skipped);
+// KA: rows in flight in the diagonal solves
+template <int NP, int NW, int KA, class RW, class WK>
 __device__ __forceinline__ void phase_gram_diag(int tid, const RW& rw, WK& wk, int mtn) {
   constexpr int MT = NP / 16;
   constexpr int LDA = WK::LDA;
@@ -1430,7 +1454,7 @@ __device__ __forceinline__ void phase_gram_diag(int tid, const RW& rw, WK& wk, i
       float xc[16];
 #pragma unroll
       for (int i = 0; i < 16; ++i) xc[i] = (i == j) ? 1.f : 0.f;
-      solve_block16<LDA>(xc, wk.am(), 16 * bb);
+      solve_block16<LDA, KA>(xc, wk.am(), 16 * bb);
       materialize16(xc);
 #pragma unroll
       for (int i = 0; i < 16; ++i) wk.x()[(16 * bb + i) * LDA + 16 * bb + j] = xc[i];
@@ -1639,11 +1663,14 @@ __device__ __forceinline__ void phase_cq_ck(int lane, const RW& rw, const f32x4 
 
 // 3a: W = beta (v - e^G rk Ck) in the accumulator layout, split into bf16
 // hi/lo B operands: k-step ks, lane group g, element e -> node 32ks + 4g + e
-// (e < 4), 32ks + 16 + 4g + e-4, i.e. registers of tiles 2ks, 2ks+1
+// (e < 4), 32ks + 16 + 4g + e-4, i.e. registers of tiles 2ks, 2ks+1.
+// NW here counts column waves (waves x column split); col0: the workgroup's
+// first value column.
 template <int NP, int NW, class RW, class WK>
 __device__ __forceinline__ void phase_w(int lane, int wave, const RW& rw, const WK& wk,
                                         const f32x4 (&ck)[NP / 16][Waves<NW>::TT],
-                                        bf16x8 (&wh)[NP / 32][Waves<NW>::TT], bf16x8 (&wl)[NP / 32][Waves<NW>::TT]) {
+                                        bf16x8 (&wh)[NP / 32][Waves<NW>::TT], bf16x8 (&wl)[NP / 32][Waves<NW>::TT],
+                                        int col0 = 0) {
   constexpr int TT = Waves<NW>::TT, CW = Waves<NW>::CW;
   constexpr int KS = NP / 32;
   const int n16 = lane & 15, g4 = lane >> 4;
@@ -1658,7 +1685,7 @@ __device__ __forceinline__ void phase_w(int lane, int wave, const RW& rw, const 
     }
 #pragma unroll
     for (int t = 0; t < TT; ++t) {
-      const int col = CW * wave + 16 * t + n16;
+      const int col = col0 + CW * wave + 16 * t + n16;
       float w8[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
@@ -1683,7 +1710,7 @@ template <int NP, int NW, class RW, class WK>
 __device__ __forceinline__ void phase_out(const VerifyParams& P, const Item& it, int lane, int wave, RW& rw,
                                           const WK& wk, const f32x4 (&cq)[NP / 16][Waves<NW>::TT],
                                           const bf16x8 (&wh)[NP / 32][Waves<NW>::TT],
-                                          const bf16x8 (&wl)[NP / 32][Waves<NW>::TT], int mtn) {
+                                          const bf16x8 (&wl)[NP / 32][Waves<NW>::TT], int mtn, int col0 = 0) {
   constexpr int TT = Waves<NW>::TT, CW = Waves<NW>::CW;
   constexpr int MT = NP / 16;
   constexpr int KS = NP / 32;
@@ -1719,7 +1746,7 @@ __device__ __forceinline__ void phase_out(const VerifyParams& P, const Item& it,
     const int i = 16 * mt + n16;
 #pragma unroll
     for (int t = 0; t < TT; ++t) {
-      const int col = CW * wave + 16 * t + 4 * g4;
+      const int col = col0 + CW * wave + 16 * t + 4 * g4;
       *reinterpret_cast<f32x4*>(&vn_s[vn_at(i, col)]) = acc[t];
       if (!P.vn_stage && p.aux_v && i < it.n) {
         float* dst = p.aux_v + (int64_t)it.h * p.aux_v_h_stride + (it.row0 + i) * p.aux_v_row_stride + col;
@@ -1740,7 +1767,7 @@ __device__ __forceinline__ void phase_out(const VerifyParams& P, const Item& it,
   for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
     for (int t = 0; t < TT; ++t) {
-      const int col = CW * wave + 16 * t + n16;
+      const int col = col0 + CW * wave + 16 * t + n16;
       const float* base = vn_s + 4 * g4 * kD + (col & 3);
       const int ch = ((col >> 2) ^ (4 * g4)) & 31;
       float v8[8];
@@ -1762,7 +1789,7 @@ __device__ __forceinline__ void phase_out(const VerifyParams& P, const Item& it,
     const int i = 16 * mt + n16;
 #pragma unroll
     for (int t = 0; t < TT; ++t) {
-      const int col = CW * wave + 16 * t + 4 * g4;
+      const int col = col0 + CW * wave + 16 * t + 4 * g4;
       const f32x4 ov = wk.cO[i] * cq[mt][t] + acc[t];
       if (P.o_stage) {
         const bf16x2 lo = __builtin_convertvector((f32x2{ov[0], ov[1]}), bf16x2);  // round to nearest even
@@ -1784,17 +1811,21 @@ __device__ __forceinline__ void phase_out(const VerifyParams& P, const Item& it,
 // the key saves) are written once and not read back by this launch: they go
 // out as non-temporal stores, which at batch 64 made the verify 6.6% and the
 // fused commit -> verify 3.1% faster than ordinary stores.
-template <int NP, bool LATE, int NW, class RW>
-__device__ __forceinline__ void phase_stores(const VerifyParams& P, const Item& it, int tid, const RW& rw) {
+// CS: value columns split over CS workgroups; this one stores columns col0 ..
+// col0 + 128 / CS - 1 of every row.
+template <int NP, bool LATE, int NW, class RW, int CS = 1>
+__device__ __forceinline__ void phase_stores(const VerifyParams& P, const Item& it, int tid, const RW& rw,
+                                             int col0 = 0) {
   constexpr int NT = Waves<NW>::NT;
+  constexpr int VQ = 32 / CS, OQ = 16 / CS;  // 16-byte pieces of a row per workgroup
   const OutArgs p = out_args<LATE>(P);
   const float* vn_s = reinterpret_cast<const float*>(rw.q);
   const uint16_t* o_s = rw.ostage();
   if (p.vn_stage) {  // rows of 32 x 16 bytes
     float* dst = p.aux_v + (int64_t)it.h * p.aux_v_h_stride + it.row0 * p.aux_v_row_stride;
 #pragma unroll
-    for (int u = 0; u < NP * 32 / NT; ++u) {
-      const int i = (NT / 32) * u + (tid >> 5), q = tid & 31;
+    for (int u = 0; u < NP * VQ / NT; ++u) {
+      const int i = (NT / VQ) * u + tid / VQ, q = col0 / 4 + tid % VQ;
       if (i < it.n)
         __builtin_nontemporal_store(*reinterpret_cast<const f32x4*>(&vn_s[vn_at(i, 4 * q)]),
                                     reinterpret_cast<f32x4*>(dst + i * p.aux_v_row_stride + 4 * q));
@@ -1803,8 +1834,8 @@ __device__ __forceinline__ void phase_stores(const VerifyParams& P, const Item& 
   if (p.o_stage) {  // rows of 16 x 16 bytes
     uint16_t* dst = static_cast<uint16_t*>(p.o) + it.row0 * p.o_row_stride + (int64_t)it.h * p.o_h_stride;
 #pragma unroll
-    for (int u = 0; u < NP * 16 / NT; ++u) {
-      const int i = (NT / 16) * u + (tid >> 4), q = tid & 15;
+    for (int u = 0; u < NP * OQ / NT; ++u) {
+      const int i = (NT / OQ) * u + tid / OQ, q = col0 / 8 + tid % OQ;
       if (i < it.n)
         __builtin_nontemporal_store(*reinterpret_cast<const u32x4*>(&o_s[qkv_at(i, 8 * q)]),
                                     reinterpret_cast<u32x4*>(dst + i * p.o_row_stride + 8 * q));
@@ -1841,11 +1872,16 @@ __device__ __forceinline__ void fused_status(const Item& it, int lane, uint32_t 
 
 // The body of the one-head-per-workgroup kernels (COMMIT: the fused commit ->
 // verify form).
-template <int NP, bool S0VEC, bool COMMIT, bool RAWK, bool RVN, bool PDMA = false>
+// CS (plain verify of up to 32 nodes): the item's value columns are split
+// over CS workgroups, CS items apart in the grid's last dimension; each
+// forms phase 1 in full and phases 2-3 on its 128 / CS columns.
+template <int NP, bool S0VEC, bool COMMIT, bool RAWK, bool RVN, bool PDMA = false, int CS = 1>
 __device__ __forceinline__ void verify_body(const VerifyParams& P) {
   constexpr int MT = NP / 16;
   constexpr int NW = WavesFor<NP>();
-  constexpr int TT = Waves<NW>::TT, CW = Waves<NW>::CW;
+  constexpr int NWC = NW * CS;  // column waves of the item (of all its workgroups)
+  constexpr int TT = Waves<NWC>::TT, CW = Waves<NWC>::CW;
+  static_assert(CS == 1 || (!COMMIT && NP <= 32), "the column split serves the plain 32-wide verify");
   // The 32-wide fused form runs phase 1 (which needs no state) before its
   // commit, under the state stream, and stages the commit's keys and
   // write-back in the v region, whose rows it copies in afterwards.
@@ -1869,14 +1905,23 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
   const int n16 = lane & 15, g4 = lane >> 4;
 
   Item it;
-  item_heads(p, blockIdx.x, it);
+  int col0 = 0;  // the workgroup's first value column
+  if constexpr (CS > 1) {
+    const int items = p.batch * p.hv;
+    const int sp = blockIdx.x / items;  // (uniform)
+    col0 = sp * (kD / CS);
+    item_heads(p, blockIdx.x - sp * items, it);
+  } else {
+    item_heads(p, blockIdx.x, it);
+  }
   if (!item_rows<NP>(p, it, P.n_lo, P.n_hi, P.cls)) return;
   // Thread 0 of the request's head-0 workgroup writes its status word (the
   // condition is evaluated where it is written: held from here, it would
   // cost the fused kernel a register through the state stream).
   if constexpr (!COMMIT)
-    if (p.status && it.h == 0 && tid == 0) p.status[it.b] = it.span_bad ? DFT_STATUS_SPAN : 0;
-  const float* S0 = it.S0;
+    if (p.status && it.h == 0 && col0 == 0 && tid == 0) p.status[it.b] = it.span_bad ? DFT_STATUS_SPAN : 0;
+  // (the state rows of the workgroup's columns: v is the row index)
+  const float* S0 = CS > 1 ? it.S0 + (int64_t)col0 * p.state_v_stride : it.S0;
   PendingHead ph{};
   if constexpr (COMMIT) {
     ph = pending_head(&P.c, it.b);
@@ -1925,9 +1970,9 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
     pword = *path_word(P.c, it.b, lane);
     asm volatile("" ::: "memory");
   }
-  if (wave == 0) issue_gates(p, it, lane, S0, sm.graw, COMMIT ? path_word(P.c, it.b, lane) : nullptr);
+  if (wave == 0) issue_gates(p, it, lane, sm.graw, COMMIT ? path_word(P.c, it.b, lane) : nullptr);
   if (p.anc_f32) dense_ancestry<NP, NW>(p, it, wave, lane, sm);
-  issue_rows<NP, 0, kPlanes, NW>(p, it, wave, lane, S0, sm);
+  issue_rows<NP, 0, kPlanes, NW>(p, it, wave, lane, sm);
   if constexpr (COMMIT && !kEarly) {
     pd = decode_pending(ph, lane, pword);
     issue_pending<NW, RAWK, RVN>(P.c, pd, it.h, wave, lane, S0, kr, pv);
@@ -1948,9 +1993,9 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
   // commit before phase 1 and issues it at once.
   constexpr bool kSplit = S0VEC && !COMMIT;
   if (kSplit) {
-    issue_state_group<false, false, NW>(S0, p.state_v_stride, wave, lane, 0, s0r);
+    issue_state_group<false, false, NWC>(S0, p.state_v_stride, wave, lane, 0, s0r);
   } else if (S0VEC) {
-    issue_state<COMMIT, kEarly, NW>(S0, p.state_v_stride, wave, lane, s0r);
+    issue_state<COMMIT, kEarly, NWC>(S0, p.state_v_stride, wave, lane, s0r);
   } else {
 #pragma unroll
     for (int t = 0; t < TT; ++t)
@@ -1996,12 +2041,13 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
     }
     __syncthreads();  // am and x take the Gram tiles and X
   }
-  if constexpr (kSplit) issue_state_group<false, false, NW>(S0, p.state_v_stride, wave, lane, 1, s0r);
+  if constexpr (kSplit) issue_state_group<false, false, NWC>(S0, p.state_v_stride, wave, lane, 1, s0r);
   // (the 32-wide fused form saves after Cq/Ck: at this point its tile is
   // still streaming in, and the saves' stores would wait on the full queue)
-  if constexpr (!kEarly) phase_saves<NP, COMMIT, NW>(P, it, tid, sm, sm);
+  if constexpr (!kEarly) phase_saves<NP, COMMIT, NW, VerifySmem<NP>, VerifySmem<NP>, CS>(P, it, tid, sm, sm, col0);
   const int mtn = (it.n + 15) >> 4;  // uniform over the workgroup
-  phase_gram_diag<NP, NW>(tid, sm, sm, mtn);
+  // (the plain verify with a vector state has registers for 3 rows ahead)
+  phase_gram_diag<NP, NW, (!COMMIT && S0VEC) ? 3 : 1>(tid, sm, sm, mtn);
   if constexpr (kEarly && RVN) {
     // The recompute forms hold few registers for the path (raw rows, 10 per
     // lane): their loads go out here, once the diagonal solves (a 32-float
@@ -2013,7 +2059,7 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
       issue_pending<NW, RAWK, RVN>(P.c, pd, it.h, wave, lane, S0, kr, pv);
     }
   }
-  if constexpr (kSplit) issue_state_group<false, false, NW>(S0, p.state_v_stride, wave, lane, 2, s0r);
+  if constexpr (kSplit) issue_state_group<false, false, NWC>(S0, p.state_v_stride, wave, lane, 2, s0r);
   __syncthreads();
 #pragma unroll
   for (int d = 1; d < MT; ++d) {
@@ -2021,7 +2067,7 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
     phase_offdiag<NP, NW>(tid, d, sm, mtn);
     __syncthreads();
   }
-  if constexpr (kSplit) issue_state_group<false, false, NW>(S0, p.state_v_stride, wave, lane, 3, s0r);
+  if constexpr (kSplit) issue_state_group<false, false, NWC>(S0, p.state_v_stride, wave, lane, 3, s0r);
   phase_pq<NP, NW>(tid, sm, sm, mtn);
   phase_split_x<NP, NW>(tid, sm, mtn);
   if constexpr (kEarly) {
@@ -2048,7 +2094,7 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
     // with the q/k copies at the start, they would be held through the commit)
     int lane_v = lane;
     asm volatile("" : "+v"(lane_v));
-    issue_rows<NP, 2, 3, NW>(p, it, wave, lane_v, S0, sm);
+    issue_rows<NP, 2, 3, NW>(p, it, wave, lane_v, sm);
   }
 
   f32x4 cq[MT][TT], ck[MT][TT];
@@ -2056,30 +2102,30 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
     // Cq first; once every wave is done with the q rows, the v rows are
     // copied into their region while Ck computes
     bf16x8 sh[4][TT], sl[4][TT];  // the state split once, for both passes
-    phase_cq_ck<NP, 1, NW, 1>(lane, sm, s0r, cq, ck, mtn, sh, sl);
+    phase_cq_ck<NP, 1, NWC, 1>(lane, sm, s0r, cq, ck, mtn, sh, sl);
     __syncthreads();  // X and Pq complete, the q rows consumed
-    issue_rows<NP, 2, 3, NW>(p, it, wave, lane, S0, sm);
-    phase_cq_ck<NP, 2, NW, 2>(lane, sm, s0r, cq, ck, mtn, sh, sl);
+    issue_rows<NP, 2, 3, NW>(p, it, wave, lane, sm);
+    phase_cq_ck<NP, 2, NWC, 2>(lane, sm, s0r, cq, ck, mtn, sh, sl);
     __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 15));  // the v row copies (untracked by the backend)
     __syncthreads();
   } else {
     bf16x8 sh[4][TT], sl[4][TT];  // (unused: one pass)
-    phase_cq_ck<NP, 3, NW, 0>(lane, sm, s0r, cq, ck, mtn, sh, sl);
+    phase_cq_ck<NP, 3, NWC, 0>(lane, sm, s0r, cq, ck, mtn, sh, sl);
     if constexpr (kEarly) __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 15));  // the v row copies (untracked)
     __syncthreads();  // X and Pq complete
   }
   if constexpr (kEarly) phase_saves<NP, COMMIT, NW>(P, it, tid, sm, sm);  // the k rows are intact until phase 3
   bf16x8 wh[NP / 32][TT], wl[NP / 32][TT];
-  phase_w<NP, NW>(lane, wave, sm, sm, ck, wh, wl);
+  phase_w<NP, NWC>(lane, wave, sm, sm, ck, wh, wl, col0);
   __syncthreads();  // every wave has read its v rows: the q/k/v region takes the outputs
-  phase_out<NP, NW>(P, it, lane, wave, sm, sm, cq, wh, wl, mtn);
+  phase_out<NP, NWC>(P, it, lane, wave, sm, sm, cq, wh, wl, mtn, col0);
   if (P.vn_stage || P.o_stage) {
     __syncthreads();
     // fused form: an opaque thread id, so that the store offsets are
     // recomputed here instead of held (and spilled) from phase 1
     int tid_s = tid;
     if constexpr (COMMIT) asm volatile("" : "+v"(tid_s));
-    phase_stores<NP, COMMIT, NW>(P, it, tid_s, sm);
+    phase_stores<NP, COMMIT, NW, VerifySmem<NP>, CS>(P, it, tid_s, sm, col0);
   }
   if constexpr (COMMIT)
     if (it.h == 0 && wave == 0) fused_status(it, lane, sm.graw[4][lane & 15], sm.graw[4]);
@@ -2088,10 +2134,10 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
 // Both widths run at 4 waves per SIMD (at most 128 registers): the 32-wide
 // kernel as 4 workgroups of 4 waves per CU, the 64-wide one as 2 of 8 waves
 // (its LDS holds two per CU).
-template <int NP, bool S0VEC>
+template <int NP, bool S0VEC, int CS = 1>
 __global__ void __launch_bounds__(64 * WavesFor<NP>()) __attribute__((amdgpu_waves_per_eu(4)))
 tree_verify_kernel(const VerifyParams P) {
-  verify_body<NP, S0VEC, false, false, false>(P);
+  verify_body<NP, S0VEC, false, false, false, false, CS>(P);
 }
 
 // P must stay this kernel's first (only) argument: out_args<true> reads it
@@ -2195,12 +2241,27 @@ int launch_size_order(const int32_t* cu_seqlens, int batch, int n_nodes, int32_t
   return hipGetLastError() == hipSuccess ? DFT_OK : DFT_ERR_LAUNCH;
 }
 
+// Launches of up to 32 nodes whose items would leave most of the chip idle
+// (at most kSplitItems of them: batch 1 at 32 v-heads is 32) split each
+// item's value columns over two workgroups: each forms phase 1 in full and
+// phases 2-3, the state read and the stores on half the columns, which
+// shortens a workgroup's life where the launch is latency-bound.
+constexpr int kSplitItems = 256;
+
 int launch_tree_verify(const dft_verify_args* a, hipStream_t stream) {
   const VerifyParams P = make_params(a);
   const dim3 grid((unsigned)(a->batch * a->hv)), block(64 * WavesFor<32>()), block64(64 * WavesFor<64>());
   VerifyParams narrow, wide;
   bool split;
   split_by_size(a, P, narrow, wide, split);
+  if (a->n_nodes <= 32 && (int64_t)a->batch * a->hv <= kSplitItems) {
+    const dim3 grid2((unsigned)(2 * a->batch * a->hv));
+    if (P.s0_vec)
+      hipLaunchKernelGGL((tree_verify_kernel<32, true, 2>), grid2, block, 0, stream, narrow);
+    else
+      hipLaunchKernelGGL((tree_verify_kernel<32, false, 2>), grid2, block, 0, stream, narrow);
+    return hipGetLastError() == hipSuccess ? DFT_OK : DFT_ERR_LAUNCH;
+  }
   if (a->n_nodes > 32) {
     if (P.s0_vec)
       hipLaunchKernelGGL((tree_verify_kernel<64, true>), grid, block64, 0, stream, wide);
