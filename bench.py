@@ -17,9 +17,12 @@ schedules of that work are timed:
 Inputs are resident in HBM before timing starts.  Printed: one JSON line.
 ``value`` = verified nodes / s / layer = batch * nodes / (step time / 24).
 ``roofline`` is for the kernel with the most time per step, from HIP-event
-timing of that kernel alone; ``cpu_baseline`` times the CPU oracle (numpy,
-the fp32 restatement of the reference recurrence) on one layer of the same
-workload.
+timing of the step (24 launches of that kernel); ``cpu_baseline`` times the
+batched PyTorch fp32 CPU restatement (oracle/gdn_tree_torch.py, pinned
+against the numpy oracle) on one layer of the same workload.  Beside the
+headline: the launch with saved keys / values, the separate schedule, the
+conv and mask kernels, the ragged batch, 64-node trees at batch 64 and the
+batch-1 plugin path.
 """
 from __future__ import annotations
 
@@ -47,6 +50,7 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-ragged", action="store_true", help="skip the packed ragged workload's line")
     ap.add_argument("--no-plugin", action="store_true", help="skip the batch-1 plugin path's line")
+    ap.add_argument("--no-nn64", action="store_true", help="skip the 64-node trees' line")
     ap.add_argument("--only-plugin", action="store_true", help="time the batch-1 plugin path alone")
     ap.add_argument("--only-ragged", action="store_true", help="time the packed ragged workload alone")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
@@ -57,13 +61,16 @@ def parse():
 
 
 class Workload:
-    """Device buffers of the stacked step; every tensor preallocated."""
+    """Device buffers of the stacked step; every tensor preallocated.  n:
+    nodes per tree (32 for the headline; 64, the reference's default tree
+    size FC1_TREE_N of fc1_fused.py:4, for its own line)."""
 
-    def __init__(self, dev, seed=2):
+    def __init__(self, dev, seed=2, n=N):
         import torch
         from dforktree_amd import ops, synth
+        self.n = n
         C = 2 * HK * D + HV * D
-        rows = B * N
+        rows = B * n
         self.rows = rows
         self.y = synth.device_randn_(torch.empty(L, rows, C, device=dev, dtype=torch.bfloat16), seed)
         # the previous step's y: the pipelined commit reads its raw k rows
@@ -78,7 +85,7 @@ class Workload:
         # pool layout [layer, slot, head, V, K]
         self.state = synth.device_randn_(torch.empty(L, B, HV, D, D, device=dev), seed + 3, std=0.02)
         g = torch.Generator().manual_seed(seed)
-        parents = [synth.tree_parents(N, "random", g) for _ in range(B)]
+        parents = [synth.tree_parents(n, "random", g) for _ in range(B)]
         paths = [synth.accepted_path(p, MAX_PATH, g) for p in parents]
         self.path_lens = [len(p) for p in paths]
         idx = torch.full((B, MAX_PATH), -1, dtype=torch.int32)
@@ -86,7 +93,7 @@ class Workload:
             idx[i, :len(p)] = p
         self.accept = idx.to(dev)
         self.parent = torch.cat(parents).to(dev)
-        self.anc_bits = ops.tree_struct(self.parent, 4, batch=B, n_nodes=N, want=("anc_bits",))["anc_bits"]
+        self.anc_bits = ops.tree_struct(self.parent, 4, batch=B, n_nodes=n, want=("anc_bits",))["anc_bits"]
         self.o = torch.empty(L, rows, HV, D, device=dev, dtype=torch.bfloat16)
         self.keys = torch.empty(L, HK, rows, D, device=dev)   # one key set per k-head
         self.vals = torch.empty(L, HV, rows, D, device=dev)
@@ -98,12 +105,12 @@ class Workload:
     def verify(self, l):
         from dforktree_amd import ops
         ops.tree_verify(self.y[l], self.a[l], self.b[l], self.A_log, self.dt_bias, self.state[l].transpose(-1, -2),
-                        hk=HK, hv=HV, anc_bits=self.anc_bits, batch=B, n_nodes=N, neg_exp_A=self.neg, o=self.o[l],
-                        aux_k=self.keys[l], aux_v=self.vals[l], aux_g=self.gains[l], aux_k_per_khead=True)
+                        hk=HK, hv=HV, anc_bits=self.anc_bits, batch=B, n_nodes=self.n, neg_exp_A=self.neg,
+                        o=self.o[l], aux_k=self.keys[l], aux_v=self.vals[l], aux_g=self.gains[l], aux_k_per_khead=True)
 
     def commit(self):
         from dforktree_amd import ops
-        ops.tree_commit(self.state, self.keys, self.vals, self.gains, self.accept, n_nodes=N, k_head_div=HV // HK)
+        ops.tree_commit(self.state, self.keys, self.vals, self.gains, self.accept, n_nodes=self.n, k_head_div=HV // HK)
 
     def step(self):
         for l in range(L):
@@ -130,9 +137,9 @@ class Workload:
             keys.update(pending_values=self.vals[l], aux_v=self.vals2[l])
         ops.tree_commit_verify(self.y[l], self.a[l], self.b[l], self.A_log, self.dt_bias,
                                self.state[l].transpose(-1, -2), hk=HK, hv=HV, anc_bits=self.anc_bits, batch=B,
-                               n_nodes=N, neg_exp_A=self.neg, o=self.o[l], aux_g=self.gains2[l],
+                               n_nodes=self.n, neg_exp_A=self.neg, o=self.o[l], aux_g=self.gains2[l],
                                aux_k_per_khead=True, pending_path=self.accept, pending_gains=self.gains[l],
-                               prev_n_nodes=N, pending_k_head_div=HV // HK, **keys)
+                               prev_n_nodes=self.n, pending_k_head_div=HV // HK, **keys)
 
     def fused_step(self):
         for l in range(L):
@@ -183,14 +190,15 @@ class Workload:
     # ---- algorithmic bytes: every mandatory tensor touched once
     def verify_bytes_per_launch(self):
         C = 2 * HK * D + HV * D
+        n = self.n
         per_req = (HV * D * D * 4          # S0 read
-                   + N * C * 2             # y = [q|k|v] bf16 read
-                   + 2 * N * HV * 2        # a, b bf16 read
-                   + N * 8                 # ancestor bit masks
-                   + N * HV * D * 2        # o bf16 write
-                   + HV * N * D * 4        # vn fp32 write
-                   + HV * N * 4            # G write
-                   + HK * N * D * 4)       # normalised k fp32 write (per k-head)
+                   + n * C * 2             # y = [q|k|v] bf16 read
+                   + 2 * n * HV * 2        # a, b bf16 read
+                   + n * 8                 # ancestor bit masks
+                   + n * HV * D * 2        # o bf16 write
+                   + HV * n * D * 4        # vn fp32 write
+                   + HV * n * 4            # G write
+                   + HK * n * D * 4)       # normalised k fp32 write (per k-head)
         return B * per_req
 
     def fused_bytes_per_launch(self, raw_keys=True, raw_values=True):
@@ -207,8 +215,8 @@ class Workload:
                     + (ell * HV * 2 if raw_values else 0)        # path b gates
                     + ell * HV * 4                               # path gains
                     + MAX_PATH * 4)                              # path indices
-        key_saves = B * HK * N * D * 4 if raw_keys else 0
-        value_saves = B * HV * N * D * 4 if raw_values else 0
+        key_saves = B * HK * self.n * D * 4 if raw_keys else 0
+        value_saves = B * HV * self.n * D * 4 if raw_values else 0
         return self.verify_bytes_per_launch() - key_saves - value_saves + tot
 
     def commit_bytes_per_launch(self):
@@ -481,55 +489,55 @@ def _cpu_model():
 
 
 def cpu_baseline(seconds):
-    """The CPU oracle on one layer of the workload (64 requests x 32 nodes,
-    verify + commit of each accepted path), repeated for ~`seconds`.  The
-    numpy BLAS gets one thread per core this process may run on (capped by
-    OMP_NUM_THREADS when the environment sets it, the CPU share of the box);
-    the trees' ancestry is built outside the timed region, as the GPU path
-    gets it from tree_struct once per step."""
+    """The CPU baseline: one layer of the workload (64 requests x 32 nodes,
+    verify + commit of each accepted path) through the batched PyTorch fp32
+    restatement (oracle/gdn_tree_torch.py, pinned against the numpy oracle),
+    repeated for ~`seconds`.  torch gets one thread per core this process may
+    run on (capped by OMP_NUM_THREADS when the environment sets it, the CPU
+    share of the box); the trees' ancestry and the path masks are built
+    outside the timed region, as the GPU path gets them once per step."""
     import numpy as np
     import torch
     from dforktree_amd import synth
     from oracle import gdn_tree as O
+    from oracle import gdn_tree_torch as T
     affinity = len(os.sched_getaffinity(0))
-    want = min(affinity, int(os.environ.get("OMP_NUM_THREADS", affinity) or affinity))
-    limiter, threads = None, None
-    try:
-        from threadpoolctl import threadpool_info, threadpool_limits
-        limiter = threadpool_limits(limits=want, user_api="blas")
-        threads = max([i.get("num_threads", 1) for i in threadpool_info() if i.get("user_api") == "blas"] or [1])
-    except Exception:  # threadpoolctl missing: numpy's BLAS runs with what the environment gives it
-        threads = want
+    threads = min(affinity, int(os.environ.get("OMP_NUM_THREADS", affinity) or affinity))
+    prev_threads = torch.get_num_threads()
+    torch.set_num_threads(threads)
     bt = synth.make_batch(2, 0, [N] * B, hk=HK, hv=HV)
-    y = bt.y.float().numpy().reshape(B, N, -1)
-    a = bt.a.numpy().reshape(B, N, -1)
-    b = bt.b.numpy().reshape(B, N, -1)
-    S0 = np.ascontiguousarray(bt.state.numpy().transpose(0, 1, 3, 2))
-    par = bt.parent.numpy().reshape(B, N)
+    y = bt.y.float().reshape(B, N, -1)
+    a = bt.a.reshape(B, N, -1)
+    b = bt.b.reshape(B, N, -1)
+    S0 = bt.state.transpose(-1, -2).contiguous()  # (k, v)
+    par = bt.parent.reshape(B, N)
     g = torch.Generator().manual_seed(3)
-    paths = [synth.accepted_path(torch.from_numpy(p), MAX_PATH, g).tolist() for p in par]
-    anc = np.stack([O.tree_struct(p)[0] for p in par])  # once per step, not per layer
+    paths = [synth.accepted_path(p, MAX_PATH, g) for p in par]
+    anc = torch.from_numpy(np.stack([O.tree_struct(p.numpy())[0] for p in par]).astype(np.float32))
+    on = torch.zeros(B, N)
+    for i, p in enumerate(paths):
+        on[i, p.long()] = 1
+    u = torch.tensor([int(p[-1]) for p in paths])
 
     def layer():
-        r = O.tree_gdn_split(y, a, b, bt.A_log.numpy(), bt.dt_bias.numpy(), S0, anc, HK, HV, D, D)
-        for i in range(B):
-            O.closed_commit(S0[i], r["k"][i], r["vn"][i], r["G"][i], paths[i])
+        r = T.tree_gdn_split(y, a, b, bt.A_log, bt.dt_bias, S0, anc, HK, HV, D, D)
+        return T.closed_commit(S0, r["k"], r["vn"], r["G"], on, u)
 
-    layer()  # warm-up
-    times = []
-    t_end = time.perf_counter() + seconds
-    while time.perf_counter() < t_end or len(times) < 3:
-        t0 = time.perf_counter()
-        layer()
-        times.append(time.perf_counter() - t0)
+    with torch.inference_mode():
+        layer()  # warm-up
+        times = []
+        t_end = time.perf_counter() + seconds
+        while time.perf_counter() < t_end or len(times) < 3:
+            t0 = time.perf_counter()
+            layer()
+            times.append(time.perf_counter() - t0)
+    torch.set_num_threads(prev_threads)
     t = float(np.median(times))
-    if limiter is not None:
-        limiter.restore_original_limits()
     return {"value": B * N / t, "unit": "nodes/s/layer", "cores": threads, "kind": "port",
             "affinity_cores": affinity, "cpu_model": _cpu_model(),
             "sample": f"{len(times)} x one layer of the workload ({B} requests x {N} nodes, verify + "
-                      f"commit of the accepted paths) through the numpy fp32 oracle (numpy {np.__version__}, "
-                      f"BLAS on {threads} threads), median {t * 1e3:.0f} ms"}
+                      f"commit of the accepted paths) through the batched PyTorch fp32 restatement "
+                      f"(torch {torch.__version__}, {threads} threads), median {t * 1e3:.0f} ms"}
 
 
 def main():
@@ -568,14 +576,14 @@ def main():
     for l in range(L):
         w.verify(l)
     torch.cuda.synchronize()
-    t_fused_layers = time_graph(lambda: [w.fused(l) for l in range(L)], reps_kernel, args.warmup, args.eager)
-    t_fused = t_fused_layers / L
     # the same launch reading saved values (raw key rows), and saved keys and values
     t_fused_sv = time_graph(lambda: [w.fused(l, raw_values=False) for l in range(L)], reps_kernel, args.warmup,
                             args.eager) / L
     t_fused_saved = time_graph(lambda: [w.fused(l, raw_keys=False, raw_values=False) for l in range(L)], reps_kernel,
                                args.warmup, args.eager) / L
+    # the step is 24 launches of the dominant kernel: its launch time is taken from this one timing
     t_step = time_graph(w.fused_step, args.steps, args.warmup, args.eager)
+    t_fused = t_step / L
     # conv and mask run once per layer in a step: 24 back-to-back launches per replay, as for verify
     w.conv_setup(dev)
     t_conv = time_graph(lambda: [w.conv() for _ in range(L)], reps_kernel, args.warmup, args.eager) / L
@@ -593,10 +601,26 @@ def main():
                   "unordered_us_per_layer": round(t_unord * 1e3, 2),
                   "nodes_per_s_per_layer": round(rw.rows / (t_ragged * 1e-3), 1),
                   "hbm_frac": round(rw.bytes_per_launch() / (t_ragged * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+    nn64 = None
+    if not args.no_ragged:
+        del rw
+    if not args.no_nn64:
+        torch.cuda.empty_cache()
+        w64 = Workload(dev, seed=4, n=64)  # the reference's default tree size (FC1_TREE_N, fc1_fused.py:4)
+        t64_v = time_graph(lambda: [w64.verify(l) for l in range(L)], reps_kernel, args.warmup, args.eager) / L
+        t64_f = time_graph(w64.fused_step, reps_kernel, args.warmup, args.eager) / L
+        nn64 = {"workload": "batch 64, uniform 64-node random recursive trees, 24 layers (the reference's default "
+                            "tree size); verify, and the pipelined commit -> verify (raw key rows, recomputed values)",
+                "verify_us_per_layer": round(t64_v * 1e3, 2),
+                "verify_nodes_per_s_per_layer": round(B * 64 / (t64_v * 1e-3), 1),
+                "verify_hbm_frac": round(w64.verify_bytes_per_launch() / (t64_v * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                "commit_verify_us_per_layer": round(t64_f * 1e3, 2),
+                "nodes_per_s_per_layer": round(B * 64 / (t64_f * 1e-3), 1),
+                "hbm_frac": round(w64.fused_bytes_per_launch() / (t64_f * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                "algorithmic_bytes_per_launch": w64.fused_bytes_per_launch()}
+        del w64
     plugin = None
     if not args.no_plugin:
-        if not args.no_ragged:
-            del rw
         torch.cuda.empty_cache()
         plugin = plugin_lines(dev, reps_kernel, args.warmup, args.eager)
     if args.copy_calibration:
@@ -671,10 +695,13 @@ def main():
         "commit_verify_saved_keys": {"us_per_layer": round(t_fused_saved * 1e3, 2),
                                      "hbm_frac": frac(w.fused_bytes_per_launch(raw_keys=False, raw_values=False),
                                                       t_fused_saved)},
-        # state bytes the separate kernels need (verify read + commit read and write) per unit time,
-        # and the state bytes the pipelined schedule actually moves (one read + one write)
-        "state_traffic_hbm_frac": frac(w.state_bytes_per_step(), t_step),
-        "state_moved_hbm_frac": frac(w.state_bytes_moved_pipelined(), t_step),
+        # state bytes per unit time: what the pipelined schedule moves (one read and one write per
+        # request-layer), and an equivalent that also credits the separate verify's own state read, which the
+        # fused launch does not perform (3 x 2 MiB per request-layer: the bytes the separate kernels need)
+        "state_traffic": {"moved_hbm_frac": frac(w.state_bytes_moved_pipelined(), t_step),
+                          "moved_bytes_per_step": w.state_bytes_moved_pipelined(),
+                          "separate_equivalent_hbm_frac": frac(w.state_bytes_per_step(), t_step),
+                          "separate_equivalent_bytes_per_step": w.state_bytes_per_step()},
         "separate": {"ms_per_step": round(t_step_sep, 4), "value": round(B * N / (t_step_sep * 1e-3 / L), 1),
                      "verify_us_per_layer": round(t_verify * 1e3, 2), "verify_hbm_frac": frac(vb, t_verify),
                      "commit_ms": round(t_commit, 4), "commit_hbm_frac": frac(cb, t_commit),
@@ -685,6 +712,7 @@ def main():
         "mask_pack_us": round(t_mask * 1e3, 2),
         "mask_pack_hbm_frac": frac(w.mask_bytes_per_launch(), t_mask),
         "ragged": ragged,
+        "nn64": nn64,
         "plugin": plugin,
     }
     if not args.no_cpu_baseline:

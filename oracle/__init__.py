@@ -21,6 +21,10 @@ Contents (``oracle.gdn_tree``):
 * ``closed_commit`` / ``snapshot_commit`` closed-form accepted-path commit
                              (tree_kernels.py:111-127, fc1_fused.py:26-49)
 
+``oracle.gdn_tree_torch``: the split verify and the closed commit as batched
+PyTorch fp32 CPU ops (the CPU baseline bench.py times), pinned against
+``oracle.gdn_tree``.
+
 ``oracle.mask``: ``packbits`` / ``segment_packbits`` (numpy.packbits per
 segment, as flashinfer packs the custom mask for fc1_plan.py:26) and
 ``tree_mask`` / ``tree_mask_packed`` (the mask of fc1_branch64.py:39).

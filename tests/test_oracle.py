@@ -271,3 +271,34 @@ def test_snapshot_at_inner_node_uses_ancestors_only():
     assert rel_l2(S_anc, f["states"][:, u]) < 1e-5
     S_all = O.closed_commit(S0, r["k"][0], r["vn"][0], r["G"][0], path, u=u, anc=None, dtype=np.float64)
     assert rel_l2(S_all, f["states"][:, u]) > 1e-3
+
+
+# ---------------------------------------------------------------- torch restatement (the CPU baseline)
+@pytest.mark.parametrize("n,kind", [(16, "random"), (32, "chain"), (32, "random"), (48, "random")])
+def test_torch_restatement_matches_oracle(n, kind):
+    """oracle.gdn_tree_torch (the batched torch fp32 form bench.py times as
+    its CPU baseline) against the numpy oracle, three requests at once: o, vn,
+    k and G within 1e-5, and the batched path commit against closed_commit
+    of each request's accepted walk."""
+    import torch
+    from oracle import gdn_tree_torch as T
+    rng = np.random.default_rng(77 + n)
+    reqs = [inputs(n, rng=rng) + (rand_tree(n, kind, rng),) for _ in range(3)]
+    y, aa, bb = (np.stack([r[i] for r in reqs]) for i in range(3))
+    A_log, dtb = reqs[0][3], reqs[0][4]
+    S0 = np.stack([r[5] for r in reqs])
+    anc = np.stack([O.tree_struct(r[6])[0] for r in reqs]).astype(np.float32)
+    want = O.tree_gdn_split(y, aa, bb, A_log, dtb, S0, anc, 2, 4, D, D)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a))  # noqa: E731
+    got = T.tree_gdn_split(t(y), t(aa), t(bb), t(A_log), t(dtb), t(S0), t(anc), 2, 4, D, D)
+    for key in ("o", "vn", "k", "G"):
+        assert rel_l2(got[key].numpy(), want[key]) < 1e-5, key
+    # each request commits the walk from the root to its last node
+    paths = [sorted(np.nonzero(anc[b, n - 1])[0]) for b in range(3)]
+    on = torch.zeros(3, n)
+    for b, pth in enumerate(paths):
+        on[b, pth] = 1
+    S = T.closed_commit(t(S0), got["k"], got["vn"], got["G"], on, torch.full((3,), n - 1, dtype=torch.long))
+    for b in range(3):
+        ref = O.closed_commit(S0[b], want["k"][b], want["vn"][b], want["G"][b], paths[b])
+        assert rel_l2(S[b].numpy(), ref) < 1e-5
