@@ -1989,11 +1989,14 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
   // The verify issues its state tile in 4 groups (the k-steps phase 2
   // consumes in order) through phase 1: a wave blocked on a full memory queue
   // then stalls between compute phases instead of ahead of all of them
-  // (1.7% faster at batch 64).  The fused form needs the whole tile for its
-  // commit before phase 1 and issues it at once.
-  constexpr bool kSplit = S0VEC && !COMMIT;
+  // (1.7% faster at batch 64).  So does the 32-wide fused form, whose commit
+  // follows phase 1 (64.05 -> 62.01 us at batch 64, raw rows copied ahead of
+  // the tile), except the form that holds raw path rows in registers beside
+  // the tile, which spilled; the 64-wide one commits before phase 1 and
+  // issues its tile at once.
+  constexpr bool kSplit = S0VEC && (!COMMIT || (kEarly && (kPathDma || !(RAWK && RVN))));
   if (kSplit) {
-    issue_state_group<false, false, NWC>(S0, p.state_v_stride, wave, lane, 0, s0r);
+    issue_state_group<COMMIT, kEarly, NWC>(S0, p.state_v_stride, wave, lane, 0, s0r);
   } else if (S0VEC) {
     issue_state<COMMIT, kEarly, NWC>(S0, p.state_v_stride, wave, lane, s0r);
   } else {
@@ -2012,7 +2015,7 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
   if (wave == 0) {
     // the gate words were wave 0's first copies: wait for them only (the
     // fused form: for everything before the state, the path loads included)
-    __builtin_amdgcn_s_waitcnt(waitcnt_imm(COMMIT ? kStateLoads : kQkvDma + (kSplit ? kGroupLoads : kStateLoads), 15));
+    __builtin_amdgcn_s_waitcnt(waitcnt_imm((COMMIT ? 0 : kQkvDma) + (kSplit ? kGroupLoads : kStateLoads), 15));
     asm volatile("" ::: "memory");
     if (lane < NP) decode_gates(p, it, lane, sm.graw, sm);
   }
@@ -2041,7 +2044,7 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
     }
     __syncthreads();  // am and x take the Gram tiles and X
   }
-  if constexpr (kSplit) issue_state_group<false, false, NWC>(S0, p.state_v_stride, wave, lane, 1, s0r);
+  if constexpr (kSplit) issue_state_group<COMMIT, kEarly, NWC>(S0, p.state_v_stride, wave, lane, 1, s0r);
   // (the 32-wide fused form saves after Cq/Ck: at this point its tile is
   // still streaming in, and the saves' stores would wait on the full queue)
   if constexpr (!kEarly) phase_saves<NP, COMMIT, NW, VerifySmem<NP>, VerifySmem<NP>, CS>(P, it, tid, sm, sm, col0);
@@ -2059,7 +2062,7 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
       issue_pending<NW, RAWK, RVN>(P.c, pd, it.h, wave, lane, S0, kr, pv);
     }
   }
-  if constexpr (kSplit) issue_state_group<false, false, NWC>(S0, p.state_v_stride, wave, lane, 2, s0r);
+  if constexpr (kSplit) issue_state_group<COMMIT, kEarly, NWC>(S0, p.state_v_stride, wave, lane, 2, s0r);
   __syncthreads();
 #pragma unroll
   for (int d = 1; d < MT; ++d) {
@@ -2067,7 +2070,7 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
     phase_offdiag<NP, NW>(tid, d, sm, mtn);
     __syncthreads();
   }
-  if constexpr (kSplit) issue_state_group<false, false, NWC>(S0, p.state_v_stride, wave, lane, 3, s0r);
+  if constexpr (kSplit) issue_state_group<COMMIT, kEarly, NWC>(S0, p.state_v_stride, wave, lane, 3, s0r);
   phase_pq<NP, NW>(tid, sm, sm, mtn);
   phase_split_x<NP, NW>(tid, sm, mtn);
   if constexpr (kEarly) {
