@@ -115,21 +115,38 @@ __global__ void __launch_bounds__(64) tree_conv4_bf16_kernel(const dft_conv_args
 
   if (active) {
     const uint16_t* xb = static_cast<const uint16_t*>(p.x) + (int64_t)b * p.x_req_stride + c0;
-    // token rows: every load is issued (a tap outside the tokens reads row 0
-    // and is discarded), so none waits on a branch
-    u32x4 raw[4];
-    bool tok[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      tok[j] = col[j] >= 3 && col[j] < 3 + p.n_nodes;
-      raw[j] = *reinterpret_cast<const u32x4*>(xb + (tok[j] ? col[j] - 3 : 0) * p.x_node_stride);
-    }
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-      if (!tok[j]) raw[j] = u32x4{0u, 0u, 0u, 0u};
     // the state slot (needed by conv-state taps only); a negative one reads slot 0
     if (p.cs_indices) slot = ld_i(p.cs_indices, b, p.cs_indices_dtype);
     if (slot < 0) slot = 0;
+    // Token rows: every load is issued (a tap outside the tokens reads row 0
+    // and is discarded), so none waits on a branch.  A tap on a bf16 conv-state
+    // column (a node within two edges of the root) gathers the column's 8
+    // values into the same registers instead, issued with the token loads:
+    // read through the per-element path below (8 two-byte loads per tap, each
+    // waited for in turn), these taps cost random 32-node trees about 5 us per
+    // launch at batch 64 (computing a chain's columns, which reach the state
+    // at 3 nodes only, ran 39.7 -> 34.7 us).
+    const bool cs_bf16 = p.cs_dtype == DFT_BF16;
+    u32x4 raw[4];
+    bool tok[4], csg[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      tok[j] = col[j] >= 3 && col[j] < 3 + p.n_nodes;
+      csg[j] = cs_bf16 && col[j] >= 0 && col[j] < 3;  // uniform
+      if (csg[j]) {
+        const uint16_t* cs = static_cast<const uint16_t*>(p.conv_state) + slot * p.cs_slot_stride +
+                             (int64_t)c0 * p.cs_chan_stride + col[j] * p.cs_col_stride;
+        uint16_t h[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) h[e] = cs[(int64_t)e * p.cs_chan_stride];
+        raw[j] = *reinterpret_cast<const u32x4*>(h);
+      } else {
+        raw[j] = *reinterpret_cast<const u32x4*>(xb + (tok[j] ? col[j] - 3 : 0) * p.x_node_stride);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (!tok[j] && !csg[j]) raw[j] = u32x4{0u, 0u, 0u, 0u};
 
     float acc[8];
 #pragma unroll
@@ -138,13 +155,13 @@ __global__ void __launch_bounds__(64) tree_conv4_bf16_kernel(const dft_conv_args
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       float v[8];
-      if (col[j] >= 0 && col[j] < 3) {  // a conv-state column (near the root)
+      if (col[j] >= 0 && col[j] < 3 && !csg[j]) {  // a conv-state column of another dtype
 #pragma unroll
         for (int e = 0; e < 8; ++e)
           v[e] = ld_f(p.conv_state,
                       slot * p.cs_slot_stride + (int64_t)(c0 + e) * p.cs_chan_stride + col[j] * p.cs_col_stride,
                       p.cs_dtype);
-      } else {  // a token row, or zero outside [conv_state || x]
+      } else {  // a token row, a gathered bf16 state column, or zero outside [conv_state || x]
         const uint16_t* h = reinterpret_cast<const uint16_t*>(&raw[j]);
 #pragma unroll
         for (int e = 0; e < 8; ++e) v[e] = bf16_bits_to_f32(h[e]);
