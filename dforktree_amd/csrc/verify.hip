@@ -1875,13 +1875,235 @@ __device__ __forceinline__ void fused_status(const Item& it, int lane, uint32_t 
 // CS (plain verify of up to 32 nodes): the item's value columns are split
 // over CS workgroups, CS items apart in the grid's last dimension; each
 // forms phase 1 in full and phases 2-3 on its 128 / CS columns.
+// ---------------------------------------------------------------------------
+// Trees of 33-64 nodes in small launches: each (request, v-head) runs on two
+// workgroups of 8 waves, each taking 64 value columns (col0 = 0 or 64).  Both
+// form phase 1 in full.  In phases 2-3 wave w takes column tile c = w & 3
+// (16 columns) and half h = w >> 2: it reads rows k = 64h .. 64h + 63 of its
+// columns' state (so a workgroup reads its 32 KiB once) and forms partial Cq
+// and Ck over those k for every node tile.  The two halves of a column tile
+// swap the partials of each other's node tiles through LDS, and from then on
+// wave (c, h) owns node tiles 2h and 2h + 1: their W, vn and o.  X W and
+// Pq vn of tiles 2-3 also need k-step 0 (nodes 0-31), whose W and vn the
+// first half passes on through LDS.  The sums of the two k halves are formed
+// in another order than the one-workgroup kernel's, so Cq and Ck can differ
+// from it in the last bits.
+// ---------------------------------------------------------------------------
+template <bool ON>
+struct HalfXch {
+  int unused;
+};
+template <>
+struct HalfXch<true> {
+  f32x4 part[8][4][64];  // wave w's partials of its partner's node tiles: Cq, Cq, Ck, Ck
+  bf16x8 w[4][2][64];    // the first half's W (k-step 0; hi, lo) of column tile c
+};
+
+// k-step s (rows k = 32s .. 32s + 31) of column tile c's state, in the MFMA layout
+__device__ __forceinline__ void issue_state_half(const float* S0, int64_t v_stride, int c, int lane, int s,
+                                                 f32x4& a, f32x4& b) {
+  const int n16 = lane & 15, g4 = lane >> 4;
+  const float* rowp = S0 + (int64_t)(16 * c + n16) * v_stride + 4 * g4 + 32 * s;
+  a = *reinterpret_cast<const f32x4*>(rowp);
+  b = *reinterpret_cast<const f32x4*>(rowp + 16);
+}
+
+// partial Cq / Ck over k-steps 2h, 2h + 1 for every node tile, in
+// phase_cq_ck's layouts (WHICH and KEEP as there; s0h holds the two k-steps)
+template <int WHICH, int KEEP, class RW>
+__device__ __forceinline__ void cq_ck_half(int lane, int h, const RW& rw, const f32x4 (&s0h)[4], f32x4 (&cq)[4],
+                                           f32x4 (&ck)[4], int mtn, bf16x8 (&sh)[2], bf16x8 (&sl)[2]) {
+  constexpr bool DQ = (WHICH & 1) != 0, DK = (WHICH & 2) != 0;
+  const int n16 = lane & 15, g4 = lane >> 4;
+  const int op = qkv_op4(n16, g4);
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt) {
+    if (DQ) cq[mt] = f32x4{};
+    if (DK) ck[mt] = f32x4{};
+  }
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int s = 2 * h + j;
+    bf16x8 bhi, blo;
+    if constexpr (KEEP == 2) {
+      bhi = sh[j];
+      blo = sl[j];
+    } else {
+      const float xs[8] = {s0h[2 * j][0],     s0h[2 * j][1],     s0h[2 * j][2],     s0h[2 * j][3],
+                           s0h[2 * j + 1][0], s0h[2 * j + 1][1], s0h[2 * j + 1][2], s0h[2 * j + 1][3]};
+      split_bf16x8(xs, bhi, blo);
+      if constexpr (KEEP == 1) {
+        sh[j] = bhi;
+        sl[j] = blo;
+      }
+    }
+    const int o1 = op ^ (32 * s), o2 = op ^ (32 * s + 16);
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+      if (mt >= mtn) break;  // padding rows stay zero
+      bf16x8 aq{}, ak{};
+      if (DQ) aq = lds_bf16x8_split(rw.q + 16 * mt * kD + o1, rw.q + 16 * mt * kD + o2);
+      if (DK) ak = lds_bf16x8_split(rw.k + 16 * mt * kD + o1, rw.k + 16 * mt * kD + o2);
+      if (DQ) cq[mt] = mfma_bf16_16x16x32(bhi, aq, cq[mt]);
+      if (DK) ck[mt] = mfma_bf16_16x16x32(ak, bhi, ck[mt]);
+      if (DQ) cq[mt] = mfma_bf16_16x16x32(blo, aq, cq[mt]);
+      if (DK) ck[mt] = mfma_bf16_16x16x32(ak, blo, ck[mt]);
+    }
+  }
+}
+
+// Phases 2-3 of the two-workgroup 64-wide form, from the state's k half s0h
+// to o and vn staged (or stored) for node tiles 2h, 2h + 1 of the wave's 16
+// columns.  Starts after phase 1 (X and Pq split, no barrier yet).
+template <class RW, class WK>
+__device__ __forceinline__ void tail_halves(const VerifyParams& P, const Item& it, int lane, int wave, RW& rw,
+                                            const WK& wk, HalfXch<true>& xc, const f32x4 (&s0h)[4], int mtn,
+                                            int col0) {
+  constexpr int LDA = WK::LDA;
+  const dft_verify_args& p = P.a;
+  const int c = wave & 3, h = wave >> 2, n16 = lane & 15, g4 = lane >> 4;
+  // Cq first; once every wave is done with the q rows, the v rows are
+  // copied into their region while Ck computes (as in the one-workgroup form)
+  f32x4 cq[4], ck[4];
+  bf16x8 sh[2], sl[2];
+  cq_ck_half<1, 1>(lane, h, rw, s0h, cq, ck, mtn, sh, sl);
+  __syncthreads();  // X and Pq complete, the q rows consumed
+  issue_rows<64, 2, 3, 8>(p, it, wave, lane, rw);
+  cq_ck_half<2, 2>(lane, h, rw, s0h, cq, ck, mtn, sh, sl);
+  // the partner's node tiles go to it; this wave keeps tiles 2h, 2h + 1
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    xc.part[wave][j][lane] = h ? cq[j] : cq[2 + j];
+    xc.part[wave][2 + j][lane] = h ? ck[j] : ck[2 + j];
+  }
+  __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 15));  // the v row copies (untracked by the backend)
+  __syncthreads();
+  const int pw = wave ^ 4;
+  f32x4 cqo[2], cko[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    cqo[j] = (h ? cq[2 + j] : cq[j]) + xc.part[pw][j][lane];
+    cko[j] = (h ? ck[2 + j] : ck[j]) + xc.part[pw][2 + j][lane];
+  }
+  // W = beta (v - e^G rk Ck) of k-step h (node tiles 2h, 2h + 1), in
+  // phase_w's operand layout
+  const int colw = col0 + 16 * c + n16;
+  bf16x8 wh, wl;
+  {
+    f32x4 bt[2], gcv[2];
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+      bt[hh] = *reinterpret_cast<const f32x4*>(&wk.beta[16 * (2 * h + hh) + 4 * g4]);
+      gcv[hh] = *reinterpret_cast<const f32x4*>(&wk.gc[16 * (2 * h + hh) + 4 * g4]);
+    }
+    float w8[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int hh = e >> 2, r = e & 3;
+      const int i = 16 * (2 * h + hh) + 4 * g4 + r;
+      const float vv = bf16_bits_to_f32(rw.vrows()[qkv_at(i, colw)]);
+      w8[e] = bt[hh][r] * (vv - gcv[hh][r] * cko[hh][r]);
+    }
+    split_bf16x8(w8, wh, wl);
+  }
+  if (h == 0) {
+    xc.w[c][0][lane] = wh;
+    xc.w[c][1][lane] = wl;
+  }
+  __syncthreads();  // every wave has read its v rows (the q/k region takes vn); W of k-step 0 is out
+  bf16x8 w0h = wh, w0l = wl;
+  if (h) {
+    w0h = xc.w[c][0][lane];
+    w0l = xc.w[c][1][lane];
+  }
+  // tile mt of [F; V] (F = X or Pq in the split operand layout, V = W or vn
+  // of k-steps 0 and 1): lane (n, g) gets node 16mt + n, columns 4g .. + 3
+  auto product = [&](const float* f, bf16x8 v0h, bf16x8 v0l, bf16x8 v1h, bf16x8 v1l, int mt) {
+    f32x4 acc{};
+    {
+      const float* chunk = f + (16 * mt + n16) * LDA + 8 * g4;
+      const bf16x8 ah = *reinterpret_cast<const bf16x8*>(chunk);
+      const bf16x8 al = *reinterpret_cast<const bf16x8*>(chunk + 4);
+      acc = mfma_bf16_16x16x32(v0h, ah, acc);
+      acc = mfma_bf16_16x16x32(v0l, ah, acc);
+      acc = mfma_bf16_16x16x32(v0h, al, acc);
+    }
+    if (h) {  // tiles 2-3: k-step 1 too (uniform); both factors are lower triangular
+      const float* chunk = f + (16 * mt + n16) * LDA + 32 + 8 * g4;
+      const bf16x8 ah = *reinterpret_cast<const bf16x8*>(chunk);
+      const bf16x8 al = *reinterpret_cast<const bf16x8*>(chunk + 4);
+      acc = mfma_bf16_16x16x32(v1h, ah, acc);
+      acc = mfma_bf16_16x16x32(v1l, ah, acc);
+      acc = mfma_bf16_16x16x32(v1h, al, acc);
+    }
+    return acc;
+  };
+  float* vn_s = reinterpret_cast<float*>(rw.q);  // spans q and k
+  const int colo = col0 + 16 * c + 4 * g4;      // the product tiles' first column
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int mt = 2 * h + j;
+    if (mt >= mtn) break;  // padding rows: not stored (uniform)
+    const f32x4 acc = product(wk.x(), w0h, w0l, wh, wl, mt);
+    const int i = 16 * mt + n16;
+    *reinterpret_cast<f32x4*>(&vn_s[vn_at(i, colo)]) = acc;
+    if (!P.vn_stage && p.aux_v && i < it.n) {
+      float* dst = p.aux_v + (int64_t)it.h * p.aux_v_h_stride + (it.row0 + i) * p.aux_v_row_stride + colo;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) dst[r] = acc[r];
+    }
+  }
+  // vn of every tile staged; every wave is done with X, where o is staged
+  __syncthreads();
+  // vn back in W's layout (phase_out's read-back) for k-steps 0 and, in the
+  // second half, 1; padding tiles were never written and read as zeros
+  bf16x8 vh[2], vl[2];
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks) {
+    const float* base = vn_s + 4 * g4 * kD + (colw & 3);
+    const int ch = ((colw >> 2) ^ (4 * g4)) & 31;
+    float v8[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int hh = e >> 2, r = e & 3;
+      const float v = base[(32 * ks + 16 * hh + r) * kD + ((ch ^ (16 * hh + r)) << 2)];
+      v8[e] = (2 * ks + hh < mtn && ks <= h) ? v : 0.f;  // uniform
+    }
+    split_bf16x8(v8, vh[ks], vl[ks]);
+  }
+  uint16_t* o_s = rw.ostage();
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int mt = 2 * h + j;
+    if (mt >= mtn) break;
+    const f32x4 acc = product(wk.am(), vh[0], vl[0], vh[1], vl[1], mt);
+    const int i = 16 * mt + n16;
+    const f32x4 ov = wk.cO[i] * cqo[j] + acc;
+    if (P.o_stage) {
+      const bf16x2 lo = __builtin_convertvector((f32x2{ov[0], ov[1]}), bf16x2);  // round to nearest even
+      const bf16x2 hi = __builtin_convertvector((f32x2{ov[2], ov[3]}), bf16x2);
+      uint2 w;
+      __builtin_memcpy(&w.x, &lo, 4);
+      __builtin_memcpy(&w.y, &hi, 4);
+      *reinterpret_cast<uint2*>(&o_s[qkv_at(i, colo)]) = w;
+    } else if (i < it.n) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        st_f(p.o, (it.row0 + i) * p.o_row_stride + (int64_t)it.h * p.o_h_stride + colo + r, p.o_dtype, ov[r]);
+    }
+  }
+}
+
 template <int NP, bool S0VEC, bool COMMIT, bool RAWK, bool RVN, bool PDMA = false, int CS = 1>
 __device__ __forceinline__ void verify_body(const VerifyParams& P) {
   constexpr int MT = NP / 16;
   constexpr int NW = WavesFor<NP>();
-  constexpr int NWC = NW * CS;  // column waves of the item (of all its workgroups)
+  // the 64-wide column split: waves split the k half and node tiles (tail_halves)
+  constexpr bool kHalves = NP > 32 && CS > 1;
+  constexpr int NWC = kHalves ? NW : NW * CS;  // column waves of the item (of all its workgroups)
   constexpr int TT = Waves<NWC>::TT, CW = Waves<NWC>::CW;
-  static_assert(CS == 1 || (!COMMIT && NP <= 32), "the column split serves the plain 32-wide verify");
+  static_assert(CS == 1 || !COMMIT, "the column split serves the plain verify");
+  static_assert(!kHalves || (CS == 2 && S0VEC), "the 64-wide split takes two workgroups and a vector state");
   // The 32-wide fused form runs phase 1 (which needs no state) before its
   // commit, under the state stream, and stages the commit's keys and
   // write-back in the v region, whose rows it copies in afterwards.
@@ -1898,6 +2120,8 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
   // the recomputed path values' matrices and key norms: only the forms that
   // recompute them hold them (4.3 KiB)
   __shared__ alignas(16) float rvx[RVN ? kRvx : 4];
+  // the 64-wide split's exchange between the two halves (40 KiB)
+  __shared__ HalfXch<kHalves> xch;
 
   // (the wave index as a scalar: in a vector register it is held, and at the
   // fused form's register cap spilled, through phase 1)
@@ -1986,6 +2210,7 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
   asm volatile("" ::: "memory");
 
   f32x4 s0r[TT][8];
+  f32x4 s0h[4];  // the 64-wide split: k-steps 2h, 2h + 1 of the wave's column tile
   // The verify issues its state tile in 4 groups (the k-steps phase 2
   // consumes in order) through phase 1: a wave blocked on a full memory queue
   // then stalls between compute phases instead of ahead of all of them
@@ -1995,7 +2220,9 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
   // the tile, which spilled; the 64-wide one commits before phase 1 and
   // issues its tile at once.
   constexpr bool kSplit = S0VEC && (!COMMIT || (kEarly && (kPathDma || !(RAWK && RVN))));
-  if (kSplit) {
+  if constexpr (kHalves) {
+    issue_state_half(S0, p.state_v_stride, wave & 3, lane, 2 * (wave >> 2), s0h[0], s0h[1]);
+  } else if (kSplit) {
     issue_state_group<COMMIT, kEarly, NWC>(S0, p.state_v_stride, wave, lane, 0, s0r);
   } else if (S0VEC) {
     issue_state<COMMIT, kEarly, NWC>(S0, p.state_v_stride, wave, lane, s0r);
@@ -2044,7 +2271,10 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
     }
     __syncthreads();  // am and x take the Gram tiles and X
   }
-  if constexpr (kSplit) issue_state_group<COMMIT, kEarly, NWC>(S0, p.state_v_stride, wave, lane, 1, s0r);
+  if constexpr (kHalves)
+    issue_state_half(S0, p.state_v_stride, wave & 3, lane, 2 * (wave >> 2) + 1, s0h[2], s0h[3]);
+  else if constexpr (kSplit)
+    issue_state_group<COMMIT, kEarly, NWC>(S0, p.state_v_stride, wave, lane, 1, s0r);
   // (the 32-wide fused form saves after Cq/Ck: at this point its tile is
   // still streaming in, and the saves' stores would wait on the full queue)
   if constexpr (!kEarly) phase_saves<NP, COMMIT, NW, VerifySmem<NP>, VerifySmem<NP>, CS>(P, it, tid, sm, sm, col0);
@@ -2062,7 +2292,7 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
       issue_pending<NW, RAWK, RVN>(P.c, pd, it.h, wave, lane, S0, kr, pv);
     }
   }
-  if constexpr (kSplit) issue_state_group<COMMIT, kEarly, NWC>(S0, p.state_v_stride, wave, lane, 2, s0r);
+  if constexpr (kSplit && !kHalves) issue_state_group<COMMIT, kEarly, NWC>(S0, p.state_v_stride, wave, lane, 2, s0r);
   __syncthreads();
 #pragma unroll
   for (int d = 1; d < MT; ++d) {
@@ -2070,7 +2300,7 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
     phase_offdiag<NP, NW>(tid, d, sm, mtn);
     __syncthreads();
   }
-  if constexpr (kSplit) issue_state_group<COMMIT, kEarly, NWC>(S0, p.state_v_stride, wave, lane, 3, s0r);
+  if constexpr (kSplit && !kHalves) issue_state_group<COMMIT, kEarly, NWC>(S0, p.state_v_stride, wave, lane, 3, s0r);
   phase_pq<NP, NW>(tid, sm, sm, mtn);
   phase_split_x<NP, NW>(tid, sm, mtn);
   if constexpr (kEarly) {
@@ -2101,7 +2331,9 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
   }
 
   f32x4 cq[MT][TT], ck[MT][TT];
-  if constexpr (VerifySmem<NP>::kLateV) {
+  if constexpr (kHalves) {
+    tail_halves(P, it, lane, wave, sm, sm, xch, s0h, mtn, col0);
+  } else if constexpr (VerifySmem<NP>::kLateV) {
     // Cq first; once every wave is done with the q rows, the v rows are
     // copied into their region while Ck computes
     bf16x8 sh[4][TT], sl[4][TT];  // the state split once, for both passes
@@ -2118,10 +2350,12 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
     __syncthreads();  // X and Pq complete
   }
   if constexpr (kEarly) phase_saves<NP, COMMIT, NW>(P, it, tid, sm, sm);  // the k rows are intact until phase 3
-  bf16x8 wh[NP / 32][TT], wl[NP / 32][TT];
-  phase_w<NP, NWC>(lane, wave, sm, sm, ck, wh, wl, col0);
-  __syncthreads();  // every wave has read its v rows: the q/k/v region takes the outputs
-  phase_out<NP, NWC>(P, it, lane, wave, sm, sm, cq, wh, wl, mtn, col0);
+  if constexpr (!kHalves) {
+    bf16x8 wh[NP / 32][TT], wl[NP / 32][TT];
+    phase_w<NP, NWC>(lane, wave, sm, sm, ck, wh, wl, col0);
+    __syncthreads();  // every wave has read its v rows: the q/k/v region takes the outputs
+    phase_out<NP, NWC>(P, it, lane, wave, sm, sm, cq, wh, wl, mtn, col0);
+  }
   if (P.vn_stage || P.o_stage) {
     __syncthreads();
     // fused form: an opaque thread id, so that the store offsets are
@@ -2136,10 +2370,11 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
 
 // Both widths run at 4 waves per SIMD (at most 128 registers): the 32-wide
 // kernel as 4 workgroups of 4 waves per CU, the 64-wide one as 2 of 8 waves
-// (its LDS holds two per CU).
+// (its LDS holds two per CU).  The 64-wide column split holds one workgroup
+// per CU (its LDS), 2 waves per SIMD.
 template <int NP, bool S0VEC, int CS = 1>
-__global__ void __launch_bounds__(64 * WavesFor<NP>()) __attribute__((amdgpu_waves_per_eu(4)))
-tree_verify_kernel(const VerifyParams P) {
+__global__ void __launch_bounds__(64 * WavesFor<NP>())
+    __attribute__((amdgpu_waves_per_eu((NP > 32 && CS > 1) ? 2 : 4))) tree_verify_kernel(const VerifyParams P) {
   verify_body<NP, S0VEC, false, false, false, false, CS>(P);
 }
 
@@ -2249,7 +2484,10 @@ int launch_size_order(const int32_t* cu_seqlens, int batch, int n_nodes, int32_t
 // item's value columns over two workgroups: each forms phase 1 in full and
 // phases 2-3, the state read and the stores on half the columns, which
 // shortens a workgroup's life where the launch is latency-bound.
-constexpr int kSplitItems = 256;
+// Launches over 32 nodes with at most kSplitItems64 items do the same with
+// the 64-wide kernel (tail_halves; 110 KiB of LDS, one workgroup per CU, so
+// at most 256 workgroups for the 256 CUs).
+constexpr int kSplitItems = 256, kSplitItems64 = 128;
 
 int launch_tree_verify(const dft_verify_args* a, hipStream_t stream) {
   const VerifyParams P = make_params(a);
@@ -2257,8 +2495,15 @@ int launch_tree_verify(const dft_verify_args* a, hipStream_t stream) {
   VerifyParams narrow, wide;
   bool split;
   split_by_size(a, P, narrow, wide, split);
-  if (a->n_nodes <= 32 && (int64_t)a->batch * a->hv <= kSplitItems) {
-    const dim3 grid2((unsigned)(2 * a->batch * a->hv));
+  const int64_t items = (int64_t)a->batch * a->hv;
+  if (a->n_nodes > 32 && items <= kSplitItems64 && P.s0_vec) {
+    const dim3 grid2((unsigned)(2 * items));
+    hipLaunchKernelGGL((tree_verify_kernel<64, true, 2>), grid2, block64, 0, stream, wide);
+    if (split) hipLaunchKernelGGL((tree_verify_kernel<32, true, 2>), grid2, block, 0, stream, narrow);
+    return hipGetLastError() == hipSuccess ? DFT_OK : DFT_ERR_LAUNCH;
+  }
+  if (a->n_nodes <= 32 && items <= kSplitItems) {
+    const dim3 grid2((unsigned)(2 * items));
     if (P.s0_vec)
       hipLaunchKernelGGL((tree_verify_kernel<32, true, 2>), grid2, block, 0, stream, narrow);
     else

@@ -375,6 +375,34 @@ def test_verify_64_wide_output_forms(cuda, o_dtype):
     check_against_oracle(batch, o, k, v, g, o_bf16=(o_dtype == torch.bfloat16))
 
 
+@pytest.mark.parametrize("case", ["b1_fp32_dense", "b4_packed_slots", "b5_one_workgroup"])
+def test_verify_64_wide_column_split(cuda, case):
+    """Launches over 32 nodes with at most 128 (request, v-head) items run
+    each item on two workgroups (value columns split, state k halves split
+    over wave pairs): batch 1 and 4 at full width (32 v-heads) take that
+    form, batch 5 (160 items) the one-workgroup kernel.  fp32 output is held
+    to 5e-5, as the one-workgroup kernel is."""
+    from dforktree_amd import synth
+    announce(f"verify 64-wide column split {case}")
+    if case == "b1_fp32_dense":
+        batch = synth.make_batch(21, 0, [64], hk=16, hv=32, kinds="random")
+        o, k, v, g = run_gpu(batch, cuda, o_dtype=torch.float32)
+        ref = oracle_verify(batch)[0]
+        assert rel_l2(np32(o), ref["o"]) <= 5e-5
+        assert rel_l2(np32(v), ref["vn"]) <= 5e-5
+        check_against_oracle(batch, o, k, v, g, o_bf16=False)
+    elif case == "b4_packed_slots":
+        batch = synth.make_batch(22, 0, [64, 40, 9, 33], hk=16, hv=32, kinds=["chain", "random", "bushy", "random"])
+        pool = torch.randn(6, 32, 128, 128) * 0.02
+        slots = torch.tensor([5, 0, -1, 2], dtype=torch.int32)
+        batch.state = pool[slots.clamp(min=0).long()]
+        o, k, v, g = run_gpu(batch, cuda, packed=True, state=pool.to(cuda), state_indices=slots.to(cuda))
+        check_against_oracle(batch, o, k, v, g)
+    else:
+        batch = synth.make_batch(23, 0, [48] * 5, hk=16, hv=32, kinds=["random", "chain", "bushy", "random", "chain"])
+        check_against_oracle(batch, *run_gpu(batch, cuda, use_bits=True))
+
+
 def test_verify_fp16_gates_and_output(cuda):
     """fp16 gate inputs a, b and an fp16 output o (DFT_F16 operands): the
     oracle takes the same fp16-rounded a, b; o is compared after fp16
