@@ -58,9 +58,25 @@ tree_commit_kernel(const CommitParams P) {
   __shared__ int s_cnt, s_u;
 
   const int tid = threadIdx.x, lane = tid & 63;
-  int id = blockIdx.x;
-  const int e = id % p.n_ends;
-  id /= p.n_ends;
+  // block id -> (layer, request, head) unit and end.  The ends of one unit
+  // read the same source tile: their blocks sit 8 ids apart, so that they
+  // land on one XCD (blocks are dealt to the 8 XCDs in turn) and the later
+  // reads of the tile hit that XCD's L2.  Units past the last whole group
+  // of 8 take their ends from consecutive ids.
+  int id = blockIdx.x, e;
+  {
+    const int units = p.n_layers * p.batch * p.hv;
+    const int full = (units / 8) * 8 * p.n_ends;
+    if (id < full) {
+      const int grp = id / (8 * p.n_ends), rem = id - grp * 8 * p.n_ends;
+      e = rem >> 3;
+      id = grp * 8 + (rem & 7);
+    } else {
+      const int t = id - full;
+      e = t % p.n_ends;
+      id = (units / 8) * 8 + t / p.n_ends;
+    }
+  }
   const int h = id % p.hv;
   id /= p.hv;
   const int b = id % p.batch;
