@@ -1473,8 +1473,22 @@ __device__ __forceinline__ void phase_gram_diag(int tid, const RW& rw, WK& wk, i
 }
 
 
+// acc + X_(bi, ba) T for T in the accumulator layout, as neg_diag_times
+template <int LDA>
+__device__ __forceinline__ f32x4 x_block_times(const float* x, int bi, int ba, f32x4 T, f32x4 acc, int n16, int g4) {
+#pragma unroll
+  for (int s = 0; s < 4; ++s) acc = mfma_f32_16x16x4(x[(16 * bi + n16) * LDA + 16 * ba + 4 * g4 + s], T[s], acc);
+  return acc;
+}
+
 // 1d, one level: off-diagonal blocks X_ij = -D_i sum_{m=j}^{i-1} A_im X_mj at
-// distance d = i - j (each level needs the previous ones)
+// distance d = i - j (each level needs the previous ones).  With four block
+// rows the last level is folded into the second: the lower-left 2 x 2
+// blocks are X_LL = -X_BB A_LL X_TT (X_TT, X_BB the inverses of the
+// diagonal 32 x 32 halves, complete after level 1), so
+// X_30 = -(X_32 (A_20 X_00 + A_21 X_10) + X_33 (A_30 X_00 + A_31 X_10))
+// needs no level-2 block; a third wave forms it beside X_20 and X_31.
+// The caller stops after level 2 when MT is 4.
 template <int NP, int NW, class WK>
 __device__ __forceinline__ void phase_offdiag(int tid, int d, WK& wk, int mtn) {
   constexpr int MT = NP / 16;
@@ -1487,6 +1501,20 @@ __device__ __forceinline__ void phase_offdiag(int tid, int d, WK& wk, int mtn) {
     for (int bm = 0; bm < MT; ++bm)
       if (bm >= bj && bm < bi) T = block_mma<LDA, true>(T, wk.am(), bi, bm, wk.x(), bj, n16, g4);
     store_block<LDA>(wk.x(), bi, bj, neg_diag_times<LDA>(wk.x(), bi, T, n16, g4), n16, g4);
+  }
+  if constexpr (MT == 4) {
+    if (d == 2 && wave == 2 && mtn > 3) {
+      f32x4 T20 = {}, T30 = {};
+#pragma unroll
+      for (int bm = 0; bm < 2; ++bm) {
+        T20 = block_mma<LDA, true>(T20, wk.am(), 2, bm, wk.x(), 0, n16, g4);
+        T30 = block_mma<LDA, true>(T30, wk.am(), 3, bm, wk.x(), 0, n16, g4);
+      }
+      f32x4 acc = {};
+      acc = x_block_times<LDA>(wk.x(), 3, 2, T20, acc, n16, g4);
+      acc = x_block_times<LDA>(wk.x(), 3, 3, T30, acc, n16, g4);
+      store_block<LDA>(wk.x(), 3, 0, -acc, n16, g4);
+    }
   }
 }
 
@@ -2295,7 +2323,7 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
   if constexpr (kSplit && !kHalves) issue_state_group<COMMIT, kEarly, NWC>(S0, p.state_v_stride, wave, lane, 2, s0r);
   __syncthreads();
 #pragma unroll
-  for (int d = 1; d < MT; ++d) {
+  for (int d = 1; d < (MT == 4 ? 3 : MT); ++d) {  // (four block rows: level 3 is folded into level 2)
     if (d >= mtn) break;
     phase_offdiag<NP, NW>(tid, d, sm, mtn);
     __syncthreads();
