@@ -1368,15 +1368,17 @@ __device__ __forceinline__ void phase_norms(const dft_verify_args& p, int tid, c
 // k-head) and G.  Needs the norms and G; reads the k rows.
 // CS: the workgroups of a column split share the saves, each writing key
 // columns col0 .. col0 + 128 / CS - 1 (the first one writes G).
-template <int NP, bool LATE, int NW, class RW, class WK, int CS = 1>
+// NTS: the threads taking part (tid 0 .. NTS - 1; by default the workgroup).
+template <int NP, bool LATE, int NW, class RW, class WK, int CS = 1, int NTS = Waves<NW>::NT>
 __device__ __forceinline__ void phase_saves(const VerifyParams& P, const Item& it, int tid, const RW& rw,
                                             const WK& wk, int col0 = 0) {
   constexpr int KQ = 32 / CS;  // 4-column pieces of a key row per workgroup
+  static_assert(NTS >= NP, "the G saves take a thread per node");
   const OutArgs p = out_args<LATE>(P);
   const bool per_khead = (p.flags & DFT_VERIFY_AUX_K_PER_KHEAD) != 0;
   if (p.aux_k && (!per_khead || it.rr == 0)) {
     float* dk = p.aux_k + (int64_t)(per_khead ? it.hk : it.h) * p.aux_k_h_stride + it.row0 * p.aux_k_row_stride;
-    for (int c = tid; c < it.n * KQ; c += Waves<NW>::NT) {
+    for (int c = tid; c < it.n * KQ; c += NTS) {
       const int i = c / KQ, d = col0 + (c % KQ) * 4;
       const uint2 u = *reinterpret_cast<const uint2*>(&rw.k[qkv_at(i, d)]);
       const float r = wk.rk[i];
@@ -2305,10 +2307,17 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
     issue_state_group<COMMIT, kEarly, NWC>(S0, p.state_v_stride, wave, lane, 1, s0r);
   // (the 32-wide fused form saves after Cq/Ck: at this point its tile is
   // still streaming in, and the saves' stores would wait on the full queue)
-  if constexpr (!kEarly) phase_saves<NP, COMMIT, NW, VerifySmem<NP>, VerifySmem<NP>, CS>(P, it, tid, sm, sm, col0);
+  // The saves go to the waves past the diagonal blocks, which form only
+  // off-diagonal A tiles while the others solve (the 64-wide kernel: waves
+  // 4-7; the 32-wide: waves 2-3).
+  constexpr int kSaveWave0 = MT;
   const int mtn = (it.n + 15) >> 4;  // uniform over the workgroup
   // (the plain verify with a vector state has registers for 3 rows ahead)
   phase_gram_diag<NP, NW, (!COMMIT && S0VEC) ? 3 : 1>(tid, sm, sm, mtn);
+  if constexpr (!kEarly)
+    if (wave >= kSaveWave0)
+      phase_saves<NP, COMMIT, NW, VerifySmem<NP>, VerifySmem<NP>, CS, 64 * (NW - kSaveWave0)>(
+          P, it, tid - 64 * kSaveWave0, sm, sm, col0);
   if constexpr (kEarly && RVN) {
     // The recompute forms hold few registers for the path (raw rows, 10 per
     // lane): their loads go out here, once the diagonal solves (a 32-float
