@@ -383,6 +383,52 @@ __device__ __forceinline__ void materialize16(const float (&x)[16]) {
   asm volatile("" ::"v"(x[8]), "v"(x[9]), "v"(x[10]), "v"(x[11]), "v"(x[12]), "v"(x[13]), "v"(x[14]), "v"(x[15]));
 }
 
+// lane k of each group of 4 lanes, to all 4 (one quad-permute move)
+template <int K>
+__device__ __forceinline__ float quad_bcast(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), K * 0x55, 0xf, 0xf, false));
+}
+
+// The same forward substitution on a whole wave: lane 4j + q holds rows
+// 4q .. 4q + 3 of column j.  Step m broadcasts x_m (held by lane
+// 4j + m / 4) to its column's 4 lanes with one quad-permute move, and each
+// lane updates its 4 rows with A's column m there (rows 4q .. 4q + 3 of at's
+// row m: one aligned 16-byte read, issued kAhead steps before its use).
+// A's entries at and above the diagonal are zero (the tile is masked to
+// strict ancestors, which precede a node), so rows i <= m are left as they
+// are and each element sees the same fused multiply-adds in the same order
+// as in solve_block16: the result is bit-identical.  A step is one move and
+// four multiply-adds on the chain instead of up to 15, and one 16-byte read.
+// Writes X_bb to x (pitch LDA) at (base, base).
+template <int LDA, int kAhead>
+__device__ __forceinline__ void solve_block16_wave(const float* at, float* x, int base, int lane) {
+  static_assert(LDA % 4 == 0, "16-byte aligned rows");
+  const int j = lane >> 2, q = lane & 3;
+  f32x4 xv;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) xv[r] = (4 * q + r == j) ? 1.f : 0.f;
+  const float* col = at + base * LDA + base + 4 * q;  // row m of at: col + m LDA
+  f32x4 rows[kAhead];
+#pragma unroll
+  for (int m = 0; m < kAhead; ++m) rows[m] = *reinterpret_cast<const f32x4*>(col + m * LDA);
+#pragma unroll
+  for (int m = 0; m < 15; ++m) {
+    const f32x4 a = rows[m % kAhead];
+    if (m + kAhead < 15) rows[m % kAhead] = *reinterpret_cast<const f32x4*>(col + (m + kAhead) * LDA);
+    float xm;
+    switch (m >> 2) {
+      case 0: xm = quad_bcast<0>(xv[m & 3]); break;
+      case 1: xm = quad_bcast<1>(xv[m & 3]); break;
+      case 2: xm = quad_bcast<2>(xv[m & 3]); break;
+      default: xm = quad_bcast<3>(xv[m & 3]); break;
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) xv[r] -= a[r] * xm;
+  }
+#pragma unroll
+  for (int r = 0; r < 4; ++r) x[(base + 4 * q + r) * LDA + base + j] = xv[r];
+}
+
 // acc += A_blk(bi, bm) * B_blk(bm, bj) over one 16x16x16 block product with
 // fp32 MFMA; A from a row-major or (transposed) column-major LDS matrix, B
 // row-major.  Lane (n, g), k-step s covers k = 4s + g.
@@ -1439,7 +1485,9 @@ __device__ __forceinline__ void a_tile(const RW& rw, WK& wk, int ti, int tj, int
 
 // mtn: 16-row tiles that hold nodes (the rest are padding and are skipped);
 // KA: rows in flight in the diagonal solves
-template <int NP, int NW, int KA, class RW, class WK>
+// WS: the diagonal blocks solved by whole waves (solve_block16_wave), else
+// on 16 lanes (solve_block16).
+template <int NP, int NW, int KA, bool WS, class RW, class WK>
 __device__ __forceinline__ void phase_gram_diag(int tid, const RW& rw, WK& wk, int mtn) {
   constexpr int MT = NP / 16;
   constexpr int LDA = WK::LDA;
@@ -1451,7 +1499,9 @@ __device__ __forceinline__ void phase_gram_diag(int tid, const RW& rw, WK& wk, i
   }
   if (wave < mtn) {
     a_tile<NP>(rw, wk, wave, wave, n16, g4);
-    if (lane < 16) {
+    if constexpr (WS) {
+      solve_block16_wave<LDA, KA>(wk.am(), wk.x(), 16 * wave, lane);
+    } else if (lane < 16) {
       const int bb = wave, j = lane;
       float xc[16];
 #pragma unroll
@@ -2312,8 +2362,13 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
   // 4-7; the 32-wide: waves 2-3).
   constexpr int kSaveWave0 = MT;
   const int mtn = (it.n + 15) >> 4;  // uniform over the workgroup
-  // (the plain verify with a vector state has registers for 3 rows ahead)
-  phase_gram_diag<NP, NW, (!COMMIT && S0VEC) ? 3 : 1>(tid, sm, sm, mtn);
+  // (the plain verify with a vector state has registers for 3 rows ahead.
+  // The 32-wide fused forms, whose phase 1 runs under their state stream,
+  // keep the 16-lane solve: with the whole-wave one the headline form
+  // measured 62.73 -> 63.13 us at batch 64, and the form holding raw path
+  // rows in registers spilled.)
+  constexpr bool kWaveSolve = !kEarly;
+  phase_gram_diag<NP, NW, (!COMMIT && S0VEC) ? 3 : 1, kWaveSolve>(tid, sm, sm, mtn);
   if constexpr (!kEarly)
     if (wave >= kSaveWave0)
       phase_saves<NP, COMMIT, NW, VerifySmem<NP>, VerifySmem<NP>, CS, 64 * (NW - kSaveWave0)>(
