@@ -2174,6 +2174,26 @@ __device__ __forceinline__ void tail_halves(const VerifyParams& P, const Item& i
   }
 }
 
+// The kernel arguments the plain verify reads before its first copies,
+// forced into scalar registers at entry: read where they are used, behind
+// the branches on item_rows' index arrays, they came in some eight
+// dependent rounds of scalar loads, which a latency-bound launch (batch 1)
+// waits out one by one (batch-1 verify 8.35 -> 8.17 us at 32 nodes, 12.05
+// -> 11.72 at 64).  Only the column-split kernels, which serve the small
+// launches, do so: after the opaque statement the index arrays are read
+// with vector loads, which in a full launch queue behind the state stream
+// (the ragged layer measured 112.1 -> 113.5 us with it).
+__device__ __forceinline__ void args_early(const VerifyParams& P) {
+  const dft_verify_args& p = P.a;
+  asm volatile("" ::"s"(p.batch), "s"(p.n_nodes), "s"(p.hk), "s"(p.hv), "s"(p.y), "s"(p.y_row_stride),
+               "s"(p.cu_seqlens), "s"(p.a), "s"(p.a_row_stride), "s"(p.a_dtype), "s"(p.b), "s"(p.b_row_stride),
+               "s"(p.b_dtype), "s"(p.A_log), "s"(p.A_log_dtype));
+  asm volatile("" ::"s"(p.dt_bias), "s"(p.dt_bias_dtype), "s"(p.neg_exp_A), "s"(p.anc_f32), "s"(p.anc_bits),
+               "s"(p.state), "s"(p.state_slot_stride), "s"(p.state_h_stride), "s"(p.state_v_stride),
+               "s"(p.state_indices), "s"(p.state_indices_dtype), "s"(p.status), "s"(p.size_order), "s"(P.n_lo),
+               "s"(P.n_hi), "s"(P.cls));
+}
+
 template <int NP, bool S0VEC, bool COMMIT, bool RAWK, bool RVN, bool PDMA = false, int CS = 1>
 __device__ __forceinline__ void verify_body(const VerifyParams& P) {
   constexpr int MT = NP / 16;
@@ -2208,6 +2228,7 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n16 = lane & 15, g4 = lane >> 4;
 
+  if constexpr (!COMMIT && CS > 1) args_early(P);
   Item it;
   int col0 = 0;  // the workgroup's first value column
   if constexpr (CS > 1) {
