@@ -80,6 +80,17 @@ __global__ void __launch_bounds__(256) tree_conv_kernel(const dft_conv_args p) {
 // Block size, in interleaved runs: one wave over 512 channels 40.0 us,
 // 128 threads over 1024 channels 40.8 us, 256 threads over 2048 channels
 // 41.3 us; 16 channels per thread (256 threads over 4096) 44.2 us.
+// Request b's index (a slot) from an int32 or int64 array as two 32-bit
+// loads with no branch between them; idx NULL reads nothing (returns 0).
+__device__ __forceinline__ int64_t req_index(const void* idx, int dt, int b) {
+  if (!idx) return 0;
+  const int32_t* w = static_cast<const int32_t*>(idx);
+  const bool wide = dt == DFT_I64;
+  const int32_t lo = w[wide ? 2 * b : b];
+  const int32_t hi = w[wide ? 2 * b + 1 : b];
+  return wide ? (int64_t)(((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo) : (int64_t)lo;
+}
+
 template <bool CIDX64>
 __global__ void __launch_bounds__(64) tree_conv4_bf16_kernel(const dft_conv_args p, int cblocks) {
   __shared__ u32x4 stage[64 * 3];
@@ -105,18 +116,25 @@ __global__ void __launch_bounds__(64) tree_conv4_bf16_kernel(const dft_conv_args
 #pragma unroll
     for (int j = 0; j < 4; ++j) col[j] = ci[j];
   }
+  // The request's conv-state slot and window slot come in the same batch:
+  // read where they are used (behind a dtype branch, and the window slot
+  // after the arithmetic), each was one more dependent round trip, which a
+  // batch-1 launch waits out in full.  Branch-free: the index's low word, and
+  // its high word for 64-bit indices (for 32-bit ones the same word again).
+  const int64_t slot_raw = req_index(p.cs_indices, p.cs_indices_dtype, b);
+  const int64_t dst_raw = req_index(p.iw_indices, p.iw_indices_dtype, b);
   // the weights (8 channels x 4 taps) do not depend on them
   const int cw = active ? c0 : 0;
   const u32x4* wp = reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(p.weight) + (int64_t)cw * 4);
   uint16_t w[32];  // w[4 e + j]: channel c0 + e, tap j
 #pragma unroll
   for (int q = 0; q < 4; ++q) *reinterpret_cast<u32x4*>(&w[8 * q]) = wp[q];
-  int64_t slot = b, dst = b;
+  int64_t slot = p.cs_indices ? slot_raw : b;
+  const int64_t dst = p.iw_indices ? dst_raw : b;
 
   if (active) {
     const uint16_t* xb = static_cast<const uint16_t*>(p.x) + (int64_t)b * p.x_req_stride + c0;
     // the state slot (needed by conv-state taps only); a negative one reads slot 0
-    if (p.cs_indices) slot = ld_i(p.cs_indices, b, p.cs_indices_dtype);
     if (slot < 0) slot = 0;
     // Token rows: every load is issued (a tap outside the tokens reads row 0
     // and is discarded), so none waits on a branch.  A tap on a bf16 conv-state
@@ -183,7 +201,6 @@ __global__ void __launch_bounds__(64) tree_conv4_bf16_kernel(const dft_conv_args
     }
   }
   if (p.iw) {
-    if (p.iw_indices) dst = ld_i(p.iw_indices, b, p.iw_indices_dtype);
     __syncthreads();
     if (dst >= 0) {  // uniform over the block (one request); a negative slot writes no window
       u32x4* iw = reinterpret_cast<u32x4*>(static_cast<uint16_t*>(p.iw) + dst * p.iw_slot_stride +
