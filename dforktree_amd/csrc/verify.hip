@@ -1363,9 +1363,23 @@ __device__ __forceinline__ void issue_state(const float* S0, int64_t v_stride, i
   for (int s = 0; s < 4; ++s) issue_state_group<NT, LINES, NW>(S0, v_stride, wave, lane, s, s0r);
 }
 
+// x plus lane l ^ 1, l ^ 2 (quad permutes) or l ^ 7 (mirror within the 8
+// lanes of a half row): one move each instead of a cross-lane LDS permute
+template <int CTRL>
+__device__ __forceinline__ float dpp_add(float x) {
+  return x + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xf, 0xf, false));
+}
+constexpr int kDppXor1 = 0xB1, kDppXor2 = 0x4E, kDppHalfMirror = 0x141;
+
 // 1a: row norms (4 threads per q/k row) and the path-cumulative decay
-// (NT / NP threads per node), spread over all waves
-template <int NP, int NW, class RW, class WK>
+// (NT / NP = 8 threads per node), spread over all waves.  DPP: the sums over
+// a row's 4 threads and a node's 8 are DPP adds, and a thread's 16 pair
+// products go to 4 accumulators (chains of 4 instead of one of 16); else
+// cross-lane permutes and one chain.  The DPP form made batch-1 verify
+// 8.12 -> 7.91 us (32 nodes), 11.76 -> 11.55 (64) and the ragged layer
+// 112.5 -> 111.7 us, but the one-workgroup 32-wide kernels at batch 64
+// 0.3-0.7% slower (the headline 62.16 -> 62.36 us): they keep the other.
+template <int NP, int NW, bool DPP, class RW, class WK>
 __device__ __forceinline__ void phase_norms(const dft_verify_args& p, int tid, const RW& rw, WK& wk) {
   constexpr int NT = Waves<NW>::NT;
   static_assert((2 * NP) % (NT / 4) == 0, "whole passes of q and k rows");
@@ -1373,7 +1387,7 @@ __device__ __forceinline__ void phase_norms(const dft_verify_args& p, int tid, c
   for (int r0 = 0; r0 < 2 * NP; r0 += NT / 4) {
     const int r = r0 + (tid >> 2), qd = tid & 3, i = r % NP;
     const uint16_t* rows = r < NP ? rw.q : rw.k;
-    float ss = 0.f;  // bf16 pair dot products, accumulated in fp32
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};  // bf16 pair dot products, accumulated in fp32
 #pragma unroll
     for (int c = 32 * qd; c < 32 * qd + 32; c += 8) {
       const uint4 u = *reinterpret_cast<const uint4*>(rows + qkv_at(i, c));
@@ -1381,11 +1395,22 @@ __device__ __forceinline__ void phase_norms(const dft_verify_args& p, int tid, c
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const bf16x2 v = __builtin_bit_cast(bf16x2, w[e]);
-        ss = __builtin_amdgcn_fdot2_f32_bf16(v, v, ss, false);
+        if constexpr (DPP)
+          acc[e] = __builtin_amdgcn_fdot2_f32_bf16(v, v, acc[e], false);
+        else
+          acc[0] = __builtin_amdgcn_fdot2_f32_bf16(v, v, acc[0], false);
       }
     }
-    ss += __shfl_xor(ss, 1);
-    ss += __shfl_xor(ss, 2);
+    float ss;
+    if constexpr (DPP) {
+      ss = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+      ss = dpp_add<kDppXor1>(ss);
+      ss = dpp_add<kDppXor2>(ss);
+    } else {
+      ss = acc[0];
+      ss += __shfl_xor(ss, 1);
+      ss += __shfl_xor(ss, 2);
+    }
     if (qd == 0) {
       const float rn = rsqrtf(ss + 1e-6f);
       if (r < NP) wk.rq[i] = rn * p.scale;
@@ -1395,6 +1420,7 @@ __device__ __forceinline__ void phase_norms(const dft_verify_args& p, int tid, c
   constexpr int TPN = NT / NP;  // threads per node, each summing NP / TPN consecutive nodes
   constexpr int JPT = NP / TPN;
   static_assert(JPT % 4 == 0, "whole 16-byte reads of g");
+  static_assert(TPN == 8, "the node sums are over 8 lanes");
   const int i = tid / TPN, sub = tid % TPN;
   const uint64_t bits = wk.anc[i];
   float G = 0.f;
@@ -1405,8 +1431,14 @@ __device__ __forceinline__ void phase_norms(const dft_verify_args& p, int tid, c
 #pragma unroll
     for (int e = 0; e < 4; ++e) G += ((bits >> (j0 + e)) & 1ull) ? g[e] : 0.f;
   }
+  if constexpr (DPP) {
+    G = dpp_add<kDppXor1>(G);
+    G = dpp_add<kDppXor2>(G);
+    G = dpp_add<kDppHalfMirror>(G);  // (each quad's sum plus the other quad's)
+  } else {
 #pragma unroll
-  for (int o = 1; o < TPN; o <<= 1) G += __shfl_xor(G, o);
+    for (int o = 1; o < TPN; o <<= 1) G += __shfl_xor(G, o);
+  }
   if (sub == 0) wk.G[i] = G;
 }
 
@@ -2358,7 +2390,7 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
   // tile has landed the path is committed into it (keys staged in am + x,
   // still unused) and the tile goes back to its slot, so that the write-back
   // streams under the rest of phase 1.
-  phase_norms<NP, NW>(p, tid, sm, sm);
+  phase_norms<NP, NW, (NP > 32 || CS > 1)>(p, tid, sm, sm);
   __syncthreads();
   if constexpr (COMMIT && !kEarly) {
     commit_tile<NW, false, RAWK, RVN>(pd, sm.pkey(), rvx, kr, pv, wave, lane, s0r,
