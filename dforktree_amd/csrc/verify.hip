@@ -1373,12 +1373,13 @@ constexpr int kDppXor1 = 0xB1, kDppXor2 = 0x4E, kDppHalfMirror = 0x141;
 
 // 1a: row norms (4 threads per q/k row) and the path-cumulative decay
 // (NT / NP = 8 threads per node), spread over all waves.  DPP: the sums over
-// a row's 4 threads and a node's 8 are DPP adds, and a thread's 16 pair
-// products go to 4 accumulators (chains of 4 instead of one of 16); else
-// cross-lane permutes and one chain.  The DPP form made batch-1 verify
-// 8.12 -> 7.91 us (32 nodes), 11.76 -> 11.55 (64) and the ragged layer
-// 112.5 -> 111.7 us, but the one-workgroup 32-wide kernels at batch 64
-// 0.3-0.7% slower (the headline 62.16 -> 62.36 us): they keep the other.
+// a row's 4 threads and a node's 8 are DPP adds, else cross-lane permutes;
+// the two give the same sums bit for bit (each step adds a lane's value and
+// its partner's, and the 8-lane mirror meets the same quad sums as the
+// xor-4 permute), so every kernel's norms and decays agree.  Splitting a
+// thread's 16 pair products over 4 accumulators as well was 0.2 us faster
+// at batch 1 but rounded the norms differently from the fused kernels,
+// whose commit -> verify then no longer matched commit followed by verify.
 template <int NP, int NW, bool DPP, class RW, class WK>
 __device__ __forceinline__ void phase_norms(const dft_verify_args& p, int tid, const RW& rw, WK& wk) {
   constexpr int NT = Waves<NW>::NT;
@@ -1387,7 +1388,7 @@ __device__ __forceinline__ void phase_norms(const dft_verify_args& p, int tid, c
   for (int r0 = 0; r0 < 2 * NP; r0 += NT / 4) {
     const int r = r0 + (tid >> 2), qd = tid & 3, i = r % NP;
     const uint16_t* rows = r < NP ? rw.q : rw.k;
-    float acc[4] = {0.f, 0.f, 0.f, 0.f};  // bf16 pair dot products, accumulated in fp32
+    float acc[1] = {0.f};  // bf16 pair dot products, accumulated in fp32
 #pragma unroll
     for (int c = 32 * qd; c < 32 * qd + 32; c += 8) {
       const uint4 u = *reinterpret_cast<const uint4*>(rows + qkv_at(i, c));
@@ -1395,15 +1396,12 @@ __device__ __forceinline__ void phase_norms(const dft_verify_args& p, int tid, c
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const bf16x2 v = __builtin_bit_cast(bf16x2, w[e]);
-        if constexpr (DPP)
-          acc[e] = __builtin_amdgcn_fdot2_f32_bf16(v, v, acc[e], false);
-        else
-          acc[0] = __builtin_amdgcn_fdot2_f32_bf16(v, v, acc[0], false);
+        acc[0] = __builtin_amdgcn_fdot2_f32_bf16(v, v, acc[0], false);
       }
     }
     float ss;
     if constexpr (DPP) {
-      ss = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+      ss = acc[0];
       ss = dpp_add<kDppXor1>(ss);
       ss = dpp_add<kDppXor2>(ss);
     } else {
