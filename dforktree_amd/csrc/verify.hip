@@ -291,6 +291,13 @@ static_assert(sizeof(VerifySmem<64>) <= 80 * 1024, "two 64-wide workgroups per C
 static_assert(2 * 32 * 36 >= 16 * kD && 2 * 64 * 68 >= 16 * kD, "am + x hold the 16 staged path keys");
 static_assert(2 * 32 * 36 >= 4 * 512 && 2 * 64 * 68 >= 8 * 512, "am + x hold every wave's 2 KiB write-back staging");
 
+// The mixed-width kernel's LDS (tree_verify_mixed_kernel): one 64-wide item's
+// arrays, or two 32-wide items' side by side.  Only that kernel touches it.
+constexpr int kMixedLds = sizeof(VerifySmem<64>) > 2 * sizeof(VerifySmem<32>) ? (int)sizeof(VerifySmem<64>)
+                                                                              : (int)(2 * sizeof(VerifySmem<32>));
+static_assert(sizeof(VerifySmem<32>) % 16 == 0 && kMixedLds <= 80 * 1024, "two mixed workgroups per CU");
+__shared__ uint4 mixed_lds[kMixedLds / 16];
+
 __device__ __forceinline__ f32x4 mfma_bf16_16x16x32(bf16x8 a, bf16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
@@ -1180,9 +1187,10 @@ struct Item {
 
 // block id -> (request, v-head); the R v-heads sharing a k-head get ids 8
 // apart so that they land on the same XCD (shared q/k rows in its L2)
-__device__ __forceinline__ void item_heads(const dft_verify_args& p, int id, Item& it) {
+// over `batch` requests (a bijection of [0, batch * hv))
+__device__ __forceinline__ void item_heads(const dft_verify_args& p, int batch, int id, Item& it) {
   const int R = p.hv / p.hk;
-  const int pairs = p.batch * p.hk;
+  const int pairs = batch * p.hk;
   const int full = (pairs / 8) * 8 * R;
   int pair, rr;
   if (id < full) {
@@ -1198,6 +1206,9 @@ __device__ __forceinline__ void item_heads(const dft_verify_args& p, int id, Ite
   it.hk = pair - it.b * p.hk;
   it.rr = rr;
   it.h = it.hk * R + rr;
+}
+__device__ __forceinline__ void item_heads(const dft_verify_args& p, int id, Item& it) {
+  item_heads(p, p.batch, id, it);
 }
 
 // rows, node count and state tile of a request (loads the index arrays).
@@ -2009,6 +2020,15 @@ struct HalfXch<true> {
   bf16x8 w[4][2][64];    // the first half's W (k-step 0; hi, lo) of column tile c
 };
 
+// An item chosen by the caller (the mixed-width kernel): the request (its
+// class-relative index when records are read) and v-head, the class bounds
+// item_rows applies, and where the item's arrays start in mixed_lds.
+struct Given {
+  Item it;
+  int n_lo, n_hi, cls;
+  int lds_off;
+};
+
 // k-step s (rows k = 32s .. 32s + 31) of column tile c's state, in the MFMA layout
 __device__ __forceinline__ void issue_state_half(const float* S0, int64_t v_stride, int c, int lane, int s,
                                                  f32x4& a, f32x4& b) {
@@ -2224,8 +2244,10 @@ __device__ __forceinline__ void args_early(const VerifyParams& P) {
                "s"(P.n_hi), "s"(P.cls));
 }
 
-template <int NP, bool S0VEC, bool COMMIT, bool RAWK, bool RVN, bool PDMA = false, int CS = 1>
-__device__ __forceinline__ void verify_body(const VerifyParams& P) {
+// tid_in: the thread within the item's waves; blk: the block id the item is
+// taken from.  With GIVEN the item and its LDS come from `given`.
+template <int NP, bool S0VEC, bool COMMIT, bool RAWK, bool RVN, bool PDMA = false, int CS = 1, bool GIVEN = false>
+__device__ __forceinline__ void verify_body(const VerifyParams& P, int tid_in, int blk, const Given& given) {
   constexpr int MT = NP / 16;
   constexpr int NW = WavesFor<NP>();
   // the 64-wide column split: waves split the k half and node tiles (tail_halves)
@@ -2246,30 +2268,47 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
   constexpr int kQkvDma = kPlanes * (NP / (4 * NW));          // row copies per wave
   constexpr int kStateLoads = 8 * TT, kGroupLoads = 2 * TT;   // per lane: whole tile, one k-step group
   const dft_verify_args& p = P.a;
-  __shared__ VerifySmem<NP> sm;
+  static_assert(!GIVEN || (!COMMIT && CS == 1), "a given item is a plain verify");
+  // the verify's arrays: the body's own, or (a given item) its region of mixed_lds
+  VerifySmem<NP>& sm = [&]() -> VerifySmem<NP>& {
+    if constexpr (GIVEN) {
+      return *reinterpret_cast<VerifySmem<NP>*>(reinterpret_cast<char*>(mixed_lds) + given.lds_off);
+    } else {
+      __shared__ VerifySmem<NP> own;
+      return own;
+    }
+  }();
   // the recomputed path values' matrices and key norms: only the forms that
   // recompute them hold them (4.3 KiB)
-  __shared__ alignas(16) float rvx[RVN ? kRvx : 4];
-  // the 64-wide split's exchange between the two halves (40 KiB)
-  __shared__ HalfXch<kHalves> xch;
+  float* const rvx = [&]() -> float* {
+    if constexpr (GIVEN) {
+      return nullptr;
+    } else {
+      __shared__ alignas(16) float own[RVN ? kRvx : 4];
+      return own;
+    }
+  }();
 
   // (the wave index as a scalar: in a vector register it is held, and at the
   // fused form's register cap spilled, through phase 1)
-  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int tid = tid_in, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n16 = lane & 15, g4 = lane >> 4;
 
   if constexpr (!COMMIT && CS > 1) args_early(P);
   Item it;
   int col0 = 0;  // the workgroup's first value column
-  if constexpr (CS > 1) {
+  if constexpr (GIVEN) {
+    it = given.it;
+  } else if constexpr (CS > 1) {
     const int items = p.batch * p.hv;
-    const int sp = blockIdx.x / items;  // (uniform)
+    const int sp = (unsigned)blk / (unsigned)items;  // (uniform)
     col0 = sp * (kD / CS);
-    item_heads(p, blockIdx.x - sp * items, it);
+    item_heads(p, blk - sp * items, it);
   } else {
-    item_heads(p, blockIdx.x, it);
+    item_heads(p, blk, it);
   }
-  if (!item_rows<NP>(p, it, P.n_lo, P.n_hi, P.cls)) return;
+  if (!item_rows<NP>(p, it, GIVEN ? given.n_lo : P.n_lo, GIVEN ? given.n_hi : P.n_hi, GIVEN ? given.cls : P.cls))
+    return;
   // Thread 0 of the request's head-0 workgroup writes its status word (the
   // condition is evaluated where it is written: held from here, it would
   // cost the fused kernel a register through the state stream).
@@ -2475,6 +2514,8 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
 
   f32x4 cq[MT][TT], ck[MT][TT];
   if constexpr (kHalves) {
+    // the 64-wide split's exchange between the two halves (40 KiB)
+    __shared__ HalfXch<true> xch;
     tail_halves(P, it, lane, wave, sm, sm, xch, s0h, mtn, col0);
   } else if constexpr (VerifySmem<NP>::kLateV) {
     // Cq first; once every wave is done with the q rows, the v rows are
@@ -2518,7 +2559,66 @@ __device__ __forceinline__ void verify_body(const VerifyParams& P) {
 template <int NP, bool S0VEC, int CS = 1>
 __global__ void __launch_bounds__(64 * WavesFor<NP>())
     __attribute__((amdgpu_waves_per_eu((NP > 32 && CS > 1) ? 2 : 4))) tree_verify_kernel(const VerifyParams P) {
-  verify_body<NP, S0VEC, false, false, false, false, CS>(P);
+  verify_body<NP, S0VEC, false, false, false, false, CS>(P, threadIdx.x, blockIdx.x, Given{});
+}
+
+// A packed batch with trees on both sides of 32 nodes and size-order records,
+// in one launch of 8-wave workgroups (2 per CU: the LDS of one 64-wide item
+// or of two 32-wide ones).  Blocks [0, c1 Hv) take the (request, v-head)
+// items of the c1 requests over 32 nodes on the 64-wide body; each block
+// after them takes v-heads 2j and 2j + 1 of one of the c0 other requests,
+// one per half of the workgroup (4 waves each) on the 32-wide body.  The two
+// halves verify the same tree (same node count, same exits), so they pass the
+// same barriers.  The 64-wide class's last generation then shares the chip
+// with the small trees instead of leaving most of it idle in front of a
+// second kernel.
+// Records of another launch shape are ignored: block b then takes item b
+// and its request's size picks the body; a small tree's v-heads 2j, 2j + 1
+// go to the block of head 2j, and the other block exits.  Either way every
+// item runs the body of its size class, as in the two-kernel launch.
+template <bool S0VEC>
+__global__ void __launch_bounds__(64 * WavesFor<64>()) __attribute__((amdgpu_waves_per_eu(4)))
+tree_verify_mixed_kernel(const VerifyParams P) {
+  const dft_verify_args& p = P.a;
+  const int4 hd = reinterpret_cast<const int4*>(p.size_order)[0];
+  const bool rec = hd.z == p.n_nodes && hd.w == p.batch;  // uniform
+  const int blk = blockIdx.x, half = threadIdx.x >> 8, R = p.hv / p.hk;
+  Given g;
+  g.n_lo = INT_MIN;
+  g.n_hi = INT_MAX;
+  g.lds_off = 0;
+  bool wide;
+  if (rec) {
+    const int c0 = hd.x, c1 = hd.y, hp = p.hv >> 1;
+    wide = blk < c1 * p.hv;
+    if (wide) {
+      item_heads(p, c1, blk, g.it);  // q < c1: the class-1 records from the back
+      g.cls = 1;
+    } else {
+      const int j = blk - c1 * p.hv;
+      if (j >= c0 * hp) return;
+      g.it.b = j / hp;
+      g.it.h = 2 * (j - g.it.b * hp);
+      g.cls = 0;
+    }
+  } else {
+    item_heads(p, blk, g.it);
+    const int span = p.cu_seqlens[g.it.b + 1] - p.cu_seqlens[g.it.b];
+    wide = span > 32;  // (cut to n_nodes, which is over 32 here)
+    if (!wide && (g.it.h & 1)) return;
+    g.cls = -1;
+    if (wide) g.n_lo = 33;
+  }
+  if (wide) {
+    verify_body<64, S0VEC, false, false, false, false, 1, true>(P, threadIdx.x, blk, g);
+  } else {
+    g.it.h += half;
+    g.it.hk = g.it.h / R;
+    g.it.rr = g.it.h - g.it.hk * R;
+    g.n_hi = 32;
+    g.lds_off = half * (int)sizeof(VerifySmem<32>);
+    verify_body<32, S0VEC, false, false, false, false, 1, true>(P, threadIdx.x & 255, blk, g);
+  }
 }
 
 // P must stay this kernel's first (only) argument: out_args<true> reads it
@@ -2530,7 +2630,7 @@ static_assert(std::is_trivially_copyable<VerifyParams>::value, "VerifyParams is 
 template <int NP, bool RAWK, bool RVN, bool PDMA = false>
 __global__ void __launch_bounds__(64 * WavesFor<NP>()) __attribute__((amdgpu_waves_per_eu(4)))
 tree_commit_verify_kernel(const VerifyParams P) {
-  verify_body<NP, true, true, RAWK, RVN, PDMA>(P);
+  verify_body<NP, true, true, RAWK, RVN, PDMA>(P, threadIdx.x, blockIdx.x, Given{});
 }
 
 static VerifyParams make_params(const dft_verify_args* a) {
@@ -2559,7 +2659,10 @@ static VerifyParams make_params(const dft_verify_args* a) {
 // The 64-wide kernel goes first: the reverse order measured 0.4% slower on
 // 128 requests of 8-64 nodes.  With size-order records each kernel takes its
 // own class's requests from the front of its grid, and its exiting blocks
-// come last.
+// come last.  The plain verify with records, a vector state and an even
+// v-head count runs instead as the one mixed-width kernel
+// (tree_verify_mixed_kernel): 112.98 -> 111.65 and 112.12 -> 110.28 us per
+// ragged layer in interleaved runs on two boxes.
 static void split_by_size(const dft_verify_args* a, const VerifyParams& P, VerifyParams& narrow, VerifyParams& wide,
                           bool& split) {
   narrow = wide = P;
@@ -2651,6 +2754,10 @@ int launch_tree_verify(const dft_verify_args* a, hipStream_t stream) {
       hipLaunchKernelGGL((tree_verify_kernel<32, true, 2>), grid2, block, 0, stream, narrow);
     else
       hipLaunchKernelGGL((tree_verify_kernel<32, false, 2>), grid2, block, 0, stream, narrow);
+    return hipGetLastError() == hipSuccess ? DFT_OK : DFT_ERR_LAUNCH;
+  }
+  if (split && a->size_order && P.s0_vec && a->hv % 2 == 0) {
+    hipLaunchKernelGGL((tree_verify_mixed_kernel<true>), grid, block64, 0, stream, P);
     return hipGetLastError() == hipSuccess ? DFT_OK : DFT_ERR_LAUNCH;
   }
   if (a->n_nodes > 32) {

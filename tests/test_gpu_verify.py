@@ -15,7 +15,8 @@ from oracle import gdn_tree as O
 pytestmark = pytest.mark.gpu
 
 
-def run_gpu(batch, dev, use_bits=False, o_dtype=torch.bfloat16, packed=None, state_indices=None, state=None):
+def run_gpu(batch, dev, use_bits=False, o_dtype=torch.bfloat16, packed=None, state_indices=None, state=None,
+            records=False):
     from dforktree_amd import ops
     g = batch.to(dev)
     rows = g.y.shape[0]
@@ -29,6 +30,8 @@ def run_gpu(batch, dev, use_bits=False, o_dtype=torch.bfloat16, packed=None, sta
               state_indices=state_indices)
     if packed:
         kw.update(cu_seqlens=g.cu_seqlens, n_nodes=batch.n_max, batch=batch.batch)
+        if records:  # size-order records: a batch on both sides of 32 nodes takes the mixed-width kernel
+            kw["size_order"] = ops.size_order(g.cu_seqlens, batch.n_max)
     else:
         kw.update(batch=batch.batch, n_nodes=batch.sizes[0])
     if use_bits or packed:
@@ -96,14 +99,18 @@ def test_verify_batched_uniform_bits(cuda):
     check_against_oracle(batch, *run_gpu(batch, cuda, use_bits=True))
 
 
-def test_verify_packed_ragged(cuda):
-    """Packed varlen rows with cu_seqlens, sizes 1..64, the 64-wide path."""
+@pytest.mark.parametrize("hk,hv,records", [(2, 4, False), (2, 4, True), (2, 2, True), (1, 4, True), (2, 8, True)])
+def test_verify_packed_ragged(cuda, hk, hv, records):
+    """Packed varlen rows with cu_seqlens, sizes 1..64: two kernels without
+    size-order records, the mixed-width kernel with them, whose v-head pairs
+    (2j, 2j + 1) span one k-head (R = 2), two k-heads (R = 1) or half of one
+    (R = 4)."""
     from dforktree_amd import synth
-    announce("verify packed ragged")
+    announce(f"verify packed ragged hk={hk} hv={hv} records={records}")
     sizes, kinds = [8, 64, 17, 1, 33, 64, 40, 9], ["chain", "random", "bushy", "random", "chain", "bushy",
                                                  "random", "chain"]
-    batch = synth.make_batch(3, 0, sizes, hk=2, hv=4, kinds=kinds)
-    check_against_oracle(batch, *run_gpu(batch, cuda, packed=True))
+    batch = synth.make_batch(3, 0, sizes, hk=hk, hv=hv, kinds=kinds)
+    check_against_oracle(batch, *run_gpu(batch, cuda, packed=True, records=records))
 
 
 def test_verify_split_order_empty_requests_and_slots(cuda):
@@ -330,15 +337,18 @@ def test_verify_bench_shape(cuda):
     check_against_oracle(batch, *run_gpu(batch, cuda, packed=False, use_bits=True))
 
 
-def test_verify_ragged_bench_shape(cuda):
+@pytest.mark.parametrize("records", [False, True], ids=["two_kernels", "mixed_kernel"])
+def test_verify_ragged_bench_shape(cuda, records):
     """The measured ragged batch at full size: 128 packed requests with trees
     of 8-64 nodes (chains, bushy and random thirds), 4507 nodes at full
-    width, both kernel sizes in one launch, against the oracle."""
+    width, against the oracle: without size-order records as two kernels
+    (64- and 32-wide), with them as the one mixed-width kernel (its 32-wide
+    items in v-head pairs, two per workgroup)."""
     from dforktree_amd import synth
-    announce("verify ragged bench shape 128 x 8-64")
+    announce(f"verify ragged bench shape 128 x 8-64 records={records}")
     sizes, kinds = synth.ragged_sizes(128, 8, 64, seed=3)
     batch = synth.make_batch(15, 0, sizes, hk=16, hv=32, kinds=kinds)
-    check_against_oracle(batch, *run_gpu(batch, cuda, packed=True, use_bits=True))
+    check_against_oracle(batch, *run_gpu(batch, cuda, packed=True, use_bits=True, records=records))
 
 
 def test_verify_kmajor_state_element_loads(cuda):
