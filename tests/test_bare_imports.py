@@ -1,5 +1,5 @@
-"""The binding INTEGRATION.md prescribes, resolved the way the plugin resolves
-it: fc1_plugin.register puts the reference's own directory first on
+"""The plugin binding (one line added to fc1_plugin.register), resolved the way
+the plugin resolves it: fc1_plugin.register puts the reference's own directory first on
 sys.path (fc1_plugin.py:27), then the one added line puts
 ``dforktree_amd.plugin.PATH`` in front of it.  Every bare module name the
 reference's files import must then resolve -- the five replaced ones here,
@@ -51,7 +51,7 @@ standin, root, installed = sys.argv[1], sys.argv[2], sys.argv[3] == "1"
 sys.path.insert(0, standin)                      # fc1_plugin.py:27
 if installed:
     sys.path.append(root)                        # the package importable, as when installed
-    import dforktree_amd.plugin                  # the line INTEGRATION.md adds
+    import dforktree_amd.plugin                  # the line added to fc1_plugin.register
     sys.path.insert(0, dforktree_amd.plugin.PATH)
     plugin_dir = dforktree_amd.plugin.PATH
 else:                                            # the directory alone on sys.path
