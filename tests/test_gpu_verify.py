@@ -16,7 +16,7 @@ pytestmark = pytest.mark.gpu
 
 
 def run_gpu(batch, dev, use_bits=False, o_dtype=torch.bfloat16, packed=None, state_indices=None, state=None,
-            records=False):
+            records=False, n_nodes=None):
     from dforktree_amd import ops
     g = batch.to(dev)
     rows = g.y.shape[0]
@@ -29,9 +29,10 @@ def run_gpu(batch, dev, use_bits=False, o_dtype=torch.bfloat16, packed=None, sta
     kw = dict(hk=batch.hk, hv=batch.hv, o_dtype=o_dtype, aux_k=aux_k, aux_v=aux_v, aux_g=aux_g,
               state_indices=state_indices)
     if packed:
-        kw.update(cu_seqlens=g.cu_seqlens, n_nodes=batch.n_max, batch=batch.batch)
-        if records:  # size-order records: a batch on both sides of 32 nodes takes the mixed-width kernel
-            kw["size_order"] = ops.size_order(g.cu_seqlens, batch.n_max)
+        n_nodes = batch.n_max if n_nodes is None else n_nodes
+        kw.update(cu_seqlens=g.cu_seqlens, n_nodes=n_nodes, batch=batch.batch)
+        if records:  # size-order records: a launch over 32 nodes takes the mixed-width kernel
+            kw["size_order"] = ops.size_order(g.cu_seqlens, n_nodes)
     else:
         kw.update(batch=batch.batch, n_nodes=batch.sizes[0])
     if use_bits or packed:
@@ -113,13 +114,14 @@ def test_verify_packed_ragged(cuda, hk, hv, records):
     check_against_oracle(batch, *run_gpu(batch, cuda, packed=True, records=records))
 
 
-def test_verify_split_order_empty_requests_and_slots(cuda):
-    """A launch split by tree size takes each kernel's requests in its own
-    order (most 16-row tiles first): empty requests between the others,
+@pytest.mark.parametrize("records", [False, True], ids=["two_kernels", "mixed_kernel"])
+def test_verify_split_order_empty_requests_and_slots(cuda, records):
+    """A launch split by tree size, as two kernels or (with size-order
+    records) as the mixed-width kernel: empty requests between the others,
     permuted state slots with a -1 (read from slot 0), trees on both sides of
     32 nodes.  Every request matches the oracle and reports status 0."""
     from dforktree_amd import ops, synth
-    announce("verify split order: empty requests, slots")
+    announce(f"verify split order: empty requests, slots, records={records}")
     sizes = [40, 12, 64, 33, 9, 17, 64, 1, 48]
     batch = synth.make_batch(23, 0, sizes, hk=2, hv=4, kinds=["random", "chain", "bushy"] * 3)
     empty_at = [1, 5, 9]  # positions of the empty requests in the launch
@@ -141,12 +143,27 @@ def test_verify_split_order_empty_requests_and_slots(cuda):
     aux_v = torch.zeros(4, rows, 128, device=cuda)
     aux_g = torch.zeros(4, rows, device=cuda)
     status = torch.full((len(order),), -5, device=cuda, dtype=torch.int32)
+    cu_d = cu.to(cuda)
+    so = ops.size_order(cu_d, 64) if records else None
     o = ops.tree_verify(g.y, g.a, g.b, g.A_log, g.dt_bias, pool.to(cuda).transpose(-1, -2), hk=2, hv=4,
-                        anc_bits=ts["anc_bits"], cu_seqlens=cu.to(cuda), n_nodes=64, batch=len(order),
-                        state_indices=slots.to(cuda), aux_k=aux_k, aux_v=aux_v, aux_g=aux_g, status=status)
+                        anc_bits=ts["anc_bits"], cu_seqlens=cu_d, n_nodes=64, batch=len(order),
+                        state_indices=slots.to(cuda), aux_k=aux_k, aux_v=aux_v, aux_g=aux_g, status=status,
+                        size_order=so)
     torch.cuda.synchronize()
     assert status.tolist() == [0] * len(order)
     check_against_oracle(batch, o, aux_k, aux_v, aux_g)
+
+
+@pytest.mark.parametrize("sizes", [[5, 32, 17, 1, 30, 9], [33, 64, 40, 48]], ids=["all_small", "all_large"])
+def test_verify_mixed_kernel_one_class(cuda, sizes):
+    """Size-order records of a batch whose trees are all on one side of 32
+    nodes (launched at n_nodes 64): the mixed-width kernel then runs only
+    v-head pairs on the 32-wide body, or only 64-wide items.  Against the
+    oracle."""
+    from dforktree_amd import synth
+    announce(f"verify mixed kernel, one size class: {sizes}")
+    batch = synth.make_batch(31, 0, sizes, hk=2, hv=4, kinds=["random", "chain", "bushy"] * 2)
+    check_against_oracle(batch, *run_gpu(batch, cuda, packed=True, records=True, n_nodes=64))
 
 
 def size_order_records(cu, n_nodes):
